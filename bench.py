@@ -1,0 +1,228 @@
+"""Decode benchmark of one Ling-mini-2.0-shaped BailingMoeV2 decoder layer on one MI355X.
+
+Workload: one decode step of the layer (input RMSNorm, fused QKV projection, QK-norm + partial
+RoPE + paged KV write, paged GQA decode attention, output projection, residual + RMSNorm,
+router, top-k/permute, grouped SwiGLU experts + shared expert, combine + residual) for a batch
+of 32 sequences whose cached lengths are uniform in [128, 4096], block size 32, block pool
+1.25x the blocks needed, shuffled. Random-init bf16 weights (seed 0), K/V ~ N(0, 1).
+A step writes the new token's K/V at each sequence's slot and reads every cached token; the
+same step is repeated (same positions), so every step does identical work.
+
+Prints one JSON line: tokens/s through the layer (batch / step time), the HBM roofline
+fraction of the dominant kernel (grouped gate/up SwiGLU GEMM: bytes from the step's actual
+routing / its average duration, measured with HIP events on its stream) and of the whole layer,
+and the CPU oracle timed on this host's cores on a bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "decode tokens/sec @bs32 Ling-mini-2.0-shape, 1 GPU; % HBM roofline/layer"
+HBM_PEAK_GBS = 8000.0
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-steps", type=int, default=5)
+    return ap.parse_args()
+
+
+def algorithmic_bytes(shape, ctx, n_routed_active: int, B: int) -> dict:
+    """HBM bytes one decode step must move at minimum (bf16 weights and KV)."""
+    H, I = shape.hidden_size, shape.moe_intermediate_size
+    expert = 3 * I * H * 2
+    gate_up_w = (n_routed_active + shape.num_shared_experts) * 2 * I * H * 2
+    rows = B * shape.top_k + B * shape.num_shared_experts
+    gate_up = gate_up_w + B * H * 2 + rows * I * 2          # weights + x + h
+    kv_read = ctx.kv_bytes_read()
+    kv_write = B * shape.num_kv_heads * shape.head_dim * 2 * 2
+    layer = (shape.attention_weight_bytes() + kv_read + kv_write
+             + shape.num_experts * H * 4                      # fp32 router weights
+             + (n_routed_active + shape.num_shared_experts) * expert
+             + 2 * H * 2 + 2 * shape.head_dim * 2            # norm weights
+             + 4 * B * H * 2)                                 # activations in/out
+    return dict(gate_up=gate_up, layer=layer, kv_read=kv_read,
+                experts=(n_routed_active + shape.num_shared_experts) * expert)
+
+
+def cpu_baseline(w_gpu, shape, ctx, x, steps: int) -> dict:
+    """The oracle (HF-shaped CPU module forward, fp32) on the same layer and batch."""
+    import torch
+
+    from oracle.bailing_moe_v2 import decoder_layer_from_weights
+    from oracle.paged_kv import PagedKVCacheRef
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    w = {k: v.cpu() for k, v in w_gpu.items()}
+    layer = decoder_layer_from_weights(w, shape, dtype=torch.float32)
+    del w
+    kp = ctx.k_pool.float().cpu()
+    vp = ctx.v_pool.float().cpu()
+    pt = ctx.page_table.cpu()
+    pos = ctx.positions.cpu().long()
+    xc = x.float().cpu()
+    times = []
+    with torch.no_grad():
+        for i in range(steps + 2):
+            cache = PagedKVCacheRef([kp], [vp], pt)
+            t0 = time.perf_counter()
+            layer(xc, past_key_value=cache, cache_position=pos)
+            dt = time.perf_counter() - t0
+            if i >= 2:
+                times.append(dt)
+            _log(f"cpu baseline step {i}: {dt * 1e3:.1f} ms")
+    med = statistics.median(times)
+    B = x.shape[0]
+    return {"value": B / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{steps} decode steps (median, after 2 warm-up) of the same layer and "
+                      f"batch of {B} in fp32 on the host CPU; {med * 1e3:.1f} ms/step"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures the single-GPU decode layer; --gpus {args.gpus} is not "
+              "supported on this build (one GPU only).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    import tt_symbiote_amd as ts
+    from tt_symbiote_amd import hip_ops
+    from tt_symbiote_amd.workloads import (LING_MINI_2, build_decoder_layer, decode_layer_config,
+                                           layer_weights, paged_context)
+
+    dev = torch.device("cuda:0")
+    shape = LING_MINI_2
+    wl = decode_layer_config("batch32")
+    B = wl["batch"]
+    _log("building weights and paged context on the GPU ...")
+    w = layer_weights(shape, seed=args.seed, device=dev)
+    ctx = paged_context(B, wl["ctx_lo"], wl["ctx_hi"], block_size=wl["block_size"],
+                        num_kv_heads=shape.num_kv_heads, seed=args.seed + 1, slack=wl["slack"],
+                        device=dev)
+    x = torch.randn(B, 1, shape.hidden_size, generator=torch.Generator().manual_seed(2)) \
+        .to(torch.bfloat16).to(dev)
+
+    layer = build_decoder_layer(w, shape)
+    ts.set_device(layer, dev)
+    layer.mlp.keep_last_route = True
+    cfg = ts.PagedAttentionConfig(block_size=wl["block_size"], max_num_blocks=ctx.k_pool.shape[0],
+                                  batch_size=1)
+    cache = ts.HIPPagedAttentionKVCache(1, shape.num_kv_heads, shape.head_dim, cfg)
+    cache.to_device(dev)
+    cache.key_cache(0).copy_(ctx.k_pool)
+    cache.value_cache(0).copy_(ctx.v_pool)
+    cache.set_vllm_page_table(ctx.page_table)
+    pos = ctx.positions.to(dev)
+
+    def step():
+        return layer(x, past_key_values=cache, cache_position=pos)[0]
+
+    _log(f"warmup {args.warmup} steps ...")
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    n_active = int(layer.mlp.last_route.n_segments.item()) - shape.num_shared_experts
+
+    # timed region: K eager steps
+    _log(f"timing {args.steps} steps ...")
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record()
+    for _ in range(args.steps):
+        step()
+    t_end.record()
+    torch.cuda.synchronize()
+    ms_per_step = t_start.elapsed_time(t_end) / args.steps
+
+    # per-kernel pass: same steps with HIP events around the dominant kernels
+    timer = hip_ops.KernelTimer(["moe_gate_up", "moe_down", "paged_gqa_decode"])
+    hip_ops.set_kernel_timer(timer)
+    torch.cuda.synchronize()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    hip_ops.set_kernel_timer(None)
+    gate_up_ms = timer.mean_ms("moe_gate_up")
+    down_ms = timer.mean_ms("moe_down")
+    attn_ms = timer.mean_ms("paged_gqa_decode")
+
+    nbytes = algorithmic_bytes(shape, ctx, n_active, B)
+    achieved = nbytes["gate_up"] / (gate_up_ms * 1e-3) / 1e9
+    layer_gbs = nbytes["layer"] / (ms_per_step * 1e-3) / 1e9
+    _log(f"step {ms_per_step * 1e3:.1f} us | gate_up {gate_up_ms * 1e3:.1f} us "
+         f"({achieved:.0f} GB/s) | down {down_ms * 1e3:.1f} us | attention {attn_ms * 1e3:.1f} us "
+         f"| active experts {n_active} | layer {layer_gbs:.0f} GB/s")
+
+    result = {
+        "metric": METRIC,
+        "value": B / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights (seed 0), K/V cache ~ N(0,1)",
+        "config": {
+            "workload": "BailingMoeV2 decoder layer decode step (Ling-mini-2.0 shape: hidden "
+                        "2048, 16q/4kv heads x128, 256 experts top-8 I=512 + 1 shared), batch 32, "
+                        "cached lengths U[128,4096], block size 32, pool 1.25x shuffled",
+            "global_batch": B,
+            "context_tokens": int(ctx.context_lens.sum()),
+            "active_experts": n_active,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "moe_gate_up_kernel (grouped gate/up GEMM + SwiGLU)",
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "bytes_per_launch": nbytes["gate_up"],
+            "avg_launch_us": gate_up_ms * 1e3,
+        },
+        "layer_roofline": {
+            "bytes_per_step": nbytes["layer"],
+            "achieved": layer_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": layer_gbs / HBM_PEAK_GBS,
+            "kernel_us": {"moe_gate_up": gate_up_ms * 1e3, "moe_down": down_ms * 1e3,
+                          "paged_gqa_decode": attn_ms * 1e3},
+        },
+        "cpu_baseline": None,
+    }
+    if not args.no_cpu_baseline:
+        _log("cpu baseline ...")
+        result["cpu_baseline"] = cpu_baseline(w, shape, ctx, x, args.cpu_steps)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

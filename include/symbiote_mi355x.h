@@ -1,0 +1,190 @@
+/*
+ * symbiote_mi355x.h -- C ABI of the MI355X (gfx950) kernels behind the BailingMoeV2
+ * (Ling-mini-2.0) decode hot path: paged GQA decode attention over a block-table KV cache,
+ * and the MoE block (sigmoid/bias/group-limited router, token permute/unpermute, grouped
+ * SwiGLU expert GEMMs, shared expert).
+ *
+ * Conventions (every entry point):
+ *   - all tensor arguments are raw device pointers; sizes are plain ints;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream);
+ *   - the return value is a sym_status; on error sym_last_error() gives a message for the
+ *     calling thread. No entry point throws, allocates device memory or synchronizes;
+ *   - scratch memory is passed in by the caller (`workspace`, sized by the matching
+ *     *_workspace_bytes query), so a whole decode step can be captured in a HIP graph;
+ *   - bf16 tensors are raw uint16 bit patterns (torch.bfloat16 storage);
+ *   - calls are stateless and may be issued from several host threads on distinct streams.
+ *
+ * Shapes follow the reference's device layouts:
+ *   KV pools   [num_blocks, n_kv_heads, block_size, head_dim]   (ttnn_attention.py:116-137)
+ *   page table [batch, max_blocks_per_seq] int32                (ttnn_attention.py:101-102)
+ *   positions  [batch] int32: slot of the new token = tokens already cached for that sequence
+ *              (the reference's cur_pos, ttnn_attention.py:2232-2306)
+ *   expert weights stacked as gate_up [E(+1), 2*I, H] (gate rows first) and down
+ *              [E(+1), H, I] (ttnn_moe.py:1596-1609); slot E holds the shared expert.
+ */
+#ifndef SYMBIOTE_MI355X_H
+#define SYMBIOTE_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  SYM_OK = 0,
+  SYM_ERR_INVALID = 1,     /* bad argument: null pointer, size out of range */
+  SYM_ERR_UNSUPPORTED = 2, /* shape the kernels do not implement (e.g. head_dim != 128) */
+  SYM_ERR_WORKSPACE = 3,   /* workspace smaller than the *_workspace_bytes query */
+  SYM_ERR_LAUNCH = 4       /* the HIP runtime rejected a launch */
+} sym_status;
+
+/* Message for the last non-zero status returned on the calling thread. */
+const char* sym_last_error(void);
+/* ABI revision; bumped on any signature change. */
+int sym_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------
+ * RMSNorm over the last dim, bf16 in/out, fp32 statistics, with optional fused residual add.
+ * Replaces the decoder layer's input_layernorm / post_attention_layernorm
+ * (modeling_bailing_moe_v2.py:440-465; formula of DeepseekV2RMSNorm,
+ * ttnn_normalization.py:54-68). If `residual` is non-NULL, s = bf16(x + residual) is written
+ * to `residual_out` and normalized; otherwise s = x. out = bf16(weight * bf16(s * rsqrt(mean(s^2)+eps))).
+ * rows >= 1, cols % 8 == 0, cols <= 16384.
+ */
+int sym_rmsnorm_bf16(const void* x, const void* residual, const void* weight, int rows, int cols,
+                     float eps, void* out, void* residual_out, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Decode prologue: per-head QK RMSNorm, partial split-half RoPE, paged KV write.
+ * Replaces TTNNBailingMoEAttention._forward_decode_paged's split / _apply_qk_norm / RoPE /
+ * paged_update_on_device sequence (ttnn_attention.py:2329-2431).
+ *   qkv        [B, (Hq + 2*Hkv) * 128] bf16, output of the fused query_key_value projection
+ *   q_norm_w, k_norm_w [128] bf16 (ignored when use_qk_norm == 0)
+ *   rope_cs    [max_pos, 2, rotary_dim/2] fp32: cos then sin of pos * inv_freq[i]
+ *   q_out      [B, Hq, 128] bf16
+ *   K and V of the new token are written at slot positions[b] of sequence b.
+ * head_dim is 128; rotary_dim even, 0 < rotary_dim <= 128. Slots whose page-table entry is
+ * outside [0, num_blocks) or whose position is >= max_pos are skipped.
+ */
+int sym_attn_decode_prologue(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                             const float* rope_cs, int max_pos, const int32_t* positions, int B,
+                             int Hq, int Hkv, int head_dim, int rotary_dim, float eps,
+                             int use_qk_norm, void* q_out, void* k_pool, void* v_pool,
+                             const int32_t* block_tables, int max_blocks_per_seq, int block_size,
+                             int num_blocks, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Paged KV write of one token per sequence: replaces TTNNPagedAttentionKVCache.
+ * paged_update_on_device -> ttnn.experimental.paged_update_cache (ttnn_attention.py:235-269).
+ *   k_new, v_new [B, Hkv, head_dim] bf16; slot = positions[b].
+ */
+int sym_paged_kv_write(const void* k_new, const void* v_new, void* k_pool, void* v_pool,
+                       const int32_t* block_tables, const int32_t* positions, int B, int Hkv,
+                       int head_dim, int block_size, int max_blocks_per_seq, int num_blocks,
+                       void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Paged prefill fill of one sequence: replaces paged_fill_on_device -> paged_fill_cache
+ * (ttnn_attention.py:202-233). k, v [Hkv, S, head_dim] bf16 written at positions
+ * start_pos .. start_pos+S-1 of sequence `batch_idx`.
+ */
+int sym_paged_kv_fill(const void* k, const void* v, void* k_pool, void* v_pool,
+                      const int32_t* block_tables, int batch_idx, int start_pos, int S, int Hkv,
+                      int head_dim, int block_size, int max_blocks_per_seq, int num_blocks,
+                      void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Paged GQA decode attention (split-K over the context, log-sum-exp merge).
+ * Replaces TTNNPagedAttentionKVCache.paged_sdpa_decode ->
+ * ttnn.transformer.paged_scaled_dot_product_attention_decode (ttnn_attention.py:288-329):
+ *   out[b, h] = softmax(scale * q[b,h] . K[b, 0..positions[b]]^T) V[b, 0..positions[b]]
+ * with kv head = h / (Hq/Hkv); K/V gathered through the page table; fp32 accumulation.
+ *   q   [B, Hq, 128] bf16;  out [B, Hq, 128] bf16
+ *   max_context: upper bound of positions[b]+1 (normally max_blocks_per_seq * block_size).
+ * Hq/Hkv in {1,2,4,8}; head_dim 128.
+ */
+size_t sym_paged_gqa_decode_workspace_bytes(int B, int Hq, int head_dim, int max_context);
+int sym_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
+                         const int32_t* block_tables, const int32_t* positions, int B, int Hq,
+                         int Hkv, int head_dim, int block_size, int max_blocks_per_seq,
+                         int num_blocks, int max_context, float scale, void* workspace,
+                         size_t workspace_bytes, void* out, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Fused MoE router + top-k + permute.
+ * Replaces TTNNMoERouterDecode.forward (ttnn_moe.py:891-1024; torch form
+ * Glm4MoeRouteTokenToExperts, ttnn_moe.py:413-436) and the dispatch/remap of
+ * TTNNExperts.forward (ttnn_moe.py:1225-1245):
+ *   s = sigmoid(logits); c = s + bias; group score = sum of the two largest c in each group of
+ *   E/n_group experts; keep the topk_group best groups; experts of other groups score 0.0;
+ *   topk_idx = top_k experts by that score (ties: lower index first);
+ *   topk_w = s[topk_idx], divided by (sum + 1e-20) when renormalize, times routed_scale.
+ * Permute: assignments (t, k) sorted by (expert, token); expert_offsets is the exclusive
+ * cumsum of expert_counts; sorted_tokens[row] = token of that row; inv_perm[t*top_k + k] =
+ * row of assignment (t, k). When with_shared != 0, rows T*top_k .. T*top_k+T-1 hold every
+ * token in order for the shared expert (stack slot E).
+ * Segment list for the grouped GEMM: seg_expert/seg_offset/seg_count[0 .. *n_segments) list
+ * the experts with at least one row in ascending order, then the shared expert.
+ *   logits [T, E] fp32; bias [E] fp32; E in {64,128,256,512}; E/n_group >= 2 and
+ *   (E/n_group) % (E/64) == 0; top_k <= 32; topk_group <= n_group.
+ * Output sizes: topk_idx/topk_w/inv_perm [T*top_k]; expert_counts [E]; expert_offsets [E+1];
+ * sorted_tokens [T*top_k + T]; seg_* [E+1]; n_segments [1].
+ */
+size_t sym_moe_route_workspace_bytes(int T, int E);
+int sym_moe_route_permute(const float* logits, const float* bias, int T, int E, int n_group,
+                          int topk_group, int top_k, float routed_scale, int renormalize,
+                          int with_shared, int32_t* topk_idx, float* topk_w,
+                          int32_t* expert_counts, int32_t* expert_offsets,
+                          int32_t* sorted_tokens, int32_t* inv_perm, int32_t* seg_expert,
+                          int32_t* seg_offset, int32_t* seg_count, int32_t* n_segments,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Grouped SwiGLU expert GEMMs over the segment list of sym_moe_route_permute.
+ * Replaces the three sparse_matmul calls + silu/mul of TTNNExperts.forward
+ * (ttnn_moe.py:1250-1289) and the shared expert TTNNGlm4MoeMLP (ttnn_moe.py:656-675):
+ *   for each segment s (expert e), row r in [seg_offset, seg_offset+seg_count):
+ *     x_r = x[sorted_tokens[r]]
+ *     h[r] = bf16(silu(x_r . Wg[e]^T) * (x_r . Wu[e]^T))     Wg = gate_up[e, :I], Wu = gate_up[e, I:]
+ *     y[r] = h[r] . Wd[e]^T                                    (fp32)
+ *   x [T, H] bf16; w_gate_up [E+1, 2I, H] bf16; w_down [E+1, H, I] bf16;
+ *   h [rows, I] bf16 and y [rows, H] fp32 with rows = T*top_k (+T with a shared expert).
+ * The segment list is read on the device; no host synchronization. H % 64 == 0, I % 64 == 0.
+ * max_segments: the length of the segment list buffers (E+1).
+ */
+int sym_moe_grouped_swiglu(const void* x, int T, int H, int I, const int32_t* sorted_tokens,
+                           const int32_t* seg_expert, const int32_t* seg_offset,
+                           const int32_t* seg_count, const int32_t* n_segments, int max_segments,
+                           const void* w_gate_up, const void* w_down, void* h, float* y,
+                           void* stream);
+/* The two halves of sym_moe_grouped_swiglu as separate launches: gate/up + SwiGLU -> h, then
+ * down -> y (same arguments and layouts). */
+int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t* sorted_tokens,
+                    const int32_t* seg_expert, const int32_t* seg_offset, const int32_t* seg_count,
+                    const int32_t* n_segments, int max_segments, const void* w_gate_up, void* h,
+                    void* stream);
+int sym_moe_down(const void* h, int T, int H, int I, const int32_t* seg_expert,
+                 const int32_t* seg_offset, const int32_t* seg_count, const int32_t* n_segments,
+                 int max_segments, const void* w_down, float* y, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Unpermute + weighted combine (+ shared expert, + residual).
+ * Replaces all_to_all_combine + mul + sum(dim=0) (ttnn_moe.py:1307-1335), the shared-expert
+ * add (ttnn_moe.py:1487-1490) and the decoder layer's residual add
+ * (modeling_bailing_moe_v2.py:467-468):
+ *   out[t] = bf16( sum_k topk_w[t,k] * y[inv_perm[t,k]]  (k ascending)
+ *                  + (shared_row0 >= 0 ? y[shared_row0 + t] : 0)
+ *                  + (residual ? residual[t] : 0) )
+ *   out [T, H] bf16; residual [T, H] bf16 or NULL. H % 8 == 0.
+ */
+int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm, const float* topk_w, int T,
+                              int top_k, int H, int shared_row0, const void* residual, void* out,
+                              void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SYMBIOTE_MI355X_H */

@@ -1,0 +1,101 @@
+"""The C-ABI library (CPU side): it loads, exports every entry point the header declares, and
+rejects bad arguments with a status code before launching anything."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from tt_symbiote_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "symbiote_mi355x.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(sym_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    assert set(_declared()) == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.sym_abi_version() == 1
+
+
+def test_workspace_queries():
+    q = _lib.query
+    assert q("sym_paged_gqa_decode_workspace_bytes", 32, 16, 128, 4128) >= 32 * 16 * 17 * 130 * 4
+    assert q("sym_paged_gqa_decode_workspace_bytes", 0, 16, 128, 100) == 0
+    assert q("sym_moe_route_workspace_bytes", 32, 256) >= 256 * 16
+    assert q("sym_moe_route_workspace_bytes", 65, 256) >= 2 * 256 * 16
+    assert q("sym_moe_route_workspace_bytes", 0, 256) == 0
+
+
+def _call(name, *args):
+    lib = _lib.load()
+    rc = getattr(lib, name)(*args)
+    return rc, lib.sym_last_error().decode()
+
+
+FAKE = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+
+
+def test_decode_rejects_unsupported_head_dim():
+    rc, msg = _call("sym_paged_gqa_decode", FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 64, 16, 4,
+                    8, 64, 1.0, FAKE, 1 << 20, FAKE, None)
+    assert rc == 2 and "head_dim" in msg
+
+
+def test_decode_rejects_group_size_and_workspace():
+    rc, _ = _call("sym_paged_gqa_decode", FAKE, FAKE, FAKE, FAKE, FAKE, 2, 12, 4, 128, 16, 4, 8,
+                  64, 1.0, FAKE, 1 << 20, FAKE, None)
+    assert rc == 2
+    rc, msg = _call("sym_paged_gqa_decode", FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 16, 4,
+                    8, 64, 1.0, FAKE, 16, FAKE, None)
+    assert rc == 3 and "workspace" in msg
+    rc, _ = _call("sym_paged_gqa_decode", FAKE, FAKE, FAKE, FAKE, FAKE, 2, 8, 2, 128, 16, 4, 8,
+                  65, 1.0, FAKE, 1 << 20, FAKE, None)
+    assert rc == 1  # max_context beyond the page table
+
+
+def test_route_rejects_bad_configs():
+    args = lambda T, E, ng, tg, k: (FAKE, FAKE, T, E, ng, tg, k, 1.0, 1, 1, FAKE, FAKE, FAKE,
+                                    FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None)
+    assert _call("sym_moe_route_permute", *args(4, 96, 8, 4, 8))[0] == 2      # E not supported
+    assert _call("sym_moe_route_permute", *args(4, 256, 7, 4, 8))[0] == 1     # n_group
+    assert _call("sym_moe_route_permute", *args(4, 256, 8, 9, 8))[0] == 1     # topk_group
+    assert _call("sym_moe_route_permute", *args(4, 256, 8, 4, 33))[0] == 1    # top_k
+    assert _call("sym_moe_route_permute", *args(4, 64, 64, 4, 2))[0] == 2     # group of 1
+    assert _call("sym_moe_route_permute", *args(4, 64, 8, 1, 9))[0] == 1      # k > kept experts
+    rc, msg = _call("sym_moe_route_permute", *args(4, 256, 8, 4, 8)[:21], 8, None)
+    assert rc == 3 and "workspace" in msg
+    assert _call("sym_moe_route_permute", *args(0, 256, 8, 4, 8))[0] == 0     # empty batch
+
+
+def test_gemm_and_norm_reject_bad_shapes():
+    rc, _ = _call("sym_moe_grouped_swiglu", FAKE, 4, 2000, 512, FAKE, FAKE, FAKE, FAKE, FAKE,
+                  257, FAKE, FAKE, FAKE, FAKE, None)
+    assert rc == 2
+    rc, _ = _call("sym_moe_grouped_swiglu", None, 4, 2048, 512, FAKE, FAKE, FAKE, FAKE, FAKE,
+                  257, FAKE, FAKE, FAKE, FAKE, None)
+    assert rc == 1
+    rc, _ = _call("sym_rmsnorm_bf16", FAKE, None, FAKE, 4, 100, 1e-6, FAKE, None, None)
+    assert rc == 2
+    rc, _ = _call("sym_rmsnorm_bf16", FAKE, FAKE, FAKE, 4, 128, 1e-6, FAKE, None, None)
+    assert rc == 1  # residual without residual_out
+    rc, _ = _call("sym_paged_kv_fill", FAKE, FAKE, FAKE, FAKE, FAKE, 0, 60, 10, 2, 128, 16, 4,
+                  8, None)
+    assert rc == 1  # positions beyond the page table
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
+    with pytest.raises(_lib.HipExtensionMissing):
+        _lib.load()

@@ -1,0 +1,320 @@
+"""Kernel parity on the GPU, through the C ABI, against the oracle.
+
+Integer outputs (router indices, permute) are compared bit for bit with the C oracle; router
+weights too (same fp32 operations). Floating-point kernels are compared with fp32 references:
+  rmsnorm / prologue / decode / grouped GEMM outputs in bf16: |err| <= 1e-2 + 1e-2*|ref|
+  (bf16 rounding of the output is 2^-9 relative);
+  the down projection given the kernel's own h: fp32, rtol 1e-4;
+  KV cache writes: exact.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import route as R
+from oracle.paged_kv import paged_decode_ref
+from tt_symbiote_amd import hip_ops
+from tt_symbiote_amd.workloads import paged_context
+
+pytestmark = pytest.mark.gpu
+
+
+def _close(got, want, atol=1e-2, rtol=1e-2):
+    got = got.float().cpu()
+    want = want.float().cpu()
+    err = (got - want).abs()
+    bound = atol + rtol * want.abs()
+    assert bool((err <= bound).all()), \
+        f"max err {err.max().item():.3e}, worst excess {(err - bound).max().item():.3e}"
+
+
+# ------------------------------------------------------------------------------- rmsnorm
+@pytest.mark.parametrize("rows,cols", [(1, 2048), (32, 2048), (5, 136), (3, 16384)])
+def test_rmsnorm(device, rows, cols):
+    g = torch.Generator().manual_seed(rows + cols)
+    x = (torch.randn(rows, cols, generator=g) * 2).bfloat16()
+    r = torch.randn(rows, cols, generator=g).bfloat16()
+    w = (1 + 0.1 * torch.randn(cols, generator=g)).bfloat16()
+    out = hip_ops.rmsnorm(x.to(device), w.to(device), 1e-6)
+    ref = x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()
+    _close(out, ref)
+    out2, s = hip_ops.rmsnorm(x.to(device), w.to(device), 1e-6, residual=r.to(device))
+    s_ref = (x.float() + r.float()).bfloat16()
+    assert torch.equal(s.cpu(), s_ref)
+    ref2 = s_ref.float() * torch.rsqrt(s_ref.float().pow(2).mean(-1, keepdim=True) + 1e-6) \
+        * w.float()
+    _close(out2, ref2)
+
+
+# ------------------------------------------------------------------------------- router
+ROUTE_CASES = [
+    # T, E, n_group, topk_group, top_k, kind
+    (1, 256, 8, 4, 8, "randn"),
+    (32, 256, 8, 4, 8, "randn"),
+    (64, 256, 8, 4, 8, "randn"),
+    (65, 256, 8, 4, 8, "randn"),
+    (1000, 256, 8, 4, 8, "randn"),
+    (9000, 256, 8, 4, 8, "zipf"),
+    (300, 64, 8, 4, 4, "randn"),
+    (300, 128, 4, 2, 6, "randn"),
+    (200, 512, 16, 8, 8, "randn"),
+    (200, 64, 1, 1, 8, "randn"),
+    (500, 256, 8, 4, 8, "ties"),
+    (100, 256, 8, 4, 8, "extreme"),
+]
+
+
+def _route_inputs(T, E, kind, seed):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "ties":
+        logits = torch.randint(-4, 5, (T, E), generator=g).float() * 0.5
+        bias = torch.zeros(E)
+    elif kind == "extreme":
+        logits = torch.randn(T, E, generator=g) * 60
+        bias = torch.randn(E, generator=g) * 0.01
+    elif kind == "zipf":
+        # expert load skewed ~ rank^-1.1: add log-popularity to the logits
+        pop = torch.arange(1, E + 1).float().pow(-1.1)
+        logits = torch.randn(T, E, generator=g) + torch.log(pop)[torch.randperm(E, generator=g)]
+        bias = torch.randn(E, generator=g) * 0.01
+    else:
+        logits = torch.randn(T, E, generator=g) * 2
+        bias = torch.randn(E, generator=g) * 0.01
+    return logits.float().contiguous(), bias.float().contiguous()
+
+
+@pytest.mark.parametrize("T,E,n_group,topk_group,top_k,kind", ROUTE_CASES)
+@pytest.mark.parametrize("with_shared", [True, False])
+def test_route_permute_bit_exact(device, T, E, n_group, topk_group, top_k, kind, with_shared):
+    logits, bias = _route_inputs(T, E, kind, seed=T * 7 + E)
+    kw = dict(n_group=n_group, topk_group=topk_group, top_k=top_k, routed_scale=2.5)
+    res = hip_ops.moe_route_permute(logits.to(device), bias.to(device), renormalize=True,
+                                    with_shared=with_shared, **kw)
+    torch.cuda.synchronize()
+    idx_ref, w_ref = R.route_c(logits.numpy(), bias.numpy(), renormalize=True, **kw)
+    idx = res.topk_idx.cpu().numpy()
+    w = res.topk_w.cpu().numpy()
+    assert np.array_equal(idx, idx_ref)
+    assert np.array_equal(w.view(np.uint32), w_ref.view(np.uint32)), \
+        f"max weight diff {np.abs(w - w_ref).max()}"
+    p = R.permute_c(idx_ref, E, with_shared=with_shared)
+    assert np.array_equal(res.expert_counts.cpu().numpy(), p["expert_counts"])
+    assert np.array_equal(res.expert_offsets.cpu().numpy(), p["expert_offsets"])
+    assert np.array_equal(res.sorted_tokens.cpu().numpy(), p["sorted_tokens"])
+    assert np.array_equal(res.inv_perm.cpu().numpy(), p["inv_perm"])
+    ns = int(res.n_segments.item())
+    assert ns == int(p["n_segments"][0])
+    for name in ("seg_expert", "seg_offset", "seg_count"):
+        assert np.array_equal(getattr(res, name).cpu().numpy()[:ns], p[name][:ns]), name
+
+
+def test_route_no_renorm(device):
+    logits, bias = _route_inputs(40, 256, "randn", seed=3)
+    kw = dict(n_group=8, topk_group=4, top_k=8, routed_scale=2.5, renormalize=False)
+    res = hip_ops.moe_route_permute(logits.to(device), bias.to(device), **kw)
+    idx_ref, w_ref = R.route_c(logits.numpy(), bias.numpy(), **kw)
+    assert np.array_equal(res.topk_idx.cpu().numpy(), idx_ref)
+    assert np.array_equal(res.topk_w.cpu().numpy(), w_ref)
+
+
+def test_route_deterministic_across_runs(device):
+    logits, bias = _route_inputs(2000, 256, "ties", seed=9)
+    kw = dict(n_group=8, topk_group=4, top_k=8, routed_scale=2.5)
+    a = hip_ops.moe_route_permute(logits.to(device), bias.to(device), **kw)
+    b = hip_ops.moe_route_permute(logits.to(device), bias.to(device), **kw)
+    for name in ("topk_idx", "topk_w", "sorted_tokens", "inv_perm"):
+        assert torch.equal(getattr(a, name), getattr(b, name))
+
+
+# ------------------------------------------------------------------------------- grouped GEMM
+def _gemm_case(T, E, H, I, top_k, seed, device, with_shared=True, skew=False):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(T, H, generator=g).bfloat16()
+    slots = E + (1 if with_shared else 0)
+    wgu = (torch.randn(slots, 2 * I, H, generator=g) * 0.05).bfloat16()
+    wd = (torch.randn(slots, H, I, generator=g) * 0.05).bfloat16()
+    logits = torch.randn(T, E, generator=g) * 2
+    if skew:
+        logits[:, :4] += 6.0   # a few experts take most tokens
+    res = hip_ops.moe_route_permute(logits.to(device), torch.zeros(E, device=device),
+                                    n_group=8, topk_group=4, top_k=top_k, routed_scale=2.5,
+                                    with_shared=with_shared)
+    return x, wgu, wd, res
+
+
+@pytest.mark.parametrize("T,E,H,I,top_k,skew", [
+    (1, 64, 256, 128, 4, False),
+    (32, 256, 2048, 512, 8, False),
+    (7, 64, 512, 192, 4, False),
+    (200, 64, 256, 128, 6, True),       # segments of > 64 rows (several passes)
+])
+def test_grouped_swiglu(device, T, E, H, I, top_k, skew):
+    x, wgu, wd, res = _gemm_case(T, E, H, I, top_k, seed=T + E, device=device, skew=skew)
+    h, y = hip_ops.moe_grouped_swiglu(x.to(device), res, wgu.to(device), wd.to(device))
+    torch.cuda.synchronize()
+    st = res.sorted_tokens.cpu().long()
+    ns = int(res.n_segments.item())
+    seg_e = res.seg_expert.cpu()[:ns].tolist()
+    seg_o = res.seg_offset.cpu()[:ns].tolist()
+    seg_c = res.seg_count.cpu()[:ns].tolist()
+    hk = h.cpu()
+    yk = y.cpu()
+    xf = x.float()
+    for e, o, c in zip(seg_e, seg_o, seg_c):
+        rows = slice(o, o + c)
+        xe = xf[st[rows]]
+        gate = xe @ wgu[e, :I].float().T
+        up = xe @ wgu[e, I:].float().T
+        h_ref = F.silu(gate) * up
+        _close(hk[rows], h_ref, atol=2e-3, rtol=8e-3)
+        y_ref = hk[rows].float() @ wd[e].float().T
+        torch.testing.assert_close(yk[rows], y_ref, rtol=1e-4, atol=1e-4)
+
+
+def test_combine(device):
+    T, E, H, I, K = 32, 256, 2048, 512, 8
+    x, wgu, wd, res = _gemm_case(T, E, H, I, K, seed=5, device=device)
+    _, y = hip_ops.moe_grouped_swiglu(x.to(device), res, wgu.to(device), wd.to(device))
+    resid = torch.randn(T, H, generator=torch.Generator().manual_seed(6)).bfloat16()
+    out = hip_ops.moe_unpermute_combine(y, res, residual=resid.to(device))
+    yc = y.cpu()
+    inv = res.inv_perm.cpu().long()
+    w = res.topk_w.cpu()
+    ref = (yc[inv] * w[..., None]).sum(1) + yc[T * K:T * K + T] + resid.float()
+    _close(out, ref, atol=1e-2, rtol=8e-3)
+    out2 = hip_ops.moe_unpermute_combine(y, res)
+    _close(out2, (yc[inv] * w[..., None]).sum(1) + yc[T * K:T * K + T], atol=1e-2, rtol=8e-3)
+
+
+# ------------------------------------------------------------------------------- attention
+def _dev_ctx(ctx, device):
+    return (ctx.k_pool.to(device), ctx.v_pool.to(device), ctx.page_table.to(device),
+            ctx.positions.to(device))
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,bs,lo,hi", [
+    (1, 16, 4, 32, 512, 512),
+    (32, 16, 4, 32, 128, 4096),
+    (4, 8, 4, 16, 0, 40),
+    (4, 8, 8, 16, 3, 70),
+    (3, 16, 2, 64, 250, 260),
+    (5, 16, 16, 32, 1, 300),
+    (2, 32, 4, 32, 1000, 3000),
+])
+def test_paged_decode(device, B, Hq, Hkv, bs, lo, hi):
+    ctx = paged_context(B, lo, hi, block_size=bs, num_kv_heads=Hkv, seed=B + Hq + bs)
+    q = torch.randn(B, Hq, 128, generator=torch.Generator().manual_seed(1)).bfloat16()
+    kp, vp, pt, pos = _dev_ctx(ctx, device)
+    scale = 128 ** -0.5
+    out = hip_ops.paged_gqa_decode(q.to(device), kp, vp, pt, pos, scale)
+    ref = paged_decode_ref(q.float(), ctx.k_pool.float(), ctx.v_pool.float(), ctx.page_table,
+                           ctx.positions, scale)
+    _close(out, ref, atol=1e-2, rtol=1e-2)
+
+
+def test_paged_decode_split_boundaries(device):
+    # cached lengths around the 256-token split: 255 -> 256 slots, 256 -> 257 slots, ...
+    lens = [0, 1, 254, 255, 256, 511, 512, 1023]
+    B = len(lens)
+    ctxs = [paged_context(1, n, n, block_size=32, num_kv_heads=4, seed=n) for n in lens]
+    nb = sum(c.k_pool.shape[0] for c in ctxs)
+    kp = torch.cat([c.k_pool for c in ctxs])
+    vp = torch.cat([c.v_pool for c in ctxs])
+    mb = max(c.page_table.shape[1] for c in ctxs)
+    pt = torch.zeros(B, mb, dtype=torch.int32)
+    off = 0
+    for b, c in enumerate(ctxs):
+        pt[b, :c.page_table.shape[1]] = c.page_table[0] + off
+        off += c.k_pool.shape[0]
+    assert off == nb
+    pos = torch.tensor(lens, dtype=torch.int32)
+    q = torch.randn(B, 16, 128, generator=torch.Generator().manual_seed(2)).bfloat16()
+    out = hip_ops.paged_gqa_decode(q.to(device), kp.to(device), vp.to(device), pt.to(device),
+                                   pos.to(device), 0.1)
+    ref = paged_decode_ref(q.float(), kp.float(), vp.float(), pt, pos, 0.1)
+    _close(out, ref)
+
+
+def test_paged_decode_block_relabelling_is_bit_exact(device):
+    ctx = paged_context(6, 100, 900, block_size=32, num_kv_heads=4, seed=3)
+    q = torch.randn(6, 16, 128, generator=torch.Generator().manual_seed(4)).bfloat16().to(device)
+    kp, vp, pt, pos = _dev_ctx(ctx, device)
+    a = hip_ops.paged_gqa_decode(q, kp, vp, pt, pos, 0.09)
+    relabel = torch.randperm(kp.shape[0], generator=torch.Generator().manual_seed(5)).to(device)
+    kp2 = torch.empty_like(kp)
+    vp2 = torch.empty_like(vp)
+    kp2[relabel] = kp
+    vp2[relabel] = vp
+    b = hip_ops.paged_gqa_decode(q, kp2, vp2, relabel[pt.long()].int(), pos, 0.09)
+    assert torch.equal(a, b)
+
+
+def test_kv_write_and_fill(device):
+    ctx = paged_context(4, 10, 200, block_size=16, num_kv_heads=4, seed=8)
+    kp, vp, pt, pos = _dev_ctx(ctx, device)
+    kn = torch.randn(4, 4, 128).bfloat16()
+    vn = torch.randn(4, 4, 128).bfloat16()
+    hip_ops.paged_kv_write(kn.to(device), vn.to(device), kp, vp, pt, pos)
+    kpc, vpc = kp.cpu(), vp.cpu()
+    for b in range(4):
+        p = int(ctx.positions[b])
+        phys = int(ctx.page_table[b, p // 16])
+        assert torch.equal(kpc[phys, :, p % 16], kn[b])
+        assert torch.equal(vpc[phys, :, p % 16], vn[b])
+    # untouched slots unchanged
+    mask = torch.ones(kp.shape[0], 4, 16, dtype=torch.bool)
+    for b in range(4):
+        p = int(ctx.positions[b])
+        mask[int(ctx.page_table[b, p // 16]), :, p % 16] = False
+    assert torch.equal(kpc[mask], ctx.k_pool[mask])
+    # prompt fill of sequence 2 from position 0
+    S = int(ctx.positions[2]) + 1
+    kf = torch.randn(4, S, 128).bfloat16()
+    vf = torch.randn(4, S, 128).bfloat16()
+    hip_ops.paged_kv_fill(kf.to(device), vf.to(device), kp, vp, pt, batch_idx=2)
+    kpc, vpc = kp.cpu(), vp.cpu()
+    for s in range(S):
+        phys = int(ctx.page_table[2, s // 16])
+        assert torch.equal(kpc[phys, :, s % 16], kf[:, s])
+        assert torch.equal(vpc[phys, :, s % 16], vf[:, s])
+
+
+@pytest.mark.parametrize("rotary_dim,use_norm", [(64, True), (128, True), (64, False)])
+def test_decode_prologue(device, rotary_dim, use_norm):
+    from oracle.bailing_moe_v2 import apply_partial_rotary
+
+    B, Hq, Hkv, D = 8, 16, 4, 128
+    ctx = paged_context(B, 5, 3000, block_size=32, num_kv_heads=Hkv, seed=11)
+    kp, vp, pt, pos = _dev_ctx(ctx, device)
+    g = torch.Generator().manual_seed(12)
+    qkv = torch.randn(B, (Hq + 2 * Hkv) * D, generator=g).bfloat16()
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16()
+    theta, max_pos = 1e6, 4096
+    inv = 1.0 / (theta ** (torch.arange(0, rotary_dim, 2).float() / rotary_dim))
+    fr = torch.arange(max_pos).float()[:, None] * inv[None]
+    table = torch.cat([fr.cos(), fr.sin()], 1).contiguous()
+    q = hip_ops.attn_decode_prologue(
+        qkv.to(device), pos, kp, vp, pt, num_heads=Hq, num_kv_heads=Hkv, rotary_dim=rotary_dim,
+        rope_cs=table.to(device), q_norm_w=qn.to(device) if use_norm else None,
+        k_norm_w=kn.to(device) if use_norm else None, eps=1e-6)
+    # oracle
+    x = qkv.float().view(B, Hq + 2 * Hkv, D)
+    qr, kr, vr = x[:, :Hq], x[:, Hq:Hq + Hkv], x[:, Hq + Hkv:]
+
+    def norm(t, w):
+        return t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()
+
+    if use_norm:
+        qr, kr = norm(qr, qn), norm(kr, kn)
+    cos = torch.cat([fr[ctx.positions.long()]] * 2, -1).cos()[:, None, :]   # [B,1,rd]
+    sin = torch.cat([fr[ctx.positions.long()]] * 2, -1).sin()[:, None, :]
+    q_ref, k_ref = apply_partial_rotary(qr.unsqueeze(2), kr.unsqueeze(2), cos, sin)
+    _close(q, q_ref[:, :, 0], atol=2e-2, rtol=1e-2)
+    kpc, vpc = kp.cpu(), vp.cpu()
+    for b in range(B):
+        p = int(ctx.positions[b])
+        phys = int(ctx.page_table[b, p // 32])
+        _close(kpc[phys, :, p % 32], k_ref[b, :, 0], atol=2e-2, rtol=1e-2)
+        assert torch.equal(vpc[phys, :, p % 32], vr[b].bfloat16())

@@ -1,0 +1,80 @@
+// Device helpers shared by the gfx950 kernels: bf16 bit conversions, wave64 reductions,
+// MFMA operand types, and the error plumbing of the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "../../include/symbiote_mi355x.h"
+
+namespace sym {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 (the rounding torch uses for .to(torch.bfloat16)).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+}
+
+// 8 bf16 packed in a uint4 -> 8 floats.
+__device__ __forceinline__ void unpack8(const uint4& v, float* f) {
+  f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x);
+  f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+  f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z);
+  f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off));
+  return v;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// 16x16x32 bf16 MFMA, fp32 accumulate. Operand layout (wave64):
+//   A[16 x 32]: lane l holds A[l % 16][8*(l/16) .. 8*(l/16)+7]
+//   B[32 x 16]: lane l holds B[8*(l/16) .. +7][l % 16]
+//   D[16 x 16]: lane l holds D[4*(l/16) + i][l % 16], i = 0..3
+__device__ __forceinline__ floatx4 mfma16x16x32(const uint4& a, const uint4& b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+}  // namespace sym
+
+// ---- host-side error plumbing (one message per calling thread) ----
+namespace sym_host {
+int set_error(int code, const char* fmt, ...);
+int check_launch(const char* what);
+}  // namespace sym_host
+
+#define SYM_REQUIRE(cond, code, ...)                         \
+  do {                                                       \
+    if (!(cond)) return sym_host::set_error((code), __VA_ARGS__); \
+  } while (0)

@@ -1,0 +1,278 @@
+// Grouped SwiGLU expert GEMMs over ragged per-expert row counts, and the weighted combine.
+//
+// Reference semantics: TTNNExperts.forward (ttnn_moe.py:1159-1343): per expert
+// h = silu(x W1^T) * (x W3^T), y = h W2^T, then combine sum_k w_k y_k (ttnn_moe.py:1307-1335);
+// shared expert TTNNGlm4MoeMLP (ttnn_moe.py:656-675) added at ttnn_moe.py:1487-1490.
+//
+// Design for gfx950 at decode sizes (about 1-6 rows per routed expert, T rows for the shared
+// expert): the kernels are weight-streaming. One wave owns 16 output columns of one segment
+// (expert) and walks the full reduction dimension once, so every weight byte is read from HBM
+// exactly once per step. The 16 weight rows form the B operand of v_mfma_f32_16x16x32_bf16:
+// lane l streams 32 contiguous bytes of row (l % 16) per 64-wide K step (4 lanes cover 128
+// contiguous bytes of a row), and the rows of the segment (tokens, gathered through
+// sorted_tokens) form the A operand, padded to 16 with zero fragments. Both operands use the
+// same lane -> K mapping, so the K order inside a step is free to follow memory order. Up to
+// MT row tiles (16 rows each) are accumulated per pass over the weights.
+// Segments live on the device: workgroups past *n_segments exit at once, so the grid is sized
+// for the worst case (E+1 segments) without a host synchronization.
+#include "common.h"
+
+namespace sym {
+
+constexpr int kGemmThreads = 256;  // 4 waves; each wave owns 16 output columns
+constexpr int kColsPerWG = 64;
+
+__device__ __forceinline__ uint4 ld16(const uint16_t* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+template <int MT>
+__global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
+    const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
+    const int32_t* __restrict__ seg_expert, const int32_t* __restrict__ seg_offset,
+    const int32_t* __restrict__ seg_count, const int32_t* __restrict__ n_segments,
+    const uint16_t* __restrict__ w_gu, uint16_t* __restrict__ h, int tiles_per_seg) {
+  const int seg = blockIdx.x / tiles_per_seg;
+  if (seg >= n_segments[0]) return;
+  const int tile = blockIdx.x - seg * tiles_per_seg;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int col0 = (tile * 4 + wave) * 16;
+  if (col0 >= I) return;
+  const int e = seg_expert[seg];
+  const int row0 = seg_offset[seg];
+  const int cnt = seg_count[seg];
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+
+  const uint16_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * 16;
+  const uint16_t* wu = wg + (size_t)I * H;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  for (int mb = 0; mb < cnt; mb += 16 * MT) {
+    const int nmt = min(MT, (cnt - mb + 15) >> 4);
+    floatx4 accg[MT], accu[MT];
+    const uint16_t* xr[MT];
+    bool ok[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      accg[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      accu[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int r = mb + mt * 16 + r16;
+      ok[mt] = r < cnt;
+      const int tok = ok[mt] ? sorted_tokens[row0 + r] : 0;
+      xr[mt] = x + (size_t)tok * H + kq * 16;
+    }
+#pragma unroll 4
+    for (int k0 = 0; k0 < H; k0 += 64) {
+      const uint4 g0 = ld16(wg + k0), g1 = ld16(wg + k0 + 8);
+      const uint4 u0 = ld16(wu + k0), u1 = ld16(wu + k0 + 8);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (mt < nmt) {
+          const uint4 a0 = ok[mt] ? ld16(xr[mt] + k0) : zero;
+          const uint4 a1 = ok[mt] ? ld16(xr[mt] + k0 + 8) : zero;
+          accg[mt] = mfma16x16x32(a0, g0, accg[mt]);
+          accg[mt] = mfma16x16x32(a1, g1, accg[mt]);
+          accu[mt] = mfma16x16x32(a0, u0, accu[mt]);
+          accu[mt] = mfma16x16x32(a1, u1, accu[mt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt < nmt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = mb + mt * 16 + kq * 4 + i;
+          if (r < cnt) {
+            const float g = accg[mt][i];
+            const float u = accu[mt][i];
+            const float hv = g / (1.0f + expf(-g)) * u;
+            h[(size_t)(row0 + r) * I + col0 + r16] = f32_to_bf16(hv);
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int MT>
+__global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
+    const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
+    const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
+    const int32_t* __restrict__ n_segments, const uint16_t* __restrict__ w_d,
+    float* __restrict__ y, int tiles_per_seg) {
+  const int seg = blockIdx.x / tiles_per_seg;
+  if (seg >= n_segments[0]) return;
+  const int tile = blockIdx.x - seg * tiles_per_seg;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int col0 = (tile * 4 + wave) * 16;
+  if (col0 >= H) return;
+  const int e = seg_expert[seg];
+  const int row0 = seg_offset[seg];
+  const int cnt = seg_count[seg];
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+
+  const uint16_t* wd = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 16;
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+
+  for (int mb = 0; mb < cnt; mb += 16 * MT) {
+    const int nmt = min(MT, (cnt - mb + 15) >> 4);
+    floatx4 acc[MT];
+    const uint16_t* hr[MT];
+    bool ok[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int r = mb + mt * 16 + r16;
+      ok[mt] = r < cnt;
+      hr[mt] = hbuf + (size_t)(row0 + (ok[mt] ? r : 0)) * I + kq * 16;
+    }
+#pragma unroll 8
+    for (int k0 = 0; k0 < I; k0 += 64) {
+      const uint4 b0 = ld16(wd + k0), b1 = ld16(wd + k0 + 8);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (mt < nmt) {
+          const uint4 a0 = ok[mt] ? ld16(hr[mt] + k0) : zero;
+          const uint4 a1 = ok[mt] ? ld16(hr[mt] + k0 + 8) : zero;
+          acc[mt] = mfma16x16x32(a0, b0, acc[mt]);
+          acc[mt] = mfma16x16x32(a1, b1, acc[mt]);
+        }
+      }
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if (mt < nmt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = mb + mt * 16 + kq * 4 + i;
+          if (r < cnt) y[(size_t)(row0 + r) * H + col0 + r16] = acc[mt][i];
+        }
+      }
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) void moe_combine_kernel(
+    const float* __restrict__ y, const int32_t* __restrict__ inv_perm,
+    const float* __restrict__ topk_w, int K, int H, int shared_row0,
+    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out) {
+  const int t = blockIdx.x;
+  for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
+    float acc[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+    for (int k = 0; k < K; ++k) {
+      const int row = inv_perm[(size_t)t * K + k];
+      const float wk = topk_w[(size_t)t * K + k];
+      const float4* yp = reinterpret_cast<const float4*>(y + (size_t)row * H + c);
+      const float4 f0 = yp[0], f1 = yp[1];
+      acc[0] += wk * f0.x; acc[1] += wk * f0.y; acc[2] += wk * f0.z; acc[3] += wk * f0.w;
+      acc[4] += wk * f1.x; acc[5] += wk * f1.y; acc[6] += wk * f1.z; acc[7] += wk * f1.w;
+    }
+    if (shared_row0 >= 0) {
+      const float4* yp = reinterpret_cast<const float4*>(y + (size_t)(shared_row0 + t) * H + c);
+      const float4 f0 = yp[0], f1 = yp[1];
+      acc[0] += f0.x; acc[1] += f0.y; acc[2] += f0.z; acc[3] += f0.w;
+      acc[4] += f1.x; acc[5] += f1.y; acc[6] += f1.z; acc[7] += f1.w;
+    }
+    if (residual) {
+      float r[8];
+      unpack8(*reinterpret_cast<const uint4*>(residual + (size_t)t * H + c), r);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += r[i];
+    }
+    uint4 o;
+    o.x = pack_bf16x2(acc[0], acc[1]);
+    o.y = pack_bf16x2(acc[2], acc[3]);
+    o.z = pack_bf16x2(acc[4], acc[5]);
+    o.w = pack_bf16x2(acc[6], acc[7]);
+    *reinterpret_cast<uint4*>(out + (size_t)t * H + c) = o;
+  }
+}
+
+}  // namespace sym
+
+using namespace sym;
+
+static int check_gemm_args(const char* what, int T, int H, int I, int max_segments) {
+  SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "%s: T=%d < 0", what, T);
+  SYM_REQUIRE(H > 0 && H % 64 == 0, SYM_ERR_UNSUPPORTED,
+              "%s: H=%d must be a positive multiple of 64", what, H);
+  SYM_REQUIRE(I > 0 && I % 64 == 0, SYM_ERR_UNSUPPORTED,
+              "%s: I=%d must be a positive multiple of 64", what, I);
+  SYM_REQUIRE(max_segments >= 1 && max_segments <= 4096, SYM_ERR_INVALID,
+              "%s: max_segments=%d out of range", what, max_segments);
+  return SYM_OK;
+}
+
+extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t* sorted_tokens,
+                               const int32_t* seg_expert, const int32_t* seg_offset,
+                               const int32_t* seg_count, const int32_t* n_segments,
+                               int max_segments, const void* w_gate_up, void* h, void* stream) {
+  int rc = check_gemm_args("moe_gate_up", T, H, I, max_segments);
+  if (rc) return rc;
+  if (T == 0) return SYM_OK;
+  SYM_REQUIRE(x && sorted_tokens && seg_expert && seg_offset && seg_count && n_segments &&
+                  w_gate_up && h,
+              SYM_ERR_INVALID, "moe_gate_up: null pointer argument");
+  (void)hipGetLastError();
+  const int tiles = (I + kColsPerWG - 1) / kColsPerWG;
+  hipLaunchKernelGGL(moe_gate_up_kernel<4>, dim3(max_segments * tiles), dim3(kGemmThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, H, I, sorted_tokens, seg_expert,
+                     seg_offset, seg_count, n_segments, (const uint16_t*)w_gate_up, (uint16_t*)h,
+                     tiles);
+  return sym_host::check_launch("moe_gate_up_kernel");
+}
+
+extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* seg_expert,
+                            const int32_t* seg_offset, const int32_t* seg_count,
+                            const int32_t* n_segments, int max_segments, const void* w_down,
+                            float* y, void* stream) {
+  int rc = check_gemm_args("moe_down", T, H, I, max_segments);
+  if (rc) return rc;
+  if (T == 0) return SYM_OK;
+  SYM_REQUIRE(h && seg_expert && seg_offset && seg_count && n_segments && w_down && y,
+              SYM_ERR_INVALID, "moe_down: null pointer argument");
+  (void)hipGetLastError();
+  const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
+  hipLaunchKernelGGL(moe_down_kernel<4>, dim3(max_segments * tiles), dim3(kGemmThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)h, H, I, seg_expert, seg_offset,
+                     seg_count, n_segments, (const uint16_t*)w_down, y, tiles);
+  return sym_host::check_launch("moe_down_kernel");
+}
+
+extern "C" int sym_moe_grouped_swiglu(const void* x, int T, int H, int I,
+                                      const int32_t* sorted_tokens, const int32_t* seg_expert,
+                                      const int32_t* seg_offset, const int32_t* seg_count,
+                                      const int32_t* n_segments, int max_segments,
+                                      const void* w_gate_up, const void* w_down, void* h, float* y,
+                                      void* stream) {
+  int rc = sym_moe_gate_up(x, T, H, I, sorted_tokens, seg_expert, seg_offset, seg_count,
+                           n_segments, max_segments, w_gate_up, h, stream);
+  if (rc) return rc;
+  return sym_moe_down(h, T, H, I, seg_expert, seg_offset, seg_count, n_segments, max_segments,
+                      w_down, y, stream);
+}
+
+extern "C" int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm,
+                                         const float* topk_w, int T, int top_k, int H,
+                                         int shared_row0, const void* residual, void* out,
+                                         void* stream) {
+  SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "moe_unpermute_combine: T=%d < 0", T);
+  if (T == 0) return SYM_OK;
+  SYM_REQUIRE(y && inv_perm && topk_w && out, SYM_ERR_INVALID,
+              "moe_unpermute_combine: null pointer argument");
+  SYM_REQUIRE(H > 0 && H % 8 == 0, SYM_ERR_UNSUPPORTED,
+              "moe_unpermute_combine: H=%d must be a positive multiple of 8", H);
+  SYM_REQUIRE(top_k >= 1 && top_k <= 64, SYM_ERR_INVALID, "moe_unpermute_combine: top_k=%d",
+              top_k);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, y, inv_perm,
+                     topk_w, top_k, H, shared_row0, (const uint16_t*)residual, (uint16_t*)out);
+  return sym_host::check_launch("moe_combine_kernel");
+}

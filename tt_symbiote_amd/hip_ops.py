@@ -1,0 +1,376 @@
+"""torch-facing wrappers of the C-ABI kernels.
+
+Every wrapper checks device, dtype, contiguity and shapes on the host before it launches
+anything, passes raw pointers plus ``torch.cuda.current_stream()``, and raises on a non-zero
+status. Outputs are allocated with torch (caching allocator) unless the caller passes them in.
+There is no CPU path here: CPU tensors are rejected.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+HEAD_DIM = 128
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+class KernelTimer:
+    """Brackets chosen entry points with HIP events on the launching stream.
+
+    Install with :func:`set_kernel_timer`; each wrapped call records a start/end event pair on
+    ``torch.cuda.current_stream()`` (the stream the kernel is launched on). After a
+    synchronisation, :meth:`mean_ms` gives the average duration per call."""
+
+    def __init__(self, names):
+        self.names = set(names)
+        self.events = {n: [] for n in self.names}
+
+    def wrap(self, name, fn):
+        if name not in self.names:
+            return fn()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        out = fn()
+        end.record()
+        self.events[name].append((start, end))
+        return out
+
+    def mean_ms(self, name) -> float:
+        ev = self.events[name]
+        return sum(s.elapsed_time(e) for s, e in ev) / len(ev) if ev else float("nan")
+
+    def count(self, name) -> int:
+        return len(self.events[name])
+
+
+_timer = None
+
+
+def set_kernel_timer(timer) -> None:
+    global _timer
+    _timer = timer
+
+
+def _timed(name, fn):
+    return fn() if _timer is None else _timer.wrap(name, fn)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _check(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device = None) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be a GPU tensor (got device {t.device})")
+    if device is not None and t.device != device:
+        raise ValueError(f"{name}: on {t.device}, expected {device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: must be contiguous")
+    if t.data_ptr() % 16:
+        # the kernels use 16-byte vector loads
+        raise ValueError(f"{name}: data pointer must be 16-byte aligned")
+
+
+def _check_shape(t: torch.Tensor, name: str, shape: tuple) -> None:
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
+# -------------------------------------------------------------------------------------------
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+            residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+            residual_out: Optional[torch.Tensor] = None):
+    """RMSNorm over the last dim (bf16). With ``residual``: returns (normed, x + residual)."""
+    _check(x, "x", torch.bfloat16)
+    cols = x.shape[-1]
+    rows = x.numel() // cols if cols else 0
+    _check(weight, "weight", torch.bfloat16, x.device)
+    _check_shape(weight, "weight", (cols,))
+    if out is None:
+        out = torch.empty_like(x)
+    _check(out, "out", torch.bfloat16, x.device)
+    _check_shape(out, "out", tuple(x.shape))
+    if residual is not None:
+        _check(residual, "residual", torch.bfloat16, x.device)
+        _check_shape(residual, "residual", tuple(x.shape))
+        if residual_out is None:
+            residual_out = torch.empty_like(x)
+        _check(residual_out, "residual_out", torch.bfloat16, x.device)
+        _check_shape(residual_out, "residual_out", tuple(x.shape))
+    _lib.call("sym_rmsnorm_bf16", _ptr(x), _ptr(residual), _ptr(weight), rows, cols, float(eps),
+              _ptr(out), _ptr(residual_out), _stream())
+    return (out, residual_out) if residual is not None else out
+
+
+# -------------------------------------------------------------------------------------------
+@dataclass
+class PagedLayout:
+    """Geometry of one layer's paged KV pools and the page table."""
+
+    num_blocks: int
+    num_kv_heads: int
+    block_size: int
+    head_dim: int
+    max_blocks_per_seq: int
+
+
+def _check_pools(k_pool, v_pool, block_tables, batch: int) -> PagedLayout:
+    _check(k_pool, "k_pool", torch.bfloat16)
+    _check(v_pool, "v_pool", torch.bfloat16, k_pool.device)
+    if k_pool.dim() != 4 or k_pool.shape != v_pool.shape:
+        raise ValueError(f"k_pool/v_pool must be [num_blocks, Hkv, block_size, D] and equal, got "
+                         f"{tuple(k_pool.shape)} / {tuple(v_pool.shape)}")
+    nb, hkv, bs, d = k_pool.shape
+    if d != HEAD_DIM:
+        raise ValueError(f"head_dim {d} unsupported (kernels implement {HEAD_DIM})")
+    _check(block_tables, "block_tables", torch.int32, k_pool.device)
+    if block_tables.dim() != 2 or block_tables.shape[0] < batch:
+        raise ValueError(f"block_tables must be [>= {batch}, max_blocks_per_seq], got "
+                         f"{tuple(block_tables.shape)}")
+    return PagedLayout(nb, hkv, bs, d, block_tables.shape[1])
+
+
+def attn_decode_prologue(qkv: torch.Tensor, positions: torch.Tensor, k_pool: torch.Tensor,
+                         v_pool: torch.Tensor, block_tables: torch.Tensor, *, num_heads: int,
+                         num_kv_heads: int, rotary_dim: int, rope_cs: Optional[torch.Tensor],
+                         q_norm_w: Optional[torch.Tensor], k_norm_w: Optional[torch.Tensor],
+                         eps: float, q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """QK-norm + partial RoPE on q/k of ``qkv`` [B, (Hq+2Hkv)*D]; writes k/v into the pools at
+    ``positions``; returns q [B, Hq, D]."""
+    _check(qkv, "qkv", torch.bfloat16)
+    B = qkv.shape[0]
+    _check_shape(qkv, "qkv", (B, (num_heads + 2 * num_kv_heads) * HEAD_DIM))
+    _check(positions, "positions", torch.int32, qkv.device)
+    _check_shape(positions, "positions", (B,))
+    lay = _check_pools(k_pool, v_pool, block_tables, B)
+    if lay.num_kv_heads != num_kv_heads:
+        raise ValueError(f"pool has {lay.num_kv_heads} kv heads, module {num_kv_heads}")
+    use_norm = q_norm_w is not None
+    if use_norm:
+        for t, n in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+            _check(t, n, torch.bfloat16, qkv.device)
+            _check_shape(t, n, (HEAD_DIM,))
+    max_pos = 0
+    if rotary_dim:
+        _check(rope_cs, "rope_cs", torch.float32, qkv.device)
+        if rope_cs.dim() != 2 or rope_cs.shape[1] != rotary_dim:
+            raise ValueError(f"rope_cs must be [max_pos, {rotary_dim}], got {tuple(rope_cs.shape)}")
+        max_pos = rope_cs.shape[0]
+    if q_out is None:
+        q_out = torch.empty(B, num_heads, HEAD_DIM, dtype=torch.bfloat16, device=qkv.device)
+    _check(q_out, "q_out", torch.bfloat16, qkv.device)
+    _check_shape(q_out, "q_out", (B, num_heads, HEAD_DIM))
+    _lib.call("sym_attn_decode_prologue", _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w),
+              _ptr(rope_cs), max_pos, _ptr(positions), B, num_heads, num_kv_heads, HEAD_DIM,
+              rotary_dim, float(eps), 1 if use_norm else 0, _ptr(q_out), _ptr(k_pool),
+              _ptr(v_pool), _ptr(block_tables), lay.max_blocks_per_seq, lay.block_size,
+              lay.num_blocks, _stream())
+    return q_out
+
+
+def paged_kv_write(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
+                   v_pool: torch.Tensor, block_tables: torch.Tensor,
+                   positions: torch.Tensor) -> None:
+    """Write one token per sequence: k_new/v_new [B, Hkv, D] at slot positions[b]."""
+    _check(k_new, "k_new", torch.bfloat16)
+    _check(v_new, "v_new", torch.bfloat16, k_new.device)
+    B = k_new.shape[0]
+    lay = _check_pools(k_pool, v_pool, block_tables, B)
+    _check_shape(k_new, "k_new", (B, lay.num_kv_heads, HEAD_DIM))
+    _check_shape(v_new, "v_new", (B, lay.num_kv_heads, HEAD_DIM))
+    _check(positions, "positions", torch.int32, k_new.device)
+    _check_shape(positions, "positions", (B,))
+    _lib.call("sym_paged_kv_write", _ptr(k_new), _ptr(v_new), _ptr(k_pool), _ptr(v_pool),
+              _ptr(block_tables), _ptr(positions), B, lay.num_kv_heads, HEAD_DIM, lay.block_size,
+              lay.max_blocks_per_seq, lay.num_blocks, _stream())
+
+
+def paged_kv_fill(k: torch.Tensor, v: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                  block_tables: torch.Tensor, batch_idx: int, start_pos: int = 0) -> None:
+    """Write a prompt's K/V [Hkv, S, D] for sequence ``batch_idx`` from ``start_pos``."""
+    _check(k, "k", torch.bfloat16)
+    _check(v, "v", torch.bfloat16, k.device)
+    lay = _check_pools(k_pool, v_pool, block_tables, batch_idx + 1)
+    if k.dim() != 3 or k.shape[0] != lay.num_kv_heads or k.shape[2] != HEAD_DIM:
+        raise ValueError(f"k must be [Hkv={lay.num_kv_heads}, S, {HEAD_DIM}], got {tuple(k.shape)}")
+    _check_shape(v, "v", tuple(k.shape))
+    _lib.call("sym_paged_kv_fill", _ptr(k), _ptr(v), _ptr(k_pool), _ptr(v_pool),
+              _ptr(block_tables), int(batch_idx), int(start_pos), k.shape[1], lay.num_kv_heads,
+              HEAD_DIM, lay.block_size, lay.max_blocks_per_seq, lay.num_blocks, _stream())
+
+
+def paged_decode_workspace_bytes(batch: int, num_heads: int, max_context: int) -> int:
+    return _lib.query("sym_paged_gqa_decode_workspace_bytes", batch, num_heads, HEAD_DIM,
+                      max_context)
+
+
+def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                     block_tables: torch.Tensor, positions: torch.Tensor, scale: float,
+                     max_context: Optional[int] = None, workspace: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode attention of q [B, Hq, D] over slots 0..positions[b] of each sequence."""
+    _check(q, "q", torch.bfloat16)
+    if q.dim() != 3 or q.shape[2] != HEAD_DIM:
+        raise ValueError(f"q must be [B, Hq, {HEAD_DIM}], got {tuple(q.shape)}")
+    B, Hq, _ = q.shape
+    lay = _check_pools(k_pool, v_pool, block_tables, B)
+    _check(positions, "positions", torch.int32, q.device)
+    _check_shape(positions, "positions", (B,))
+    cap = lay.max_blocks_per_seq * lay.block_size
+    if max_context is None:
+        max_context = cap
+    if not 0 < max_context <= cap:
+        raise ValueError(f"max_context {max_context} outside (0, {cap}]")
+    need = paged_decode_workspace_bytes(B, Hq, max_context)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _check(workspace, "workspace", torch.uint8, q.device)
+    if out is None:
+        out = torch.empty_like(q)
+    _check(out, "out", torch.bfloat16, q.device)
+    _check_shape(out, "out", tuple(q.shape))
+    _timed("paged_gqa_decode", lambda: _lib.call(
+        "sym_paged_gqa_decode", _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
+        _ptr(positions), B, Hq, lay.num_kv_heads, HEAD_DIM, lay.block_size,
+        lay.max_blocks_per_seq, lay.num_blocks, int(max_context), float(scale),
+        _ptr(workspace), workspace.numel(), _ptr(out), _stream()))
+    return out
+
+
+# -------------------------------------------------------------------------------------------
+@dataclass
+class RouteResult:
+    """Outputs of :func:`moe_route_permute` (all on the device)."""
+
+    topk_idx: torch.Tensor       # [T, K] int32
+    topk_w: torch.Tensor         # [T, K] fp32
+    expert_counts: torch.Tensor  # [E] int32
+    expert_offsets: torch.Tensor  # [E+1] int32
+    sorted_tokens: torch.Tensor  # [T*K (+T)] int32
+    inv_perm: torch.Tensor       # [T, K] int32
+    seg_expert: torch.Tensor     # [E+1] int32
+    seg_offset: torch.Tensor     # [E+1] int32
+    seg_count: torch.Tensor      # [E+1] int32
+    n_segments: torch.Tensor     # [1] int32
+    with_shared: bool
+
+    @property
+    def rows(self) -> int:
+        return self.sorted_tokens.numel()
+
+
+def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,
+                      topk_group: int, top_k: int, routed_scale: float,
+                      renormalize: bool = True, with_shared: bool = True) -> RouteResult:
+    """Fused sigmoid/bias/group-limited top-k router + expert-sorted permute."""
+    _check(logits, "logits", torch.float32)
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [T, E], got {tuple(logits.shape)}")
+    T, E = logits.shape
+    dev = logits.device
+    _check(bias, "bias", torch.float32, dev)
+    _check_shape(bias, "bias", (E,))
+    i32 = dict(dtype=torch.int32, device=dev)
+    rows = T * top_k + (T if with_shared else 0)
+    res = RouteResult(
+        topk_idx=torch.empty(T, top_k, **i32),
+        topk_w=torch.empty(T, top_k, dtype=torch.float32, device=dev),
+        expert_counts=torch.empty(E, **i32),
+        expert_offsets=torch.empty(E + 1, **i32),
+        sorted_tokens=torch.empty(rows, **i32),
+        inv_perm=torch.empty(T, top_k, **i32),
+        seg_expert=torch.empty(E + 1, **i32),
+        seg_offset=torch.empty(E + 1, **i32),
+        seg_count=torch.empty(E + 1, **i32),
+        n_segments=torch.zeros(1, **i32),
+        with_shared=bool(with_shared),
+    )
+    if T == 0:
+        return res
+    ws_bytes = _lib.query("sym_moe_route_workspace_bytes", T, E)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    _lib.call("sym_moe_route_permute", _ptr(logits), _ptr(bias), T, E, int(n_group),
+              int(topk_group), int(top_k), float(routed_scale), 1 if renormalize else 0,
+              1 if with_shared else 0, _ptr(res.topk_idx), _ptr(res.topk_w),
+              _ptr(res.expert_counts), _ptr(res.expert_offsets), _ptr(res.sorted_tokens),
+              _ptr(res.inv_perm), _ptr(res.seg_expert), _ptr(res.seg_offset),
+              _ptr(res.seg_count), _ptr(res.n_segments), _ptr(ws), ws.numel(), _stream())
+    return res
+
+
+def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up: torch.Tensor,
+                       w_down: torch.Tensor, h: Optional[torch.Tensor] = None,
+                       y: Optional[torch.Tensor] = None):
+    """h = silu(x Wg^T) * (x Wu^T), y = h Wd^T per segment; returns (h [rows, I], y [rows, H])."""
+    _check(x, "x", torch.bfloat16)
+    if x.dim() != 2:
+        raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
+    T, H = x.shape
+    dev = x.device
+    _check(w_gate_up, "w_gate_up", torch.bfloat16, dev)
+    _check(w_down, "w_down", torch.bfloat16, dev)
+    if w_gate_up.dim() != 3 or w_gate_up.shape[2] != H or w_gate_up.shape[1] % 2:
+        raise ValueError(f"w_gate_up must be [S, 2I, {H}], got {tuple(w_gate_up.shape)}")
+    S, I2, _ = w_gate_up.shape
+    I = I2 // 2
+    _check_shape(w_down, "w_down", (S, H, I))
+    max_segments = route.seg_expert.numel()
+    E = route.expert_counts.numel()
+    if S < E + (1 if route.with_shared else 0):
+        raise ValueError(f"weight stack has {S} slots; routing needs {E} experts"
+                         f"{' + shared' if route.with_shared else ''}")
+    if route.topk_idx.shape[0] != T:
+        raise ValueError(f"routing covers {route.topk_idx.shape[0]} tokens, x has {T}")
+    rows = route.rows
+    if h is None:
+        h = torch.empty(rows, I, dtype=torch.bfloat16, device=dev)
+    if y is None:
+        y = torch.empty(rows, H, dtype=torch.float32, device=dev)
+    _check(h, "h", torch.bfloat16, dev)
+    _check_shape(h, "h", (rows, I))
+    _check(y, "y", torch.float32, dev)
+    _check_shape(y, "y", (rows, H))
+    stream = _stream()
+    _timed("moe_gate_up", lambda: _lib.call(
+        "sym_moe_gate_up", _ptr(x), T, H, I, _ptr(route.sorted_tokens), _ptr(route.seg_expert),
+        _ptr(route.seg_offset), _ptr(route.seg_count), _ptr(route.n_segments), max_segments,
+        _ptr(w_gate_up), _ptr(h), stream))
+    _timed("moe_down", lambda: _lib.call(
+        "sym_moe_down", _ptr(h), T, H, I, _ptr(route.seg_expert), _ptr(route.seg_offset),
+        _ptr(route.seg_count), _ptr(route.n_segments), max_segments, _ptr(w_down), _ptr(y),
+        stream))
+    return h, y
+
+
+def moe_unpermute_combine(y: torch.Tensor, route: RouteResult,
+                          residual: Optional[torch.Tensor] = None,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[t] = sum_k w[t,k] y[inv[t,k]] (+ shared row) (+ residual[t]), bf16 [T, H]."""
+    _check(y, "y", torch.float32)
+    T, K = route.topk_idx.shape
+    H = y.shape[1]
+    dev = y.device
+    _check_shape(y, "y", (route.rows, H))
+    if residual is not None:
+        _check(residual, "residual", torch.bfloat16, dev)
+        _check_shape(residual, "residual", (T, H))
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
+    _check(out, "out", torch.bfloat16, dev)
+    _check_shape(out, "out", (T, H))
+    shared_row0 = T * K if route.with_shared else -1
+    _lib.call("sym_moe_unpermute_combine", _ptr(y), _ptr(route.inv_perm), _ptr(route.topk_w), T,
+              K, H, shared_row0, _ptr(residual), _ptr(out), _stream())
+    return out

@@ -1,0 +1,7 @@
+from .attention import HIPBailingMoEAttention
+from .decoder_layer import HIPBailingMoEDecoderLayer
+from .kv_cache import HIPPagedAttentionKVCache, PagedAttentionConfig
+from .moe import HIPBailingMoE, HIPBailingMoeV2MLP
+
+__all__ = ["HIPBailingMoEAttention", "HIPBailingMoEDecoderLayer", "HIPPagedAttentionKVCache",
+           "PagedAttentionConfig", "HIPBailingMoE", "HIPBailingMoeV2MLP"]

@@ -1,0 +1,106 @@
+"""HIP-backed BailingMoeV2 decoder layer (the caller of the attention and MoE modules).
+
+Replaces ``TTNNBailingMoEDecoderLayer`` (modeling_bailing_moe_v2.py:345-483): ``from_torch``
+wraps ``input_layernorm`` / ``post_attention_layernorm``, converts ``attention`` and picks the
+MoE block or the dense MLP by ``first_k_dense_replace`` (modeling_bailing_moe_v2.py:374-401).
+Forward keeps the reference's residual structure
+  h1  = x + attention(rmsnorm(x))
+  out = h1 + mlp(rmsnorm(h1))
+with the residual adds fused into the kernels: the post-attention RMSNorm kernel also emits
+h1 = bf16(x + attn), and the MoE combine kernel adds h1 into its output.
+"""
+from __future__ import annotations
+
+import torch
+
+from .. import hip_ops
+from ..core.module import StatefulHIPModule
+from .attention import HIPBailingMoEAttention
+from .moe import HIPBailingMoE, HIPBailingMoeV2MLP
+
+
+def _is_sparse_moe(mlp) -> bool:
+    return hasattr(mlp, "experts") and hasattr(mlp, "gate")
+
+
+class HIPBailingMoEDecoderLayer(StatefulHIPModule):
+    def __init__(self):
+        super().__init__()
+        self.attention = None
+        self.mlp = None
+        self.is_dense_layer = False
+        self.hidden_size = None
+        self.eps = 1e-6
+        self._host = {}
+        self._dev = {}
+
+    @classmethod
+    def from_torch(cls, torch_layer):
+        new = cls()
+        new._fallback_torch_layer = torch_layer
+        ln1, ln2 = torch_layer.input_layernorm, torch_layer.post_attention_layernorm
+        new.hidden_size = ln1.weight.shape[0]
+        new.eps = float(getattr(ln1, "variance_epsilon", getattr(ln1, "eps", 1e-6)))
+        new._host = dict(ln1=ln1.weight, ln2=ln2.weight)
+        attn = torch_layer.attention
+        new.attention = (attn if isinstance(attn, HIPBailingMoEAttention)
+                         else HIPBailingMoEAttention.from_torch(attn))
+        mlp = torch_layer.mlp
+        if isinstance(mlp, (HIPBailingMoE, HIPBailingMoeV2MLP)):
+            new.mlp = mlp
+        elif _is_sparse_moe(mlp):
+            new.mlp = HIPBailingMoE.from_torch(mlp)
+        else:
+            new.mlp = HIPBailingMoeV2MLP.from_torch(mlp)
+        new.is_dense_layer = isinstance(new.mlp, HIPBailingMoeV2MLP)
+        return new
+
+    @classmethod
+    def from_modules(cls, attention: HIPBailingMoEAttention, mlp, input_layernorm_weight,
+                     post_attention_layernorm_weight, eps: float = 1e-6):
+        new = cls()
+        new.attention = attention
+        new.mlp = mlp
+        new.is_dense_layer = isinstance(mlp, HIPBailingMoeV2MLP)
+        new.hidden_size = input_layernorm_weight.shape[0]
+        new.eps = float(eps)
+        new._host = dict(ln1=input_layernorm_weight, ln2=post_attention_layernorm_weight)
+        return new
+
+    def preprocess_weights_impl(self):
+        self._host = {k: v.detach().to(torch.bfloat16).contiguous() for k, v in self._host.items()}
+        return super().preprocess_weights_impl()
+
+    def move_weights_to_device_impl(self):
+        self._dev = {k: v.to(self.device) for k, v in self._host.items()}
+        self._host = {}
+        return super().move_weights_to_device_impl()
+
+    def reset_trace_state(self):
+        # The only persistent mutation of a decode step is the KV-slot write of the child
+        # attention, which handles its own state; this layer keeps none between calls.
+        return None
+
+    def forward(self, hidden_states, attention_mask=None, position_ids=None,
+                past_key_value=None, output_attentions=False, output_router_logits=False,
+                use_cache=False, position_embeddings=None, cache_position=None,
+                past_key_values=None, **kwargs):
+        cache = past_key_values if past_key_values is not None else past_key_value
+        x = hidden_states
+        if x.dtype != torch.bfloat16:
+            x = x.to(torch.bfloat16)
+        x = x.contiguous()
+        xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
+        attn_out = self.attention(
+            xn, position_embeddings=position_embeddings, attention_mask=attention_mask,
+            past_key_values=cache, cache_position=cache_position, position_ids=position_ids)[0]
+        xn2, h1 = hip_ops.rmsnorm(attn_out.contiguous(), self._dev["ln2"], self.eps, residual=x)
+        out = self.mlp(xn2, residual=h1)
+        outputs = (out,)
+        if output_attentions:
+            outputs += (None,)
+        if use_cache:
+            outputs += (cache,)
+        if output_router_logits:
+            outputs += (None,)
+        return outputs
