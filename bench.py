@@ -42,6 +42,8 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-steps", type=int, default=5)
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches instead of replaying a captured HIP graph")
     return ap.parse_args()
 
 
@@ -144,19 +146,34 @@ def main():
     torch.cuda.synchronize()
     n_active = int(layer.mlp.last_route.n_segments.item()) - shape.num_shared_experts
 
-    # timed region: K eager steps
-    _log(f"timing {args.steps} steps ...")
+    run = step
+    graph = None
+    if not args.eager:
+        # capture one decode step (all of its launches, host logic included) as a HIP graph;
+        # positions, page table and workspaces are device buffers, so a replay is a full step
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        run = graph.replay
+        for _ in range(3):
+            run()
+        torch.cuda.synchronize()
+
+    # timed region: K steps
+    _log(f"timing {args.steps} steps ({'eager' if args.eager else 'graph replay'}) ...")
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record()
     for _ in range(args.steps):
-        step()
+        run()
     t_end.record()
     torch.cuda.synchronize()
     ms_per_step = t_start.elapsed_time(t_end) / args.steps
 
-    # per-kernel pass: same steps with HIP events around the dominant kernels
+    # per-kernel pass: the same steps launched eagerly with HIP events around the dominant
+    # kernels (on the stream they are launched on)
     timer = hip_ops.KernelTimer(["moe_gate_up", "moe_down", "paged_gqa_decode"])
     hip_ops.set_kernel_timer(timer)
     torch.cuda.synchronize()
@@ -195,6 +212,7 @@ def main():
             "global_batch": B,
             "context_tokens": int(ctx.context_lens.sum()),
             "active_experts": n_active,
+            "launch": "eager" if args.eager else "hip_graph",
         },
         "roofline": {
             "bound": "hbm",

@@ -49,12 +49,12 @@ int sym_abi_version(void);
  * RMSNorm over the last dim, bf16 in/out, fp32 statistics, with optional fused residual add.
  * Replaces the decoder layer's input_layernorm / post_attention_layernorm
  * (modeling_bailing_moe_v2.py:440-465; formula of DeepseekV2RMSNorm,
- * ttnn_normalization.py:54-68). If `residual` is non-NULL, s = bf16(x + residual) is written
- * to `residual_out` and normalized; otherwise s = x. out = bf16(weight * bf16(s * rsqrt(mean(s^2)+eps))).
- * rows >= 1, cols % 8 == 0, cols <= 16384.
+ * ttnn_normalization.py:54-68). If `residual` (bf16) is non-NULL, s = x + residual is written
+ * to `residual_out` in fp32 (the layer's residual stream) and normalized; otherwise s = x.
+ * out = bf16(weight * s * rsqrt(mean(s^2) + eps)). rows >= 1, cols % 8 == 0, cols <= 16384.
  */
 int sym_rmsnorm_bf16(const void* x, const void* residual, const void* weight, int rows, int cols,
-                     float eps, void* out, void* residual_out, void* stream);
+                     float eps, void* out, float* residual_out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Decode prologue: per-head QK RMSNorm, partial split-half RoPE, paged KV write.
@@ -177,10 +177,10 @@ int sym_moe_down(const void* h, int T, int H, int I, const int32_t* seg_expert,
  *   out[t] = bf16( sum_k topk_w[t,k] * y[inv_perm[t,k]]  (k ascending)
  *                  + (shared_row0 >= 0 ? y[shared_row0 + t] : 0)
  *                  + (residual ? residual[t] : 0) )
- *   out [T, H] bf16; residual [T, H] bf16 or NULL. H % 8 == 0.
+ *   out [T, H] bf16; residual [T, H] fp32 (the residual stream) or NULL. H % 8 == 0.
  */
 int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm, const float* topk_w, int T,
-                              int top_k, int H, int shared_row0, const void* residual, void* out,
+                              int top_k, int H, int shared_row0, const float* residual, void* out,
                               void* stream);
 
 #ifdef __cplusplus

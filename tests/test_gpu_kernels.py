@@ -40,7 +40,7 @@ def test_rmsnorm(device, rows, cols):
     ref = x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()
     _close(out, ref)
     out2, s = hip_ops.rmsnorm(x.to(device), w.to(device), 1e-6, residual=r.to(device))
-    s_ref = (x.float() + r.float()).bfloat16()
+    s_ref = x.float() + r.float()
     assert torch.equal(s.cpu(), s_ref)
     ref2 = s_ref.float() * torch.rsqrt(s_ref.float().pow(2).mean(-1, keepdim=True) + 1e-6) \
         * w.float()
@@ -176,12 +176,12 @@ def test_combine(device):
     T, E, H, I, K = 32, 256, 2048, 512, 8
     x, wgu, wd, res = _gemm_case(T, E, H, I, K, seed=5, device=device)
     _, y = hip_ops.moe_grouped_swiglu(x.to(device), res, wgu.to(device), wd.to(device))
-    resid = torch.randn(T, H, generator=torch.Generator().manual_seed(6)).bfloat16()
+    resid = torch.randn(T, H, generator=torch.Generator().manual_seed(6))
     out = hip_ops.moe_unpermute_combine(y, res, residual=resid.to(device))
     yc = y.cpu()
     inv = res.inv_perm.cpu().long()
     w = res.topk_w.cpu()
-    ref = (yc[inv] * w[..., None]).sum(1) + yc[T * K:T * K + T] + resid.float()
+    ref = (yc[inv] * w[..., None]).sum(1) + yc[T * K:T * K + T] + resid
     _close(out, ref, atol=1e-2, rtol=8e-3)
     out2 = hip_ops.moe_unpermute_combine(y, res)
     _close(out2, (yc[inv] * w[..., None]).sum(1) + yc[T * K:T * K + T], atol=1e-2, rtol=8e-3)

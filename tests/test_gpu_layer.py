@@ -163,3 +163,31 @@ def test_recipe_path_two_layer_model(device):
     assert rep["summary"]["runtime_successes"] >= 2
     assert rep["regressions"] == []
     assert rep["modules_swapped"]["by_class"].get("BailingMoeV2DecoderLayer") == 2
+
+
+def test_decode_step_graph_replay_matches_eager(device, ling_layer):
+    """A HIP-graph capture of the decode step replays to the eager result on every replay,
+    with eager work and synchronisations between replays."""
+    _, layer = ling_layer
+    ctx = paged_context(32, 128, 4096, block_size=32, num_kv_heads=4, seed=3, device=device)
+    cache = _hip_cache(ctx, device)
+    x = torch.randn(32, 1, 2048, generator=torch.Generator().manual_seed(4)).bfloat16().to(device)
+    pos = ctx.positions
+
+    def step():
+        return layer(x, past_key_values=cache, cache_position=pos)[0]
+
+    eager = step().clone()
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = step()
+    torch.cuda.synchronize()
+    for i in range(4):
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs"
+        _ = (x.float() * 2).sum()          # unrelated eager work between replays
+        torch.cuda.synchronize()

@@ -5,9 +5,10 @@
 // shared expert TTNNGlm4MoeMLP (ttnn_moe.py:656-675) added at ttnn_moe.py:1487-1490.
 //
 // Design for gfx950 at decode sizes (about 1-6 rows per routed expert, T rows for the shared
-// expert): the kernels are weight-streaming. One wave owns 16 output columns of one segment
-// (expert) and walks the full reduction dimension once, so every weight byte is read from HBM
-// exactly once per step. The 16 weight rows form the B operand of v_mfma_f32_16x16x32_bf16:
+// expert): the kernels are weight-streaming. A wave owns 16 output columns of one segment
+// (expert) and a range of the reduction dimension, so every weight byte is read from HBM
+// exactly once per step, and it issues its loads in batches so that enough bytes are in flight
+// to cover HBM latency even in the last partial round of workgroups. The 16 weight rows form the B operand of v_mfma_f32_16x16x32_bf16:
 // lane l streams 32 contiguous bytes of row (l % 16) per 64-wide K step (4 lanes cover 128
 // contiguous bytes of a row), and the rows of the segment (tokens, gathered through
 // sorted_tokens) form the A operand, padded to 16 with zero fragments. Both operands use the
@@ -26,24 +27,31 @@ __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
-template <int MT>
+// gate/up + SwiGLU. One workgroup per (segment, 16 columns of h); its 4 waves split the
+// reduction over H into contiguous K-step ranges, issue each range's weight and activation
+// loads in batches of U steps (16 bytes x 4U per lane of weights in flight), and reduce their
+// partial accumulators through LDS before the SwiGLU epilogue.
+template <int MT, int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
     const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
     const int32_t* __restrict__ seg_expert, const int32_t* __restrict__ seg_offset,
     const int32_t* __restrict__ seg_count, const int32_t* __restrict__ n_segments,
     const uint16_t* __restrict__ w_gu, uint16_t* __restrict__ h, int tiles_per_seg) {
+  __shared__ float s_red[4][MT][2][4][64];
   const int seg = blockIdx.x / tiles_per_seg;
   if (seg >= n_segments[0]) return;
   const int tile = blockIdx.x - seg * tiles_per_seg;
+  const int col0 = tile * 16;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int col0 = (tile * 4 + wave) * 16;
-  if (col0 >= I) return;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
   const int e = seg_expert[seg];
   const int row0 = seg_offset[seg];
   const int cnt = seg_count[seg];
-  const int r16 = lane & 15;
-  const int kq = lane >> 4;
+  const int nsteps = H >> 6;
+  const int s_beg = (wave * nsteps) >> 2;
+  const int s_end = ((wave + 1) * nsteps) >> 2;
 
   const uint16_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * 16;
   const uint16_t* wu = wg + (size_t)I * H;
@@ -63,15 +71,46 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
       const int tok = ok[mt] ? sorted_tokens[row0 + r] : 0;
       xr[mt] = x + (size_t)tok * H + kq * 16;
     }
-#pragma unroll 4
-    for (int k0 = 0; k0 < H; k0 += 64) {
-      const uint4 g0 = ld16(wg + k0), g1 = ld16(wg + k0 + 8);
-      const uint4 u0 = ld16(wu + k0), u1 = ld16(wu + k0 + 8);
+    int st = s_beg;
+    for (; st + U <= s_end; st += U) {
+      uint4 bg[U][2], bu[U][2];
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        const int k = (st + s) << 6;
+        bg[s][0] = ld16(wg + k);
+        bg[s][1] = ld16(wg + k + 8);
+        bu[s][0] = ld16(wu + k);
+        bu[s][1] = ld16(wu + k + 8);
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         if (mt < nmt) {
-          const uint4 a0 = ok[mt] ? ld16(xr[mt] + k0) : zero;
-          const uint4 a1 = ok[mt] ? ld16(xr[mt] + k0 + 8) : zero;
+          uint4 a[U][2];
+#pragma unroll
+          for (int s = 0; s < U; ++s) {
+            const int k = (st + s) << 6;
+            a[s][0] = ok[mt] ? ld16(xr[mt] + k) : zero;
+            a[s][1] = ok[mt] ? ld16(xr[mt] + k + 8) : zero;
+          }
+#pragma unroll
+          for (int s = 0; s < U; ++s) {
+            accg[mt] = mfma16x16x32(a[s][0], bg[s][0], accg[mt]);
+            accg[mt] = mfma16x16x32(a[s][1], bg[s][1], accg[mt]);
+            accu[mt] = mfma16x16x32(a[s][0], bu[s][0], accu[mt]);
+            accu[mt] = mfma16x16x32(a[s][1], bu[s][1], accu[mt]);
+          }
+        }
+      }
+    }
+    for (; st < s_end; ++st) {
+      const int k = st << 6;
+      const uint4 g0 = ld16(wg + k), g1 = ld16(wg + k + 8);
+      const uint4 u0 = ld16(wu + k), u1 = ld16(wu + k + 8);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (mt < nmt) {
+          const uint4 a0 = ok[mt] ? ld16(xr[mt] + k) : zero;
+          const uint4 a1 = ok[mt] ? ld16(xr[mt] + k + 8) : zero;
           accg[mt] = mfma16x16x32(a0, g0, accg[mt]);
           accg[mt] = mfma16x16x32(a1, g1, accg[mt]);
           accu[mt] = mfma16x16x32(a0, u0, accu[mt]);
@@ -84,20 +123,36 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
       if (mt < nmt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = mb + mt * 16 + kq * 4 + i;
-          if (r < cnt) {
-            const float g = accg[mt][i];
-            const float u = accu[mt][i];
-            const float hv = g / (1.0f + expf(-g)) * u;
-            h[(size_t)(row0 + r) * I + col0 + r16] = f32_to_bf16(hv);
-          }
+          s_red[wave][mt][0][i][lane] = accg[mt][i];
+          s_red[wave][mt][1][i][lane] = accu[mt][i];
         }
       }
     }
+    __syncthreads();
+    {
+      // thread -> element i of lane l's 16x16 fragment: row 4*(l/16)+i, column l%16
+      const int l = threadIdx.x & 63;
+      const int i = threadIdx.x >> 6;
+      const int row = 4 * (l >> 4) + i;
+      for (int mt = 0; mt < nmt; ++mt) {
+        const float g = (s_red[0][mt][0][i][l] + s_red[1][mt][0][i][l]) +
+                        (s_red[2][mt][0][i][l] + s_red[3][mt][0][i][l]);
+        const float u = (s_red[0][mt][1][i][l] + s_red[1][mt][1][i][l]) +
+                        (s_red[2][mt][1][i][l] + s_red[3][mt][1][i][l]);
+        const int r = mb + mt * 16 + row;
+        if (r < cnt) {
+          const float hv = g / (1.0f + expf(-g)) * u;
+          h[(size_t)(row0 + r) * I + col0 + (l & 15)] = f32_to_bf16(hv);
+        }
+      }
+    }
+    __syncthreads();
   }
 }
 
-template <int MT>
+// down projection. One wave per (segment, 16 output columns) over the full reduction dim I,
+// weight loads issued in batches of U K-steps.
+template <int MT, int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
     const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
     const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
@@ -115,6 +170,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
   const int cnt = seg_count[seg];
   const int r16 = lane & 15;
   const int kq = lane >> 4;
+  const int nsteps = I >> 6;
 
   const uint16_t* wd = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 16;
   const uint4 zero = make_uint4(0, 0, 0, 0);
@@ -131,14 +187,41 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
       ok[mt] = r < cnt;
       hr[mt] = hbuf + (size_t)(row0 + (ok[mt] ? r : 0)) * I + kq * 16;
     }
-#pragma unroll 8
-    for (int k0 = 0; k0 < I; k0 += 64) {
-      const uint4 b0 = ld16(wd + k0), b1 = ld16(wd + k0 + 8);
+    int st = 0;
+    for (; st + U <= nsteps; st += U) {
+      uint4 b[U][2];
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        const int k = (st + s) << 6;
+        b[s][0] = ld16(wd + k);
+        b[s][1] = ld16(wd + k + 8);
+      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         if (mt < nmt) {
-          const uint4 a0 = ok[mt] ? ld16(hr[mt] + k0) : zero;
-          const uint4 a1 = ok[mt] ? ld16(hr[mt] + k0 + 8) : zero;
+          uint4 a[U][2];
+#pragma unroll
+          for (int s = 0; s < U; ++s) {
+            const int k = (st + s) << 6;
+            a[s][0] = ok[mt] ? ld16(hr[mt] + k) : zero;
+            a[s][1] = ok[mt] ? ld16(hr[mt] + k + 8) : zero;
+          }
+#pragma unroll
+          for (int s = 0; s < U; ++s) {
+            acc[mt] = mfma16x16x32(a[s][0], b[s][0], acc[mt]);
+            acc[mt] = mfma16x16x32(a[s][1], b[s][1], acc[mt]);
+          }
+        }
+      }
+    }
+    for (; st < nsteps; ++st) {
+      const int k = st << 6;
+      const uint4 b0 = ld16(wd + k), b1 = ld16(wd + k + 8);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        if (mt < nmt) {
+          const uint4 a0 = ok[mt] ? ld16(hr[mt] + k) : zero;
+          const uint4 a1 = ok[mt] ? ld16(hr[mt] + k + 8) : zero;
           acc[mt] = mfma16x16x32(a0, b0, acc[mt]);
           acc[mt] = mfma16x16x32(a1, b1, acc[mt]);
         }
@@ -160,7 +243,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const float* __restrict__ y, const int32_t* __restrict__ inv_perm,
     const float* __restrict__ topk_w, int K, int H, int shared_row0,
-    const uint16_t* __restrict__ residual, uint16_t* __restrict__ out) {
+    const float* __restrict__ residual, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
   for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
     float acc[8];
@@ -181,10 +264,10 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
       acc[4] += f1.x; acc[5] += f1.y; acc[6] += f1.z; acc[7] += f1.w;
     }
     if (residual) {
-      float r[8];
-      unpack8(*reinterpret_cast<const uint4*>(residual + (size_t)t * H + c), r);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += r[i];
+      const float4* rp = reinterpret_cast<const float4*>(residual + (size_t)t * H + c);
+      const float4 r0 = rp[0], r1 = rp[1];
+      acc[0] += r0.x; acc[1] += r0.y; acc[2] += r0.z; acc[3] += r0.w;
+      acc[4] += r1.x; acc[5] += r1.y; acc[6] += r1.z; acc[7] += r1.w;
     }
     uint4 o;
     o.x = pack_bf16x2(acc[0], acc[1]);
@@ -221,8 +304,8 @@ extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t
                   w_gate_up && h,
               SYM_ERR_INVALID, "moe_gate_up: null pointer argument");
   (void)hipGetLastError();
-  const int tiles = (I + kColsPerWG - 1) / kColsPerWG;
-  hipLaunchKernelGGL(moe_gate_up_kernel<4>, dim3(max_segments * tiles), dim3(kGemmThreads), 0,
+  const int tiles = I / 16;
+  hipLaunchKernelGGL((moe_gate_up_kernel<4, 4>), dim3(max_segments * tiles), dim3(kGemmThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)x, H, I, sorted_tokens, seg_expert,
                      seg_offset, seg_count, n_segments, (const uint16_t*)w_gate_up, (uint16_t*)h,
                      tiles);
@@ -240,7 +323,7 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
               SYM_ERR_INVALID, "moe_down: null pointer argument");
   (void)hipGetLastError();
   const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
-  hipLaunchKernelGGL(moe_down_kernel<4>, dim3(max_segments * tiles), dim3(kGemmThreads), 0,
+  hipLaunchKernelGGL((moe_down_kernel<4, 8>), dim3(max_segments * tiles), dim3(kGemmThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)h, H, I, seg_expert, seg_offset,
                      seg_count, n_segments, (const uint16_t*)w_down, y, tiles);
   return sym_host::check_launch("moe_down_kernel");
@@ -261,7 +344,7 @@ extern "C" int sym_moe_grouped_swiglu(const void* x, int T, int H, int I,
 
 extern "C" int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm,
                                          const float* topk_w, int T, int top_k, int H,
-                                         int shared_row0, const void* residual, void* out,
+                                         int shared_row0, const float* residual, void* out,
                                          void* stream) {
   SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "moe_unpermute_combine: T=%d < 0", T);
   if (T == 0) return SYM_OK;
@@ -273,6 +356,6 @@ extern "C" int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm
               top_k);
   (void)hipGetLastError();
   hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, y, inv_perm,
-                     topk_w, top_k, H, shared_row0, (const uint16_t*)residual, (uint16_t*)out);
+                     topk_w, top_k, H, shared_row0, residual, (uint16_t*)out);
   return sym_host::check_launch("moe_combine_kernel");
 }

@@ -66,9 +66,8 @@ __global__ __launch_bounds__(256) void attn_decode_prologue_kernel(
         const float ss = wave_sum(x0 * x0 + x1 * x1);
         const float r = rsqrtf(ss * (1.0f / kHeadDim) + eps);
         const uint16_t* w = is_q ? qn_w : kn_w;
-        // HF RMSNorm in a bf16 model: weight * (x * rsqrt(var + eps)).to(bf16)
-        x0 = bf16_to_f32(f32_to_bf16(x0 * r)) * bf16_to_f32(w[lane]);
-        x1 = bf16_to_f32(f32_to_bf16(x1 * r)) * bf16_to_f32(w[lane + 64]);
+        x0 = x0 * r * bf16_to_f32(w[lane]);
+        x1 = x1 * r * bf16_to_f32(w[lane + 64]);
       }
       if (rope_ok && rd > 0) {
         // element i lives in lane i % 64, slot i / 64
@@ -203,25 +202,46 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) qr[h][i] = s_q[h][sub * 8 + i];
 
-  // ---- scores ----
-#pragma unroll 4
+  // Issue every K and V load of this wave's 64 tokens up front (16 + 16 loads of 16 bytes per
+  // lane); V arrives while the scores and the softmax statistics are computed.
+  const uint4 zero = make_uint4(0, 0, 0, 0);
+  uint4 kreg[16], vreg[16];
+#pragma unroll
   for (int it = 0; it < 16; ++it) {
     const int tl = wave * 64 + it * 4 + tq;
     const int t = t0 + tl;
     const int phys = s_bt[tl];
+    const size_t off = phys >= 0
+        ? (((size_t)phys * Hkv + g) * block_size + (t - (t / block_size) * block_size)) * D +
+              sub * 8
+        : 0;
+    kreg[it] = phys >= 0 ? *reinterpret_cast<const uint4*>(k_pool + off) : zero;
+  }
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+    const int tl = wave * 64 + it * 4 + tq;
+    const int t = t0 + tl;
+    const int phys = s_bt[tl];
+    const size_t off = phys >= 0
+        ? (((size_t)phys * Hkv + g) * block_size + (t - (t / block_size) * block_size)) * D +
+              sub * 8
+        : 0;
+    vreg[it] = phys >= 0 ? *reinterpret_cast<const uint4*>(v_pool + off) : zero;
+  }
+
+  // ---- scores ----
+#pragma unroll
+  for (int it = 0; it < 16; ++it) {
+    const int tl = wave * 64 + it * 4 + tq;
+    float kf[8];
+    unpack8(kreg[it], kf);
     float dot[G];
 #pragma unroll
-    for (int h = 0; h < G; ++h) dot[h] = 0.f;
-    if (phys >= 0) {
-      const int off = t - (t / block_size) * block_size;
-      const uint4 kv = *reinterpret_cast<const uint4*>(
-          k_pool + (((size_t)phys * Hkv + g) * block_size + off) * D + sub * 8);
-      float kf[8];
-      unpack8(kv, kf);
+    for (int h = 0; h < G; ++h) {
+      float d = 0.f;
 #pragma unroll
-      for (int h = 0; h < G; ++h)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) dot[h] = fmaf(qr[h][i], kf[i], dot[h]);
+      for (int i = 0; i < 8; ++i) d = fmaf(qr[h][i], kf[i], d);
+      dot[h] = d;
     }
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -229,8 +249,9 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
       for (int o = 8; o > 0; o >>= 1) dot[h] += __shfl_xor(dot[h], o);
     }
     if (sub == 0) {
+      const bool valid = s_bt[tl] >= 0;
 #pragma unroll
-      for (int h = 0; h < G; ++h) s_p[h][tl] = phys >= 0 ? dot[h] : -INFINITY;
+      for (int h = 0; h < G; ++h) s_p[h][tl] = valid ? dot[h] : -INFINITY;
     }
   }
   __syncthreads();
@@ -263,23 +284,16 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
   for (int h = 0; h < G; ++h)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
-#pragma unroll 4
+#pragma unroll
   for (int it = 0; it < 16; ++it) {
     const int tl = wave * 64 + it * 4 + tq;
-    const int t = t0 + tl;
-    const int phys = s_bt[tl];
-    if (phys >= 0) {
-      const int off = t - (t / block_size) * block_size;
-      const uint4 vv = *reinterpret_cast<const uint4*>(
-          v_pool + (((size_t)phys * Hkv + g) * block_size + off) * D + sub * 8);
-      float vf[8];
-      unpack8(vv, vf);
+    float vf[8];
+    unpack8(vreg[it], vf);
 #pragma unroll
-      for (int h = 0; h < G; ++h) {
-        const float p = s_p[h][tl];
+    for (int h = 0; h < G; ++h) {
+      const float p = s_p[h][tl];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
-      }
+      for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
     }
   }
 #pragma unroll

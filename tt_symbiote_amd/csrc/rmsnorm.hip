@@ -1,9 +1,10 @@
-// Row RMSNorm with an optional fused residual add, bf16 in/out, fp32 statistics.
+// Row RMSNorm with an optional fused residual add, bf16 in, fp32 statistics.
 // Reference: the decoder layer's input_layernorm / post_attention_layernorm and residual adds
 // (modeling_bailing_moe_v2.py:440-468), RMSNorm formula of DeepseekV2RMSNorm
-// (ttnn_normalization.py:54-68) evaluated the way a bf16 HF module does:
-//   s   = bf16(x + residual)              (the residual stream is kept in bf16)
-//   out = bf16(weight * bf16(s * rsqrt(mean(s^2) + eps)))
+// (ttnn_normalization.py:54-68):
+//   s   = x + residual                    (fp32; written to residual_out as the layer's
+//                                          residual stream, no intermediate bf16 rounding)
+//   out = bf16(weight * s * rsqrt(mean(s^2) + eps))
 // One workgroup per row; each thread owns 8 consecutive columns per pass (one 16-byte load).
 #include "common.h"
 
@@ -15,7 +16,7 @@ constexpr int kNormMaxPasses = 8;  // cols <= 256 * 8 * 8 = 16384
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ w, int cols, float eps, uint16_t* __restrict__ out,
-    uint16_t* __restrict__ res_out) {
+    float* __restrict__ res_out) {
   __shared__ float s_part[kNormThreads / 64];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
@@ -30,13 +31,11 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
       if (res) {
         float r[8];
         unpack8(*reinterpret_cast<const uint4*>(res + base + c), r);
-        uint4 o;
-        o.x = pack_bf16x2(v[p][0] + r[0], v[p][1] + r[1]);
-        o.y = pack_bf16x2(v[p][2] + r[2], v[p][3] + r[3]);
-        o.z = pack_bf16x2(v[p][4] + r[4], v[p][5] + r[5]);
-        o.w = pack_bf16x2(v[p][6] + r[6], v[p][7] + r[7]);
-        *reinterpret_cast<uint4*>(res_out + base + c) = o;
-        unpack8(o, v[p]);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[p][i] += r[i];
+        float4* dst = reinterpret_cast<float4*>(res_out + base + c);
+        dst[0] = make_float4(v[p][0], v[p][1], v[p][2], v[p][3]);
+        dst[1] = make_float4(v[p][4], v[p][5], v[p][6], v[p][7]);
       }
 #pragma unroll
       for (int i = 0; i < 8; ++i) ss = fmaf(v[p][i], v[p][i], ss);
@@ -57,7 +56,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
       unpack8(*reinterpret_cast<const uint4*>(w + c), wf);
       float o[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = bf16_to_f32(f32_to_bf16(v[p][i] * r)) * wf[i];
+      for (int i = 0; i < 8; ++i) o[i] = v[p][i] * r * wf[i];
       uint4 q;
       q.x = pack_bf16x2(o[0], o[1]);
       q.y = pack_bf16x2(o[2], o[3]);
@@ -73,7 +72,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
 using namespace sym;
 
 extern "C" int sym_rmsnorm_bf16(const void* x, const void* residual, const void* weight, int rows,
-                                int cols, float eps, void* out, void* residual_out, void* stream) {
+                                int cols, float eps, void* out, float* residual_out, void* stream) {
   SYM_REQUIRE(rows >= 0, SYM_ERR_INVALID, "rmsnorm: rows=%d < 0", rows);
   if (rows == 0) return SYM_OK;
   SYM_REQUIRE(x && weight && out, SYM_ERR_INVALID, "rmsnorm: null pointer argument");
@@ -85,6 +84,6 @@ extern "C" int sym_rmsnorm_bf16(const void* x, const void* residual, const void*
   (void)hipGetLastError();
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)residual, (const uint16_t*)weight, cols,
-                     eps, (uint16_t*)out, (uint16_t*)residual_out);
+                     eps, (uint16_t*)out, residual_out);
   return sym_host::check_launch("rmsnorm_kernel");
 }

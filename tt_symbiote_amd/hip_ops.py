@@ -92,7 +92,8 @@ def _check_shape(t: torch.Tensor, name: str, shape: tuple) -> None:
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
             residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
             residual_out: Optional[torch.Tensor] = None):
-    """RMSNorm over the last dim (bf16). With ``residual``: returns (normed, x + residual)."""
+    """RMSNorm over the last dim (bf16 out). With ``residual`` (bf16): returns
+    (normed, x + residual) with the sum in fp32 (the layer's residual stream)."""
     _check(x, "x", torch.bfloat16)
     cols = x.shape[-1]
     rows = x.numel() // cols if cols else 0
@@ -106,8 +107,8 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
         _check(residual, "residual", torch.bfloat16, x.device)
         _check_shape(residual, "residual", tuple(x.shape))
         if residual_out is None:
-            residual_out = torch.empty_like(x)
-        _check(residual_out, "residual_out", torch.bfloat16, x.device)
+            residual_out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+        _check(residual_out, "residual_out", torch.float32, x.device)
         _check_shape(residual_out, "residual_out", tuple(x.shape))
     _lib.call("sym_rmsnorm_bf16", _ptr(x), _ptr(residual), _ptr(weight), rows, cols, float(eps),
               _ptr(out), _ptr(residual_out), _stream())
@@ -294,7 +295,7 @@ def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,
         seg_expert=torch.empty(E + 1, **i32),
         seg_offset=torch.empty(E + 1, **i32),
         seg_count=torch.empty(E + 1, **i32),
-        n_segments=torch.zeros(1, **i32),
+        n_segments=torch.empty(1, **i32),
         with_shared=bool(with_shared),
     )
     if T == 0:
@@ -357,14 +358,14 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up: torch.Ten
 def moe_unpermute_combine(y: torch.Tensor, route: RouteResult,
                           residual: Optional[torch.Tensor] = None,
                           out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """out[t] = sum_k w[t,k] y[inv[t,k]] (+ shared row) (+ residual[t]), bf16 [T, H]."""
+    """out[t] = sum_k w[t,k] y[inv[t,k]] (+ shared row) (+ residual[t], fp32), bf16 [T, H]."""
     _check(y, "y", torch.float32)
     T, K = route.topk_idx.shape
     H = y.shape[1]
     dev = y.device
     _check_shape(y, "y", (route.rows, H))
     if residual is not None:
-        _check(residual, "residual", torch.bfloat16, dev)
+        _check(residual, "residual", torch.float32, dev)
         _check_shape(residual, "residual", (T, H))
     if out is None:
         out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)

@@ -7,7 +7,8 @@ Forward keeps the reference's residual structure
   h1  = x + attention(rmsnorm(x))
   out = h1 + mlp(rmsnorm(h1))
 with the residual adds fused into the kernels: the post-attention RMSNorm kernel also emits
-h1 = bf16(x + attn), and the MoE combine kernel adds h1 into its output.
+h1 = x + attn in fp32 (the residual stream inside the layer is never rounded), and the MoE
+combine kernel adds h1 into its output, which is rounded to bf16 once.
 """
 from __future__ import annotations
 

@@ -142,6 +142,7 @@ class HIPBailingMoE(StatelessHIPModule):
             with_shared=self.has_shared)
 
     def forward(self, hidden_states: torch.Tensor, residual: torch.Tensor = None) -> torch.Tensor:
+        """MoE output (bf16); with ``residual`` the result is residual + MoE(x) (one rounding)."""
         shape = hidden_states.shape
         H = shape[-1]
         x = hidden_states.reshape(-1, H)
@@ -150,7 +151,7 @@ class HIPBailingMoE(StatelessHIPModule):
         x = x.contiguous()
         res = None
         if residual is not None:
-            res = residual.reshape(-1, H).to(torch.bfloat16).contiguous()
+            res = residual.reshape(-1, H).to(torch.float32).contiguous()
         route = self.route(x)
         if self.keep_last_route:
             self.last_route = route
@@ -213,5 +214,5 @@ class HIPBailingMoeV2MLP(StatelessHIPModule):
         x = hidden_states.reshape(-1, H).to(torch.bfloat16).contiguous()
         route = self._route(x.shape[0])
         _, y = hip_ops.moe_grouped_swiglu(x, route, self._dev["gate_up"], self._dev["down"])
-        res = None if residual is None else residual.reshape(-1, H).to(torch.bfloat16).contiguous()
+        res = None if residual is None else residual.reshape(-1, H).to(torch.float32).contiguous()
         return hip_ops.moe_unpermute_combine(y, route, residual=res).view(shape)
