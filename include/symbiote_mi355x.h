@@ -57,6 +57,15 @@ int sym_rmsnorm_bf16(const void* x, const void* residual, const void* weight, in
                      float eps, void* out, float* residual_out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Skinny GEMM for the decode projections: out[M, N] = x[M, K] . w[N, K]^T (+ bias[N]).
+ * Replaces the query_key_value and dense linears of TTNNBailingMoEAttention
+ * (ttnn_attention.py:2324, 2459). x, w, bias bf16; fp32 accumulation; out bf16, or fp32 when
+ * out_fp32 != 0. N % 16 == 0, K % 64 == 0; bias may be NULL.
+ */
+int sym_linear_bf16(const void* x, const void* w, const void* bias, int M, int N, int K,
+                    void* out, int out_fp32, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Decode prologue: per-head QK RMSNorm, partial split-half RoPE, paged KV write.
  * Replaces TTNNBailingMoEAttention._forward_decode_paged's split / _apply_qk_norm / RoPE /
  * paged_update_on_device sequence (ttnn_attention.py:2329-2431).
@@ -113,10 +122,23 @@ int sym_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                          size_t workspace_bytes, void* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Router logits in fp32 (fp32 MFMA): replaces the fp32 gate GEMV of TTNNMoE.forward
+ * (ttnn_moe.py:1438-1455; gate weight kept fp32, ttnn_moe.py:1542).
+ *   x [T, H] bf16 (upcast exactly); w [E, H] fp32;
+ *   parts [4, T, E] fp32: parts[q] = x[:, Hq] . w[:, Hq]^T over the q-th quarter of H.
+ * The logits are ((parts[0] + parts[1]) + parts[2]) + parts[3], summed in that order by
+ * sym_moe_route_permute (n_logit_parts = 4), so routing does not depend on launch order.
+ * H % 256 == 0, E % 16 == 0.
+ */
+int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E, float* parts,
+                          void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Fused MoE router + top-k + permute.
  * Replaces TTNNMoERouterDecode.forward (ttnn_moe.py:891-1024; torch form
  * Glm4MoeRouteTokenToExperts, ttnn_moe.py:413-436) and the dispatch/remap of
  * TTNNExperts.forward (ttnn_moe.py:1225-1245):
+ *   logits = sum of the n_logit_parts arrays [n_logit_parts, T, E] (left to right);
  *   s = sigmoid(logits); c = s + bias; group score = sum of the two largest c in each group of
  *   E/n_group experts; keep the topk_group best groups; experts of other groups score 0.0;
  *   topk_idx = top_k experts by that score (ties: lower index first);
@@ -127,15 +149,16 @@ int sym_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
  * token in order for the shared expert (stack slot E).
  * Segment list for the grouped GEMM: seg_expert/seg_offset/seg_count[0 .. *n_segments) list
  * the experts with at least one row in ascending order, then the shared expert.
- *   logits [T, E] fp32; bias [E] fp32; E in {64,128,256,512}; E/n_group >= 2 and
- *   (E/n_group) % (E/64) == 0; top_k <= 32; topk_group <= n_group.
+ *   bias [E] fp32; E in {64,128,256,512}; E/n_group >= 2 and (E/n_group) % (E/64) == 0;
+ *   top_k <= 32; topk_group <= n_group; 1 <= n_logit_parts <= 16.
  * Output sizes: topk_idx/topk_w/inv_perm [T*top_k]; expert_counts [E]; expert_offsets [E+1];
  * sorted_tokens [T*top_k + T]; seg_* [E+1]; n_segments [1].
+ * One launch when T <= 64 (routing and permute in one workgroup), two otherwise.
  */
 size_t sym_moe_route_workspace_bytes(int T, int E);
-int sym_moe_route_permute(const float* logits, const float* bias, int T, int E, int n_group,
-                          int topk_group, int top_k, float routed_scale, int renormalize,
-                          int with_shared, int32_t* topk_idx, float* topk_w,
+int sym_moe_route_permute(const float* logits, int n_logit_parts, const float* bias, int T, int E,
+                          int n_group, int topk_group, int top_k, float routed_scale,
+                          int renormalize, int with_shared, int32_t* topk_idx, float* topk_w,
                           int32_t* expert_counts, int32_t* expert_offsets,
                           int32_t* sorted_tokens, int32_t* inv_perm, int32_t* seg_expert,
                           int32_t* seg_offset, int32_t* seg_count, int32_t* n_segments,
@@ -151,7 +174,7 @@ int sym_moe_route_permute(const float* logits, const float* bias, int T, int E, 
  *     y[r] = h[r] . Wd[e]^T                                    (fp32)
  *   x [T, H] bf16; w_gate_up [E+1, 2I, H] bf16; w_down [E+1, H, I] bf16;
  *   h [rows, I] bf16 and y [rows, H] fp32 with rows = T*top_k (+T with a shared expert).
- * The segment list is read on the device; no host synchronization. H % 64 == 0, I % 64 == 0.
+ * The segment list is read on the device; no host synchronization. H % 128 == 0, I % 64 == 0.
  * max_segments: the length of the segment list buffers (E+1).
  */
 int sym_moe_grouped_swiglu(const void* x, int T, int H, int I, const int32_t* sorted_tokens,

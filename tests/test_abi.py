@@ -65,7 +65,7 @@ def test_decode_rejects_group_size_and_workspace():
 
 
 def test_route_rejects_bad_configs():
-    args = lambda T, E, ng, tg, k: (FAKE, FAKE, T, E, ng, tg, k, 1.0, 1, 1, FAKE, FAKE, FAKE,
+    args = lambda T, E, ng, tg, k: (FAKE, 1, FAKE, T, E, ng, tg, k, 1.0, 1, 1, FAKE, FAKE, FAKE,
                                     FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 20, None)
     assert _call("sym_moe_route_permute", *args(4, 96, 8, 4, 8))[0] == 2      # E not supported
     assert _call("sym_moe_route_permute", *args(4, 256, 7, 4, 8))[0] == 1     # n_group
@@ -73,8 +73,11 @@ def test_route_rejects_bad_configs():
     assert _call("sym_moe_route_permute", *args(4, 256, 8, 4, 33))[0] == 1    # top_k
     assert _call("sym_moe_route_permute", *args(4, 64, 64, 4, 2))[0] == 2     # group of 1
     assert _call("sym_moe_route_permute", *args(4, 64, 8, 1, 9))[0] == 1      # k > kept experts
-    rc, msg = _call("sym_moe_route_permute", *args(4, 256, 8, 4, 8)[:21], 8, None)
+    rc, msg = _call("sym_moe_route_permute", *args(4, 256, 8, 4, 8)[:22], 8, None)
     assert rc == 3 and "workspace" in msg
+    bad_parts = list(args(4, 256, 8, 4, 8))
+    bad_parts[1] = 0
+    assert _call("sym_moe_route_permute", *bad_parts)[0] == 1
     assert _call("sym_moe_route_permute", *args(0, 256, 8, 4, 8))[0] == 0     # empty batch
 
 
@@ -99,3 +102,13 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
     with pytest.raises(_lib.HipExtensionMissing):
         _lib.load()
+
+
+def test_linear_and_router_reject_bad_shapes():
+    assert _call("sym_linear_bf16", FAKE, FAKE, None, 4, 100, 2048, FAKE, 0, None)[0] == 2
+    assert _call("sym_linear_bf16", FAKE, FAKE, None, 4, 128, 100, FAKE, 0, None)[0] == 2
+    assert _call("sym_linear_bf16", None, FAKE, None, 4, 128, 128, FAKE, 0, None)[0] == 1
+    assert _call("sym_linear_bf16", FAKE, FAKE, None, 0, 128, 128, FAKE, 0, None)[0] == 0
+    assert _call("sym_moe_router_logits", FAKE, FAKE, 4, 2000, 256, FAKE, None)[0] == 2
+    assert _call("sym_moe_router_logits", FAKE, FAKE, 4, 2048, 250, FAKE, None)[0] == 2
+    assert _call("sym_moe_router_logits", FAKE, None, 4, 2048, 256, FAKE, None)[0] == 1

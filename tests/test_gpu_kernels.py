@@ -127,6 +127,58 @@ def test_route_deterministic_across_runs(device):
         assert torch.equal(getattr(a, name), getattr(b, name))
 
 
+def test_route_from_logit_parts_bit_exact(device):
+    """Four partial logit arrays are summed left to right inside the route kernel; the oracle
+    routes the same float32 sum."""
+    g = torch.Generator().manual_seed(21)
+    parts = (torch.randn(4, 48, 256, generator=g) * 0.7).float()
+    bias = (torch.randn(256, generator=g) * 0.01).float()
+    kw = dict(n_group=8, topk_group=4, top_k=8, routed_scale=2.5)
+    res = hip_ops.moe_route_permute(parts.to(device), bias.to(device), **kw)
+    p = parts.numpy()
+    logits = ((p[0] + p[1]) + p[2]) + p[3]
+    idx_ref, w_ref = R.route_c(logits, bias.numpy(), **kw)
+    assert np.array_equal(res.topk_idx.cpu().numpy(), idx_ref)
+    assert np.array_equal(res.topk_w.cpu().numpy(), w_ref)
+
+
+@pytest.mark.parametrize("T,H,E", [(1, 2048, 256), (32, 2048, 256), (40, 512, 64), (128, 2048, 512)])
+def test_router_logits(device, T, H, E):
+    g = torch.Generator().manual_seed(T + E)
+    x = torch.randn(T, H, generator=g).bfloat16()
+    w = (torch.randn(E, H, generator=g) * 0.02).float()
+    parts = hip_ops.moe_router_logits(x.to(device), w.to(device))
+    assert parts.shape == (4, T, E)
+    ref = x.double() @ w.double().T
+    got = parts.cpu().double().sum(0)
+    torch.testing.assert_close(got, ref, rtol=1e-5, atol=1e-5)
+    # each part is the product over its quarter of H
+    q = H // 4
+    ref1 = x[:, q:2 * q].double() @ w[:, q:2 * q].double().T
+    torch.testing.assert_close(parts[1].cpu().double(), ref1, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("M,N,K,bias,out_dtype", [
+    (32, 3072, 2048, False, torch.bfloat16),
+    (32, 2048, 2048, True, torch.bfloat16),
+    (1, 256, 512, False, torch.float32),
+    (70, 128, 192, True, torch.float32),
+])
+def test_linear(device, M, N, K, bias, out_dtype):
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(N, generator=g) * 0.1).bfloat16() if bias else None
+    out = hip_ops.linear(x.to(device), w.to(device), None if b is None else b.to(device),
+                         out_dtype=out_dtype)
+    ref = x.float() @ w.float().T + (b.float() if b is not None else 0.0)
+    assert out.dtype == out_dtype
+    if out_dtype == torch.float32:
+        torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=1e-4)
+    else:
+        _close(out, ref, atol=2e-3, rtol=8e-3)
+
+
 # ------------------------------------------------------------------------------- grouped GEMM
 def _gemm_case(T, E, H, I, top_k, seed, device, with_shared=True, skew=False):
     g = torch.Generator().manual_seed(seed)

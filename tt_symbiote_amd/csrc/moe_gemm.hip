@@ -11,7 +11,7 @@
 // to cover HBM latency even in the last partial round of workgroups. The 16 weight rows form the B operand of v_mfma_f32_16x16x32_bf16:
 // lane l streams 32 contiguous bytes of row (l % 16) per 64-wide K step (4 lanes cover 128
 // contiguous bytes of a row), and the rows of the segment (tokens, gathered through
-// sorted_tokens) form the A operand, padded to 16 with zero fragments. Both operands use the
+// sorted_tokens) form the A operand; rows past the segment repeat its last row and their outputs are dropped. Both operands use the
 // same lane -> K mapping, so the K order inside a step is free to follow memory order. Up to
 // MT row tiles (16 rows each) are accumulated per pass over the weights.
 // Segments live on the device: workgroups past *n_segments exit at once, so the grid is sized
@@ -21,16 +21,16 @@
 namespace sym {
 
 constexpr int kGemmThreads = 256;  // 4 waves; each wave owns 16 output columns
-constexpr int kColsPerWG = 64;
+constexpr int kColsPerWG = 128;  // down projection: 4 waves x 32 columns
 
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
 // gate/up + SwiGLU. One workgroup per (segment, 16 columns of h); its 4 waves split the
-// reduction over H into contiguous K-step ranges, issue each range's weight and activation
-// loads in batches of U steps (16 bytes x 4U per lane of weights in flight), and reduce their
-// partial accumulators through LDS before the SwiGLU epilogue.
+// reduction over H into contiguous K-step ranges. Each batch of U K-steps issues all of its
+// weight loads (gate and up rows) and activation loads (MT row tiles) before the MFMAs; the
+// waves' partial accumulators reduce through LDS before the SwiGLU epilogue.
 template <int MT, int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
     const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
@@ -55,25 +55,22 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
 
   const uint16_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * 16;
   const uint16_t* wu = wg + (size_t)I * H;
-  const uint4 zero = make_uint4(0, 0, 0, 0);
 
   for (int mb = 0; mb < cnt; mb += 16 * MT) {
     const int nmt = min(MT, (cnt - mb + 15) >> 4);
     floatx4 accg[MT], accu[MT];
     const uint16_t* xr[MT];
-    bool ok[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       accg[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
       accu[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const int r = mb + mt * 16 + r16;
-      ok[mt] = r < cnt;
-      const int tok = ok[mt] ? sorted_tokens[row0 + r] : 0;
-      xr[mt] = x + (size_t)tok * H + kq * 16;
+      // rows past the segment read its last row (in bounds, finite); their outputs are dropped
+      const int r = min(mb + mt * 16 + r16, cnt - 1);
+      xr[mt] = x + (size_t)sorted_tokens[row0 + r] * H + kq * 16;
     }
     int st = s_beg;
     for (; st + U <= s_end; st += U) {
-      uint4 bg[U][2], bu[U][2];
+      uint4 bg[U][2], bu[U][2], a[MT][U][2];
 #pragma unroll
       for (int s = 0; s < U; ++s) {
         const int k = (st + s) << 6;
@@ -83,21 +80,22 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
         bu[s][1] = ld16(wu + k + 8);
       }
 #pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          const int k = (st + s) << 6;
+          a[mt][s][0] = ld16(xr[mt] + k);
+          a[mt][s][1] = ld16(xr[mt] + k + 8);
+        }
+#pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         if (mt < nmt) {
-          uint4 a[U][2];
 #pragma unroll
           for (int s = 0; s < U; ++s) {
-            const int k = (st + s) << 6;
-            a[s][0] = ok[mt] ? ld16(xr[mt] + k) : zero;
-            a[s][1] = ok[mt] ? ld16(xr[mt] + k + 8) : zero;
-          }
-#pragma unroll
-          for (int s = 0; s < U; ++s) {
-            accg[mt] = mfma16x16x32(a[s][0], bg[s][0], accg[mt]);
-            accg[mt] = mfma16x16x32(a[s][1], bg[s][1], accg[mt]);
-            accu[mt] = mfma16x16x32(a[s][0], bu[s][0], accu[mt]);
-            accu[mt] = mfma16x16x32(a[s][1], bu[s][1], accu[mt]);
+            accg[mt] = mfma16x16x32(a[mt][s][0], bg[s][0], accg[mt]);
+            accg[mt] = mfma16x16x32(a[mt][s][1], bg[s][1], accg[mt]);
+            accu[mt] = mfma16x16x32(a[mt][s][0], bu[s][0], accu[mt]);
+            accu[mt] = mfma16x16x32(a[mt][s][1], bu[s][1], accu[mt]);
           }
         }
       }
@@ -108,9 +106,9 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
       const uint4 u0 = ld16(wu + k), u1 = ld16(wu + k + 8);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
+        const uint4 a0 = ld16(xr[mt] + k);
+        const uint4 a1 = ld16(xr[mt] + k + 8);
         if (mt < nmt) {
-          const uint4 a0 = ok[mt] ? ld16(xr[mt] + k) : zero;
-          const uint4 a1 = ok[mt] ? ld16(xr[mt] + k + 8) : zero;
           accg[mt] = mfma16x16x32(a0, g0, accg[mt]);
           accg[mt] = mfma16x16x32(a1, g1, accg[mt]);
           accu[mt] = mfma16x16x32(a0, u0, accu[mt]);
@@ -150,8 +148,8 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
   }
 }
 
-// down projection. One wave per (segment, 16 output columns) over the full reduction dim I,
-// weight loads issued in batches of U K-steps.
+// down projection. One wave per (segment, 32 output columns = two 16-column tiles sharing the
+// activation fragments) over the full reduction dim I, loads issued in batches of U K-steps.
 template <int MT, int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
     const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
@@ -163,7 +161,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
   const int tile = blockIdx.x - seg * tiles_per_seg;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int col0 = (tile * 4 + wave) * 16;
+  const int col0 = (tile * 4 + wave) * 32;
   if (col0 >= H) return;
   const int e = seg_expert[seg];
   const int row0 = seg_offset[seg];
@@ -172,58 +170,65 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
   const int kq = lane >> 4;
   const int nsteps = I >> 6;
 
-  const uint16_t* wd = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 16;
-  const uint4 zero = make_uint4(0, 0, 0, 0);
+  const uint16_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 16;
+  const uint16_t* wd1 = wd0 + (size_t)16 * I;
 
   for (int mb = 0; mb < cnt; mb += 16 * MT) {
     const int nmt = min(MT, (cnt - mb + 15) >> 4);
-    floatx4 acc[MT];
+    floatx4 acc0[MT], acc1[MT];
     const uint16_t* hr[MT];
-    bool ok[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const int r = mb + mt * 16 + r16;
-      ok[mt] = r < cnt;
-      hr[mt] = hbuf + (size_t)(row0 + (ok[mt] ? r : 0)) * I + kq * 16;
+      acc0[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      acc1[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+      const int r = min(mb + mt * 16 + r16, cnt - 1);
+      hr[mt] = hbuf + (size_t)(row0 + r) * I + kq * 16;
     }
     int st = 0;
     for (; st + U <= nsteps; st += U) {
-      uint4 b[U][2];
+      uint4 b0[U][2], b1[U][2], a[MT][U][2];
 #pragma unroll
       for (int s = 0; s < U; ++s) {
         const int k = (st + s) << 6;
-        b[s][0] = ld16(wd + k);
-        b[s][1] = ld16(wd + k + 8);
+        b0[s][0] = ld16(wd0 + k);
+        b0[s][1] = ld16(wd0 + k + 8);
+        b1[s][0] = ld16(wd1 + k);
+        b1[s][1] = ld16(wd1 + k + 8);
       }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          const int k = (st + s) << 6;
+          a[mt][s][0] = ld16(hr[mt] + k);
+          a[mt][s][1] = ld16(hr[mt] + k + 8);
+        }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         if (mt < nmt) {
-          uint4 a[U][2];
 #pragma unroll
           for (int s = 0; s < U; ++s) {
-            const int k = (st + s) << 6;
-            a[s][0] = ok[mt] ? ld16(hr[mt] + k) : zero;
-            a[s][1] = ok[mt] ? ld16(hr[mt] + k + 8) : zero;
-          }
-#pragma unroll
-          for (int s = 0; s < U; ++s) {
-            acc[mt] = mfma16x16x32(a[s][0], b[s][0], acc[mt]);
-            acc[mt] = mfma16x16x32(a[s][1], b[s][1], acc[mt]);
+            acc0[mt] = mfma16x16x32(a[mt][s][0], b0[s][0], acc0[mt]);
+            acc0[mt] = mfma16x16x32(a[mt][s][1], b0[s][1], acc0[mt]);
+            acc1[mt] = mfma16x16x32(a[mt][s][0], b1[s][0], acc1[mt]);
+            acc1[mt] = mfma16x16x32(a[mt][s][1], b1[s][1], acc1[mt]);
           }
         }
       }
     }
     for (; st < nsteps; ++st) {
       const int k = st << 6;
-      const uint4 b0 = ld16(wd + k), b1 = ld16(wd + k + 8);
+      const uint4 p0 = ld16(wd0 + k), p1 = ld16(wd0 + k + 8);
+      const uint4 q0 = ld16(wd1 + k), q1 = ld16(wd1 + k + 8);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
+        const uint4 a0 = ld16(hr[mt] + k);
+        const uint4 a1 = ld16(hr[mt] + k + 8);
         if (mt < nmt) {
-          const uint4 a0 = ok[mt] ? ld16(hr[mt] + k) : zero;
-          const uint4 a1 = ok[mt] ? ld16(hr[mt] + k + 8) : zero;
-          acc[mt] = mfma16x16x32(a0, b0, acc[mt]);
-          acc[mt] = mfma16x16x32(a1, b1, acc[mt]);
+          acc0[mt] = mfma16x16x32(a0, p0, acc0[mt]);
+          acc0[mt] = mfma16x16x32(a1, p1, acc0[mt]);
+          acc1[mt] = mfma16x16x32(a0, q0, acc1[mt]);
+          acc1[mt] = mfma16x16x32(a1, q1, acc1[mt]);
         }
       }
     }
@@ -233,7 +238,11 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int r = mb + mt * 16 + kq * 4 + i;
-          if (r < cnt) y[(size_t)(row0 + r) * H + col0 + r16] = acc[mt][i];
+          if (r < cnt) {
+            float* yr = y + (size_t)(row0 + r) * H + col0 + r16;
+            yr[0] = acc0[mt][i];
+            yr[16] = acc1[mt][i];
+          }
         }
       }
     }
@@ -284,8 +293,8 @@ using namespace sym;
 
 static int check_gemm_args(const char* what, int T, int H, int I, int max_segments) {
   SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "%s: T=%d < 0", what, T);
-  SYM_REQUIRE(H > 0 && H % 64 == 0, SYM_ERR_UNSUPPORTED,
-              "%s: H=%d must be a positive multiple of 64", what, H);
+  SYM_REQUIRE(H > 0 && H % 128 == 0, SYM_ERR_UNSUPPORTED,
+              "%s: H=%d must be a positive multiple of 128", what, H);
   SYM_REQUIRE(I > 0 && I % 64 == 0, SYM_ERR_UNSUPPORTED,
               "%s: I=%d must be a positive multiple of 64", what, I);
   SYM_REQUIRE(max_segments >= 1 && max_segments <= 4096, SYM_ERR_INVALID,
@@ -305,7 +314,7 @@ extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t
               SYM_ERR_INVALID, "moe_gate_up: null pointer argument");
   (void)hipGetLastError();
   const int tiles = I / 16;
-  hipLaunchKernelGGL((moe_gate_up_kernel<4, 4>), dim3(max_segments * tiles), dim3(kGemmThreads), 0,
+  hipLaunchKernelGGL((moe_gate_up_kernel<2, 4>), dim3(max_segments * tiles), dim3(kGemmThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)x, H, I, sorted_tokens, seg_expert,
                      seg_offset, seg_count, n_segments, (const uint16_t*)w_gate_up, (uint16_t*)h,
                      tiles);
@@ -323,7 +332,7 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
               SYM_ERR_INVALID, "moe_down: null pointer argument");
   (void)hipGetLastError();
   const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
-  hipLaunchKernelGGL((moe_down_kernel<4, 8>), dim3(max_segments * tiles), dim3(kGemmThreads), 0,
+  hipLaunchKernelGGL((moe_down_kernel<2, 4>), dim3(max_segments * tiles), dim3(kGemmThreads), 0,
                      (hipStream_t)stream, (const uint16_t*)h, H, I, seg_expert, seg_offset,
                      seg_count, n_segments, (const uint16_t*)w_down, y, tiles);
   return sym_host::check_launch("moe_down_kernel");

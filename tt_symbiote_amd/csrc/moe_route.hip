@@ -6,16 +6,19 @@
 // token dispatch of TTNNExperts.forward (ttnn_moe.py:1225-1245).
 //
 // Design (gfx950, wave64):
-//   kernel 1 (one workgroup per chunk of 64 tokens, one wave per token at a time): each lane owns
-//     E/64 consecutive experts, so a group of E/n_group experts spans a power-of-two run of lanes.
-//     Group top-2 is a butterfly over those lanes; group ranking reads the n_group scores with
-//     lane broadcasts; the final top-k is k rounds of a wave-wide max over 64-bit keys
-//     (order-preserving float bits << 32 | (0xFFFF - expert)), which makes ties pick the lower
-//     expert index. The chunk's routing is folded into one 64-bit token mask per expert (LDS
-//     atomic OR, order independent).
-//   kernel 2 (one workgroup): per-expert prefix over chunks, exclusive scan over experts, then
-//     every assignment's row = expert offset + earlier chunks + popcount of earlier tokens in its
-//     own chunk mask. The result does not depend on scheduling order: bit-exact across runs.
+//   router logits: fp32 MFMA (16x16x4) GEMM writing four partial sums over quarters of H.
+//   route kernel (one workgroup per chunk of 64 tokens, one wave per token at a time): each lane
+//     owns E/64 consecutive experts, so a group of E/n_group experts spans a power-of-two run of
+//     lanes. Group top-2 merges partners through DPP row operations; group ranking reads the
+//     n_group scores with readlane; the final top-k is k rounds of a wave-wide max over 64-bit
+//     keys (order-preserving float bits << 32 | (0xFFFF - expert)) -- DPP inside each 16-lane
+//     row, readlane across rows -- which makes ties pick the lower expert index. The chunk's
+//     routing is folded into one 64-bit token mask per expert (LDS atomic OR, order
+//     independent).
+//   permute (same workgroup when there is one chunk, else one extra workgroup): per-expert
+//     prefix over chunks, exclusive scan over experts, then every assignment's row = expert
+//     offset + earlier chunks + popcount of earlier tokens in its own chunk mask. The result does
+//     not depend on scheduling order: bit-exact across runs.
 //
 // Floating point: contraction is disabled in this file so the sigmoid below (own Cody-Waite exp,
 // explicit fma) and every add/divide are the IEEE operations the CPU oracle performs.
@@ -51,148 +54,145 @@ __device__ __forceinline__ uint32_t order_bits(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int off) {
-  uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-  lo = __shfl_xor(lo, off);
-  hi = __shfl_xor(hi, off);
-  return ((uint64_t)hi << 32) | lo;
-}
-
 constexpr int kChunk = 64;      // tokens per chunk (one bit each in a u64 mask)
 constexpr int kRouteThreads = 1024;
 constexpr int kMaxTopK = 32;
+constexpr int kLogitParts = 4;  // partial sums written by the router-logits kernel
 
+// ---- wave64 cross-lane helpers built on DPP row operations (VALU latency) and readlane ----
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within each 8
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within each 16
+
+template <int CTRL>
+__device__ __forceinline__ float dppf(float v) {
+  return __uint_as_float(dpp32<CTRL>(__float_as_uint(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ unsigned long long dpp64(unsigned long long v) {
+  const uint32_t lo = dpp32<CTRL>((uint32_t)v);
+  const uint32_t hi = dpp32<CTRL>((uint32_t)(v >> 32));
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long readlane64(unsigned long long v, int lane) {
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
+  return ((unsigned long long)hi << 32) | lo;
+}
+__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) {
+  return a > b ? a : b;
+}
+// Maximum over the 64 lanes (uniform result): within each 16-lane row with DPP, then across the
+// four rows with readlane.
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
+  v = umax64(v, dpp64<kDppXor1>(v));
+  v = umax64(v, dpp64<kDppXor2>(v));
+  v = umax64(v, dpp64<kDppHalfMirror>(v));
+  v = umax64(v, dpp64<kDppMirror>(v));
+  return umax64(umax64(readlane64(v, 0), readlane64(v, 16)),
+                umax64(readlane64(v, 32), readlane64(v, 48)));
+}
+// (t1, t2) <- the two largest of the union of this lane's pair and the partner's pair.
+__device__ __forceinline__ void top2_merge(float& t1, float& t2, float o1, float o2) {
+  const float n1 = fmaxf(t1, o1);
+  const float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
+  t1 = n1;
+  t2 = n2;
+}
+
+// Route one token with the calling wave (all 64 lanes). Lane l owns experts l*EPL .. l*EPL+EPL-1.
+// The partner patterns used for the group top-2 (xor 1, xor 2, half mirror, mirror, then xor 16
+// and xor 32) always pair disjoint lane sets, so no expert is counted twice.
 template <int EPL>
-__global__ __launch_bounds__(kRouteThreads) void moe_route_chunk_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int n_group,
-    int topk_group, int top_k, float routed_scale, int renorm, int32_t* __restrict__ topk_idx,
-    float* __restrict__ topk_w, unsigned long long* __restrict__ chunk_mask,
-    int32_t* __restrict__ chunk_cnt) {
-  __shared__ unsigned long long s_mask[64 * EPL];
-  __shared__ int32_t s_idx[kChunk * kMaxTopK];
-
-  const int chunk = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int nwaves = blockDim.x >> 6;
-
-  for (int e = tid; e < E; e += blockDim.x) s_mask[e] = 0ull;
-
-  const int gsz = E / n_group;  // experts per group
-  const int lpg = gsz / EPL;    // lanes per group (power of two)
+__device__ __forceinline__ void route_token(const float* __restrict__ logits, int n_parts,
+                                            size_t part_stride, const float* bv, int t, int E,
+                                            int n_group, int topk_group, int top_k,
+                                            float routed_scale, int renorm, int lane, int& my_idx,
+                                            float& my_w) {
+  const int gsz = E / n_group;
+  const int lpg = gsz / EPL;
   const int my_group = lane / lpg;
-
-  float bv[EPL];
+  float s[EPL], c[EPL];
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) bv[j] = bias[lane * EPL + j];
+  for (int j = 0; j < EPL; ++j) {
+    const size_t o = (size_t)t * E + lane * EPL + j;
+    float x = logits[o];
+    for (int q = 1; q < n_parts; ++q) x = x + logits[q * part_stride + o];
+    s[j] = route_sigmoid(x);
+    c[j] = s[j] + bv[j];
+  }
+  float t1 = -INFINITY, t2 = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const float v = c[j];
+    if (v > t1) {
+      t2 = t1;
+      t1 = v;
+    } else if (v > t2) {
+      t2 = v;
+    }
+  }
+  if (lpg >= 2) top2_merge(t1, t2, dppf<kDppXor1>(t1), dppf<kDppXor1>(t2));
+  if (lpg >= 4) top2_merge(t1, t2, dppf<kDppXor2>(t1), dppf<kDppXor2>(t2));
+  if (lpg >= 8) top2_merge(t1, t2, dppf<kDppHalfMirror>(t1), dppf<kDppHalfMirror>(t2));
+  if (lpg >= 16) top2_merge(t1, t2, dppf<kDppMirror>(t1), dppf<kDppMirror>(t2));
+  if (lpg >= 32) top2_merge(t1, t2, __shfl_xor(t1, 16), __shfl_xor(t2, 16));
+  if (lpg >= 64) top2_merge(t1, t2, __shfl_xor(t1, 32), __shfl_xor(t2, 32));
+  const float gscore = t1 + t2;
 
-  const int tok0 = chunk * kChunk;
-  const int ntok = min(kChunk, T - tok0);
+  int rank = 0;
+  for (int g = 0; g < n_group; ++g) {
+    const float o = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(gscore), g * lpg));
+    rank += (o > gscore) || (o == gscore && g < my_group);
+  }
+  const bool keep = rank < topk_group;
 
-  for (int tl = wave; tl < ntok; tl += nwaves) {
-    const int t = tok0 + tl;
-    const float* lrow = logits + (size_t)t * E + lane * EPL;
-    float s[EPL], c[EPL];
+  unsigned long long key[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) {
+    const float m = keep ? c[j] : 0.0f;
+    key[j] = ((unsigned long long)order_bits(m) << 32) |
+             (unsigned long long)(0xFFFFu - (uint32_t)(lane * EPL + j));
+  }
+  float denom = 0.0f;
+  my_idx = 0;
+  my_w = 0.0f;
+  for (int k = 0; k < top_k; ++k) {
+    unsigned long long best = 0ull;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) best = umax64(best, key[j]);
+    best = wave_max_u64(best);
+    const int e = (int)(0xFFFFu - (uint32_t)(best & 0xFFFFull));
+    const int owner = e / EPL;
+    const int jj = e - owner * EPL;
+    float sv = 0.0f;
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
-      s[j] = route_sigmoid(lrow[j]);
-      c[j] = s[j] + bv[j];
+      if (j == jj) sv = s[j];
     }
-
-    // group score = largest + second largest c of the group
-    float t1 = -INFINITY, t2 = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const float v = c[j];
-      if (v > t1) {
-        t2 = t1;
-        t1 = v;
-      } else if (v > t2) {
-        t2 = v;
-      }
-    }
-    for (int off = 1; off < lpg; off <<= 1) {
-      const float o1 = __shfl_xor(t1, off);
-      const float o2 = __shfl_xor(t2, off);
-      const float n1 = fmaxf(t1, o1);
-      const float n2 = fmaxf(fminf(t1, o1), fmaxf(t2, o2));
-      t1 = n1;
-      t2 = n2;
-    }
-    const float gscore = t1 + t2;
-
-    // rank of this lane's group among all groups (ties: lower group first)
-    int rank = 0;
-    for (int g = 0; g < n_group; ++g) {
-      const float o = __shfl(gscore, g * lpg);
-      rank += (o > gscore) || (o == gscore && g < my_group);
-    }
-    const bool keep = rank < topk_group;
-
-    unsigned long long key[EPL];
-#pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      const float m = keep ? c[j] : 0.0f;
-      key[j] = ((unsigned long long)order_bits(m) << 32) |
-               (unsigned long long)(0xFFFFu - (uint32_t)(lane * EPL + j));
-    }
-
-    float denom = 0.0f;
-    int my_idx = 0;
-    float my_w = 0.0f;
-    for (int k = 0; k < top_k; ++k) {
-      unsigned long long best = 0ull;
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) best = key[j] > best ? key[j] : best;
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) {
-        const unsigned long long o = shfl_xor_u64(best, off);
-        best = o > best ? o : best;
-      }
-      const int e = (int)(0xFFFFu - (uint32_t)(best & 0xFFFFull));
-      const int owner = e / EPL;
-      const int jj = e - owner * EPL;
-      float sv = 0.0f;
+    if (lane == owner) {
 #pragma unroll
       for (int j = 0; j < EPL; ++j) {
-        if (j == jj) sv = s[j];
-      }
-      if (lane == owner) {
-#pragma unroll
-        for (int j = 0; j < EPL; ++j) {
-          if (j == jj) key[j] = 0ull;
-        }
-      }
-      sv = __shfl(sv, owner);
-      denom = denom + sv;
-      if (lane == k) {
-        my_idx = e;
-        my_w = sv;
+        if (j == jj) key[j] = 0ull;
       }
     }
-    if (renorm) {
-      denom = denom + 1e-20f;
-      my_w = my_w / denom;
-    }
-    my_w = my_w * routed_scale;
-    if (lane < top_k) {
-      topk_idx[(size_t)t * top_k + lane] = my_idx;
-      topk_w[(size_t)t * top_k + lane] = my_w;
-      s_idx[tl * top_k + lane] = my_idx;
+    sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), owner));
+    denom = denom + sv;
+    if (lane == k) {
+      my_idx = e;
+      my_w = sv;
     }
   }
-  __syncthreads();
-  for (int a = tid; a < ntok * top_k; a += blockDim.x) {
-    const int tl = a / top_k;
-    atomicOr(&s_mask[s_idx[a]], 1ull << tl);
+  if (renorm) {
+    denom = denom + 1e-20f;
+    my_w = my_w / denom;
   }
-  __syncthreads();
-  for (int e = tid; e < E; e += blockDim.x) {
-    const unsigned long long m = s_mask[e];
-    chunk_mask[(size_t)chunk * E + e] = m;
-    chunk_cnt[(size_t)chunk * E + e] = __popcll(m);
-  }
+  my_w = my_w * routed_scale;
 }
 
 // Exclusive scan of one int per thread over a workgroup of up to 1024 threads.
@@ -224,24 +224,31 @@ __device__ int block_exclusive_scan(int v, int* s_wave, int* total) {
   return before + x - v;
 }
 
-__global__ __launch_bounds__(kRouteThreads) void moe_permute_kernel(
-    const int32_t* __restrict__ topk_idx, int T, int K, int E, int n_chunks,
-    const unsigned long long* __restrict__ chunk_mask, const int32_t* __restrict__ chunk_cnt,
-    int32_t* __restrict__ chunk_pre, int with_shared, int32_t* __restrict__ expert_counts,
-    int32_t* __restrict__ expert_offsets, int32_t* __restrict__ sorted_tokens,
-    int32_t* __restrict__ inv_perm, int32_t* __restrict__ seg_expert,
-    int32_t* __restrict__ seg_offset, int32_t* __restrict__ seg_count,
-    int32_t* __restrict__ n_segments) {
-  __shared__ int s_off[1024];
-  __shared__ int s_wave[16];
+// Counting-sort permute of all assignments, by one workgroup. `mask(c, e)` / `cnt(c, e)` give
+// chunk c's token bitmask and count for expert e.
+struct PermuteOut {
+  int32_t* expert_counts;
+  int32_t* expert_offsets;
+  int32_t* sorted_tokens;
+  int32_t* inv_perm;
+  int32_t* seg_expert;
+  int32_t* seg_offset;
+  int32_t* seg_count;
+  int32_t* n_segments;
+};
+
+template <typename MaskFn, typename CntFn>
+__device__ void permute_block(const int32_t* __restrict__ topk_idx, int T, int K, int E,
+                              int n_chunks, MaskFn mask, CntFn cnt_of,
+                              int32_t* __restrict__ chunk_pre, int with_shared, int* s_off,
+                              int* s_wave, const PermuteOut& o) {
   const int tid = threadIdx.x;
   const int e = tid;
-
   int cnt = 0;
   if (e < E) {
     for (int c = 0; c < n_chunks; ++c) {
-      const int v = chunk_cnt[(size_t)c * E + e];
-      chunk_pre[(size_t)c * E + e] = cnt;
+      const int v = cnt_of(c, e);
+      if (chunk_pre) chunk_pre[(size_t)c * E + e] = cnt;
       cnt += v;
     }
   }
@@ -252,38 +259,163 @@ __global__ __launch_bounds__(kRouteThreads) void moe_permute_kernel(
   const int slot = block_exclusive_scan(flag, s_wave, &n_routed);
   if (e < E) {
     s_off[e] = off;
-    expert_counts[e] = cnt;
-    expert_offsets[e] = off;
+    o.expert_counts[e] = cnt;
+    o.expert_offsets[e] = off;
     if (flag) {
-      seg_expert[slot] = e;
-      seg_offset[slot] = off;
-      seg_count[slot] = cnt;
+      o.seg_expert[slot] = e;
+      o.seg_offset[slot] = off;
+      o.seg_count[slot] = cnt;
     }
   }
   if (tid == 0) {
-    expert_offsets[E] = total;
+    o.expert_offsets[E] = total;
     if (with_shared) {
-      seg_expert[n_routed] = E;
-      seg_offset[n_routed] = T * K;
-      seg_count[n_routed] = T;
+      o.seg_expert[n_routed] = E;
+      o.seg_offset[n_routed] = T * K;
+      o.seg_count[n_routed] = T;
     }
-    n_segments[0] = n_routed + (with_shared ? 1 : 0);
+    o.n_segments[0] = n_routed + (with_shared ? 1 : 0);
   }
   __syncthreads();
-
   for (int a = tid; a < T * K; a += blockDim.x) {
     const int t = a / K;
     const int ex = topk_idx[a];
     const int c = t >> 6;
     const int bit = t & 63;
-    const unsigned long long m = chunk_mask[(size_t)c * E + ex];
+    const unsigned long long m = mask(c, ex);
     const unsigned long long lower = bit ? (m & ((1ull << bit) - 1ull)) : 0ull;
-    const int row = s_off[ex] + chunk_pre[(size_t)c * E + ex] + __popcll(lower);
-    sorted_tokens[row] = t;
-    inv_perm[a] = row;
+    const int pre = n_chunks > 1 ? chunk_pre[(size_t)c * E + ex] : 0;
+    const int row = s_off[ex] + pre + __popcll(lower);
+    o.sorted_tokens[row] = t;
+    o.inv_perm[a] = row;
   }
   if (with_shared) {
-    for (int t = tid; t < T; t += blockDim.x) sorted_tokens[T * K + t] = t;
+    for (int t = tid; t < T; t += blockDim.x) o.sorted_tokens[T * K + t] = t;
+  }
+}
+
+// Routes one chunk of 64 tokens (one wave per token at a time) and folds the chunk's routing
+// into per-expert token bitmasks. With a single chunk (T <= 64, the decode case) the same
+// workgroup then performs the permute, so routing is one launch.
+template <int EPL>
+__global__ __launch_bounds__(kRouteThreads) void moe_route_chunk_kernel(
+    const float* __restrict__ logits, int n_parts, const float* __restrict__ bias, int T, int E,
+    int n_group, int topk_group, int top_k, float routed_scale, int renorm,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
+    unsigned long long* __restrict__ chunk_mask, int32_t* __restrict__ chunk_cnt,
+    int with_shared, PermuteOut po) {
+  __shared__ unsigned long long s_mask[64 * EPL];
+  __shared__ int32_t s_idx[kChunk * kMaxTopK];
+  __shared__ int s_off[64 * EPL];
+  __shared__ int s_wave[16];
+
+  const int chunk = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int nwaves = blockDim.x >> 6;
+
+  for (int e = tid; e < E; e += blockDim.x) s_mask[e] = 0ull;
+
+  float bv[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) bv[j] = bias[lane * EPL + j];
+
+  const int tok0 = chunk * kChunk;
+  const int ntok = min(kChunk, T - tok0);
+  const size_t part_stride = (size_t)T * E;
+
+  for (int tl = wave; tl < ntok; tl += nwaves) {
+    const int t = tok0 + tl;
+    int my_idx;
+    float my_w;
+    route_token<EPL>(logits, n_parts, part_stride, bv, t, E, n_group, topk_group, top_k,
+                     routed_scale, renorm, lane, my_idx, my_w);
+    if (lane < top_k) {
+      topk_idx[(size_t)t * top_k + lane] = my_idx;
+      topk_w[(size_t)t * top_k + lane] = my_w;
+      s_idx[tl * top_k + lane] = my_idx;
+    }
+  }
+  __syncthreads();
+  for (int a = tid; a < ntok * top_k; a += blockDim.x) {
+    const int tl = a / top_k;
+    atomicOr(&s_mask[s_idx[a]], 1ull << tl);
+  }
+  __syncthreads();
+  if (gridDim.x == 1) {
+    // single chunk: permute straight from the LDS masks (topk_idx re-read from this block's
+    // own global writes, visible after the barrier)
+    permute_block(
+        topk_idx, T, top_k, E, 1, [&](int, int e) { return s_mask[e]; },
+        [&](int, int e) { return (int)__popcll(s_mask[e]); }, (int32_t*)nullptr, with_shared,
+        s_off, s_wave, po);
+    return;
+  }
+  for (int e = tid; e < E; e += blockDim.x) {
+    const unsigned long long m = s_mask[e];
+    chunk_mask[(size_t)chunk * E + e] = m;
+    chunk_cnt[(size_t)chunk * E + e] = __popcll(m);
+  }
+}
+
+__global__ __launch_bounds__(kRouteThreads) void moe_permute_kernel(
+    const int32_t* __restrict__ topk_idx, int T, int K, int E, int n_chunks,
+    const unsigned long long* __restrict__ chunk_mask, const int32_t* __restrict__ chunk_cnt,
+    int32_t* __restrict__ chunk_pre, int with_shared, PermuteOut po) {
+  __shared__ int s_off[1024];
+  __shared__ int s_wave[16];
+  permute_block(
+      topk_idx, T, K, E, n_chunks,
+      [&](int c, int e) { return chunk_mask[(size_t)c * E + e]; },
+      [&](int c, int e) { return (int)chunk_cnt[(size_t)c * E + e]; }, chunk_pre, with_shared,
+      s_off, s_wave, po);
+}
+
+// Router logits in fp32 with v_mfma_f32_16x16x4_f32: parts[q][t][e] = sum over the q-th
+// quarter of H of x[t][k] * w[e][k]. One workgroup per (16 experts, quarter of H); its 4 waves
+// split the quarter again and reduce through LDS; every wave covers all token tiles, so each
+// weight element is read once. Lane l streams 4 consecutive k of weight row l%16 (16 bytes)
+// and the matching 4 activations; the 4 MFMAs of a 16-wide k chunk use one element each, so A
+// and B agree on the k order.
+__global__ __launch_bounds__(256) void moe_router_logits_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ w, int T, int H, int E,
+    float* __restrict__ parts) {
+  __shared__ float s_red[4][4][64];
+  const int ntile = blockIdx.x;
+  const int q = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int quarter = H >> 2;            // H % 256 == 0
+  const int sub = quarter >> 2;           // this wave's share, a multiple of 16
+  const int k_beg = q * quarter + wave * sub;
+  const float* wr = w + (size_t)(ntile * 16 + r16) * H + kq * 4;
+  for (int mb = 0; mb < T; mb += 16) {
+    const int m = min(mb + r16, T - 1);  // rows past T repeat the last row; dropped below
+    const uint16_t* xr = x + (size_t)m * H + kq * 4;
+    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int k = k_beg; k < k_beg + sub; k += 16) {
+      const float4 b = *reinterpret_cast<const float4*>(wr + k);
+      const uint2 av = *reinterpret_cast<const uint2*>(xr + k);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bf16_lo(av.x), b.x, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bf16_hi(av.x), b.y, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bf16_lo(av.y), b.z, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bf16_hi(av.y), b.w, acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) s_red[wave][i][lane] = acc[i];
+    __syncthreads();
+    {
+      const int l = threadIdx.x & 63;
+      const int i = threadIdx.x >> 6;
+      const int row = mb + 4 * (l >> 4) + i;
+      const float v = (s_red[0][i][l] + s_red[1][i][l]) + (s_red[2][i][l] + s_red[3][i][l]);
+      if (row < T) parts[((size_t)q * T + row) * E + ntile * 16 + (l & 15)] = v;
+    }
+    __syncthreads();
   }
 }
 
@@ -298,10 +430,25 @@ extern "C" size_t sym_moe_route_workspace_bytes(int T, int E) {
   return chunks * (size_t)E * (8 + 4 + 4) + 256;
 }
 
-extern "C" int sym_moe_route_permute(const float* logits, const float* bias, int T, int E,
-                                     int n_group, int topk_group, int top_k, float routed_scale,
-                                     int renormalize, int with_shared, int32_t* topk_idx,
-                                     float* topk_w, int32_t* expert_counts,
+extern "C" int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E,
+                                     float* parts, void* stream) {
+  SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "moe_router_logits: T=%d < 0", T);
+  if (T == 0) return SYM_OK;
+  SYM_REQUIRE(x && w && parts, SYM_ERR_INVALID, "moe_router_logits: null pointer argument");
+  SYM_REQUIRE(H > 0 && H % 256 == 0, SYM_ERR_UNSUPPORTED,
+              "moe_router_logits: H=%d must be a positive multiple of 256", H);
+  SYM_REQUIRE(E > 0 && E % 16 == 0 && E / 16 <= 65535, SYM_ERR_UNSUPPORTED,
+              "moe_router_logits: E=%d must be a positive multiple of 16", E);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(moe_router_logits_kernel, dim3(E / 16, kLogitParts), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, w, T, H, E, parts);
+  return sym_host::check_launch("moe_router_logits_kernel");
+}
+
+extern "C" int sym_moe_route_permute(const float* logits, int n_logit_parts, const float* bias,
+                                     int T, int E, int n_group, int topk_group, int top_k,
+                                     float routed_scale, int renormalize, int with_shared,
+                                     int32_t* topk_idx, float* topk_w, int32_t* expert_counts,
                                      int32_t* expert_offsets, int32_t* sorted_tokens,
                                      int32_t* inv_perm, int32_t* seg_expert, int32_t* seg_offset,
                                      int32_t* seg_count, int32_t* n_segments, void* workspace,
@@ -312,6 +459,8 @@ extern "C" int sym_moe_route_permute(const float* logits, const float* bias, int
                   sorted_tokens && inv_perm && seg_expert && seg_offset && seg_count &&
                   n_segments && workspace,
               SYM_ERR_INVALID, "moe_route_permute: null pointer argument");
+  SYM_REQUIRE(n_logit_parts >= 1 && n_logit_parts <= 16, SYM_ERR_INVALID,
+              "moe_route_permute: n_logit_parts=%d out of [1,16]", n_logit_parts);
   SYM_REQUIRE(E == 64 || E == 128 || E == 256 || E == 512, SYM_ERR_UNSUPPORTED,
               "moe_route_permute: E=%d not in {64,128,256,512}", E);
   SYM_REQUIRE(n_group >= 1 && E % n_group == 0, SYM_ERR_INVALID,
@@ -340,36 +489,26 @@ extern "C" int sym_moe_route_permute(const float* logits, const float* bias, int
   unsigned long long* chunk_mask = (unsigned long long*)ws;
   int32_t* chunk_cnt = (int32_t*)(ws + (size_t)n_chunks * E * 8);
   int32_t* chunk_pre = chunk_cnt + (size_t)n_chunks * E;
+  const PermuteOut po{expert_counts, expert_offsets, sorted_tokens, inv_perm,
+                      seg_expert,    seg_offset,     seg_count,     n_segments};
 
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
   const dim3 grid(n_chunks), block(kRouteThreads);
+#define SYM_LAUNCH_ROUTE(EE)                                                                    \
+  hipLaunchKernelGGL(moe_route_chunk_kernel<EE>, grid, block, 0, s, logits, n_logit_parts, bias, \
+                     T, E, n_group, topk_group, top_k, routed_scale, renormalize, topk_idx,      \
+                     topk_w, chunk_mask, chunk_cnt, with_shared, po)
   switch (epl) {
-    case 1:
-      hipLaunchKernelGGL(moe_route_chunk_kernel<1>, grid, block, 0, s, logits, bias, T, E, n_group,
-                         topk_group, top_k, routed_scale, renormalize, topk_idx, topk_w,
-                         chunk_mask, chunk_cnt);
-      break;
-    case 2:
-      hipLaunchKernelGGL(moe_route_chunk_kernel<2>, grid, block, 0, s, logits, bias, T, E, n_group,
-                         topk_group, top_k, routed_scale, renormalize, topk_idx, topk_w,
-                         chunk_mask, chunk_cnt);
-      break;
-    case 4:
-      hipLaunchKernelGGL(moe_route_chunk_kernel<4>, grid, block, 0, s, logits, bias, T, E, n_group,
-                         topk_group, top_k, routed_scale, renormalize, topk_idx, topk_w,
-                         chunk_mask, chunk_cnt);
-      break;
-    default:
-      hipLaunchKernelGGL(moe_route_chunk_kernel<8>, grid, block, 0, s, logits, bias, T, E, n_group,
-                         topk_group, top_k, routed_scale, renormalize, topk_idx, topk_w,
-                         chunk_mask, chunk_cnt);
-      break;
+    case 1: SYM_LAUNCH_ROUTE(1); break;
+    case 2: SYM_LAUNCH_ROUTE(2); break;
+    case 4: SYM_LAUNCH_ROUTE(4); break;
+    default: SYM_LAUNCH_ROUTE(8); break;
   }
+#undef SYM_LAUNCH_ROUTE
   int rc = sym_host::check_launch("moe_route_chunk_kernel");
-  if (rc) return rc;
-  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), 0, s, topk_idx, T, top_k, E, n_chunks,
-                     chunk_mask, chunk_cnt, chunk_pre, with_shared, expert_counts, expert_offsets,
-                     sorted_tokens, inv_perm, seg_expert, seg_offset, seg_count, n_segments);
+  if (rc || n_chunks == 1) return rc;
+  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), 0, s, topk_idx, T, top_k, E,
+                     n_chunks, chunk_mask, chunk_cnt, chunk_pre, with_shared, po);
   return sym_host::check_launch("moe_permute_kernel");
 }

@@ -163,7 +163,8 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
   __shared__ float s_p[G][kSplit];
   __shared__ float s_red[4][G][D];
   __shared__ float s_stat[G][4];
-  __shared__ int s_bt[kSplit];
+  __shared__ int s_bt[kSplit];   // physical block of each token (always a valid block)
+  __shared__ int s_ok[kSplit];   // token is inside the split and its page-table entry is valid
 
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int Hq = Hkv * G;
@@ -181,18 +182,18 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
     const int h = i / D, d = i - h * D;
     s_q[h][d] = bf16_to_f32(q[((size_t)b * Hq + g * G + h) * D + d]) * scale_log2;
   }
-  // physical block of every token of the split (-1 = invalid)
+  // Physical block of every token of the split. Tokens past the sequence read the split's
+  // last valid token instead (an in-bounds row already being loaded) and are masked out, so
+  // every K/V load below is unconditional.
   {
     const int t = t0 + tid;
-    int p = -1;
-    if (t < t1) {
-      const int blk = t / block_size;
-      if (blk < mbps) {
-        const int v = block_tables[(size_t)b * mbps + blk];
-        if (v >= 0 && v < num_blocks) p = v;
-      }
-    }
+    const int tc = min(t, t1 - 1);
+    const int blk = tc / block_size;
+    int p = blk < mbps ? block_tables[(size_t)b * mbps + blk] : -1;
+    const bool valid = t < t1 && p >= 0 && p < num_blocks;
+    if (p < 0 || p >= num_blocks) p = 0;
     s_bt[tid] = p;
+    s_ok[tid] = valid;
   }
   __syncthreads();
 
@@ -204,30 +205,19 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
 
   // Issue every K and V load of this wave's 64 tokens up front (16 + 16 loads of 16 bytes per
   // lane); V arrives while the scores and the softmax statistics are computed.
-  const uint4 zero = make_uint4(0, 0, 0, 0);
   uint4 kreg[16], vreg[16];
+  size_t roff[16];
 #pragma unroll
   for (int it = 0; it < 16; ++it) {
     const int tl = wave * 64 + it * 4 + tq;
-    const int t = t0 + tl;
-    const int phys = s_bt[tl];
-    const size_t off = phys >= 0
-        ? (((size_t)phys * Hkv + g) * block_size + (t - (t / block_size) * block_size)) * D +
-              sub * 8
-        : 0;
-    kreg[it] = phys >= 0 ? *reinterpret_cast<const uint4*>(k_pool + off) : zero;
+    const int tc = min(t0 + tl, t1 - 1);
+    roff[it] = (((size_t)s_bt[tl] * Hkv + g) * block_size + (tc - (tc / block_size) * block_size)) *
+                   D + sub * 8;
   }
 #pragma unroll
-  for (int it = 0; it < 16; ++it) {
-    const int tl = wave * 64 + it * 4 + tq;
-    const int t = t0 + tl;
-    const int phys = s_bt[tl];
-    const size_t off = phys >= 0
-        ? (((size_t)phys * Hkv + g) * block_size + (t - (t / block_size) * block_size)) * D +
-              sub * 8
-        : 0;
-    vreg[it] = phys >= 0 ? *reinterpret_cast<const uint4*>(v_pool + off) : zero;
-  }
+  for (int it = 0; it < 16; ++it) kreg[it] = *reinterpret_cast<const uint4*>(k_pool + roff[it]);
+#pragma unroll
+  for (int it = 0; it < 16; ++it) vreg[it] = *reinterpret_cast<const uint4*>(v_pool + roff[it]);
 
   // ---- scores ----
 #pragma unroll
@@ -249,7 +239,7 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
       for (int o = 8; o > 0; o >>= 1) dot[h] += __shfl_xor(dot[h], o);
     }
     if (sub == 0) {
-      const bool valid = s_bt[tl] >= 0;
+      const bool valid = s_ok[tl] != 0;
 #pragma unroll
       for (int h = 0; h < G; ++h) s_p[h][tl] = valid ? dot[h] : -INFINITY;
     }

@@ -115,6 +115,32 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     return (out, residual_out) if residual is not None else out
 
 
+def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+           out_dtype: torch.dtype = torch.bfloat16, out: Optional[torch.Tensor] = None):
+    """x [M, K] bf16 . w [N, K]^T (+ bias [N]) -> [M, N] in ``out_dtype`` (bf16 or fp32)."""
+    _check(x, "x", torch.bfloat16)
+    if x.dim() != 2:
+        raise ValueError(f"x must be [M, K], got {tuple(x.shape)}")
+    M, K = x.shape
+    _check(w, "w", torch.bfloat16, x.device)
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError(f"w must be [N, {K}], got {tuple(w.shape)}")
+    N = w.shape[0]
+    if bias is not None:
+        _check(bias, "bias", torch.bfloat16, x.device)
+        _check_shape(bias, "bias", (N,))
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype {out_dtype} (bf16 or fp32)")
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype, device=x.device)
+    _check(out, "out", out_dtype, x.device)
+    _check_shape(out, "out", (M, N))
+    _timed("linear", lambda: _lib.call(
+        "sym_linear_bf16", _ptr(x), _ptr(w), _ptr(bias), M, N, K, _ptr(out),
+        1 if out_dtype == torch.float32 else 0, _stream()))
+    return out
+
+
 # -------------------------------------------------------------------------------------------
 @dataclass
 class PagedLayout:
@@ -272,14 +298,39 @@ class RouteResult:
         return self.sorted_tokens.numel()
 
 
+LOGIT_PARTS = 4
+
+
+def moe_router_logits(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """fp32 router logits of x [T, H] (bf16) against w [E, H] (fp32), returned as the four
+    partial sums [4, T, E] over quarters of H (their left-to-right sum is the logits)."""
+    _check(x, "x", torch.bfloat16)
+    if x.dim() != 2:
+        raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
+    T, H = x.shape
+    _check(w, "w", torch.float32, x.device)
+    if w.dim() != 2 or w.shape[1] != H:
+        raise ValueError(f"w must be [E, {H}], got {tuple(w.shape)}")
+    E = w.shape[0]
+    parts = torch.empty(LOGIT_PARTS, T, E, dtype=torch.float32, device=x.device)
+    _timed("moe_router_logits", lambda: _lib.call(
+        "sym_moe_router_logits", _ptr(x), _ptr(w), T, H, E, _ptr(parts), _stream()))
+    return parts
+
+
 def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,
                       topk_group: int, top_k: int, routed_scale: float,
                       renormalize: bool = True, with_shared: bool = True) -> RouteResult:
-    """Fused sigmoid/bias/group-limited top-k router + expert-sorted permute."""
+    """Fused sigmoid/bias/group-limited top-k router + expert-sorted permute. ``logits`` is
+    [T, E], or [P, T, E] partial sums added left to right (as from :func:`moe_router_logits`)."""
     _check(logits, "logits", torch.float32)
-    if logits.dim() != 2:
-        raise ValueError(f"logits must be [T, E], got {tuple(logits.shape)}")
-    T, E = logits.shape
+    if logits.dim() == 2:
+        n_parts = 1
+        T, E = logits.shape
+    elif logits.dim() == 3:
+        n_parts, T, E = logits.shape
+    else:
+        raise ValueError(f"logits must be [T, E] or [P, T, E], got {tuple(logits.shape)}")
     dev = logits.device
     _check(bias, "bias", torch.float32, dev)
     _check_shape(bias, "bias", (E,))
@@ -302,12 +353,13 @@ def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,
         return res
     ws_bytes = _lib.query("sym_moe_route_workspace_bytes", T, E)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
-    _lib.call("sym_moe_route_permute", _ptr(logits), _ptr(bias), T, E, int(n_group),
+    _timed("moe_route_permute", lambda: _lib.call(
+              "sym_moe_route_permute", _ptr(logits), n_parts, _ptr(bias), T, E, int(n_group),
               int(topk_group), int(top_k), float(routed_scale), 1 if renormalize else 0,
               1 if with_shared else 0, _ptr(res.topk_idx), _ptr(res.topk_w),
               _ptr(res.expert_counts), _ptr(res.expert_offsets), _ptr(res.sorted_tokens),
               _ptr(res.inv_perm), _ptr(res.seg_expert), _ptr(res.seg_offset),
-              _ptr(res.seg_count), _ptr(res.n_segments), _ptr(ws), ws.numel(), _stream())
+              _ptr(res.seg_count), _ptr(res.n_segments), _ptr(ws), ws.numel(), _stream()))
     return res
 
 

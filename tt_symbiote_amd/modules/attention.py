@@ -9,10 +9,10 @@ same HF fields (ttnn_attention.py:1954-2042): ``config.num_attention_heads`` /
 layout (no Meta-interleave permutation: that layout exists for TT's rotary kernel).
 
 Decode step (``seq_len == 1`` with a paged cache; ttnn_attention.py:2308-2466):
-  qkv  = x W_qkv^T (+b)                          hipBLASLt through torch
+  qkv  = x W_qkv^T (+b)                          skinny-GEMM kernel
   q, K/V slot write = one prologue kernel         QK RMSNorm, partial RoPE, paged KV write
   o    = paged GQA decode kernel (split-K + merge)
-  out  = o W_dense^T (+b)                         hipBLASLt through torch
+  out  = o W_dense^T (+b)                         skinny-GEMM kernel
 Positions are per-sequence device int32 (``cache_position`` / ``position_ids`` per row); when
 absent, the cache's host counter is used for every row, as in the reference.
 """
@@ -21,7 +21,6 @@ from __future__ import annotations
 from typing import Dict, Optional, Tuple
 
 import torch
-import torch.nn.functional as F
 
 from .. import hip_ops
 from ..core.module import StatefulHIPModule
@@ -179,7 +178,7 @@ class HIPBailingMoEAttention(StatefulHIPModule):
         kp = cache.key_cache(self.layer_idx)
         vp = cache.value_cache(self.layer_idx)
         pt = cache.page_table_device
-        qkv = F.linear(x, d["qkv_w"], d["qkv_b"])
+        qkv = hip_ops.linear(x, d["qkv_w"], d["qkv_b"])
         q = hip_ops.attn_decode_prologue(
             qkv, pos, kp, vp, pt, num_heads=self.num_heads, num_kv_heads=self.num_kv_heads,
             rotary_dim=self.rotary_dim, rope_cs=d["rope"], q_norm_w=d["q_norm"],
@@ -187,5 +186,5 @@ class HIPBailingMoEAttention(StatefulHIPModule):
         o = hip_ops.paged_gqa_decode(q, kp, vp, pt, pos, self.scaling,
                                      max_context=cache.max_context,
                                      workspace=cache.decode_workspace(B, self.num_heads))
-        out = F.linear(o.view(B, self.num_heads * self.head_dim), d["dense_w"], d["dense_b"])
+        out = hip_ops.linear(o.view(B, self.num_heads * self.head_dim), d["dense_w"], d["dense_b"])
         return out.view(B, 1, H), None, cache

@@ -10,7 +10,7 @@ forces ``norm_topk_prob`` True (ttnn_moe.py:1532). The shared expert (intermedia
 ``I * num_shared_experts``) is stored as stack slot ``E`` when its width equals ``I``.
 
 Forward (decode or prefill token counts alike, no host synchronisation):
-  logits = x_fp32 W_gate_fp32^T                   fp32 GEMM through torch
+  logits = x_fp32 W_gate_fp32^T                   fp32 MFMA kernel (four partial sums)
   route  = fused router + top-k + permute kernel  (bit-exact indices)
   h, y   = grouped SwiGLU kernels over the device segment list (+ shared expert)
   out    = unpermute + weighted combine (+ shared) (+ optional residual) kernel
@@ -20,7 +20,6 @@ from __future__ import annotations
 from typing import Dict
 
 import torch
-import torch.nn.functional as F
 
 from .. import hip_ops
 from ..core.module import StatelessHIPModule
@@ -134,8 +133,8 @@ class HIPBailingMoE(StatelessHIPModule):
         return super().deallocate_weights_impl()
 
     def route(self, x: torch.Tensor) -> hip_ops.RouteResult:
-        """Router logits (fp32) + fused top-k/permute for tokens x [T, H] (bf16)."""
-        logits = F.linear(x.float(), self._dev["gate_w"])
+        """Router logits (fp32 MFMA) + fused top-k/permute for tokens x [T, H] (bf16)."""
+        logits = hip_ops.moe_router_logits(x, self._dev["gate_w"])
         return hip_ops.moe_route_permute(
             logits, self._dev["bias"], n_group=self.n_group, topk_group=self.topk_group,
             top_k=self.top_k, routed_scale=self.routed_scaling_factor, renormalize=True,
