@@ -110,8 +110,11 @@ int sym_paged_kv_fill(const void* k, const void* v, void* k_pool, void* v_pool,
  * ttnn.transformer.paged_scaled_dot_product_attention_decode (ttnn_attention.py:288-329):
  *   out[b, h] = softmax(scale * q[b,h] . K[b, 0..positions[b]]^T) V[b, 0..positions[b]]
  * with kv head = h / (Hq/Hkv); K/V gathered through the page table; fp32 accumulation.
- *   q   [B, Hq, 128] bf16;  out [B, Hq, 128] bf16
- *   max_context: upper bound of positions[b]+1 (normally max_blocks_per_seq * block_size).
+ *   q   [B, Hq, 128] bf16;  out [B, Hq, 128] bf16 (zero for a sequence with positions[b] < 0)
+ *   max_context: attention length cap (normally max_blocks_per_seq * block_size); a sequence
+ *   attends min(positions[b] + 1, max_context) slots.
+ *   workspace: sym_paged_gqa_decode_workspace_bytes(...) bytes of per-split partial results
+ *   (no initial contents needed). Calls that overlap in time must not share a workspace.
  * Hq/Hkv in {1,2,4,8}; head_dim 128.
  */
 size_t sym_paged_gqa_decode_workspace_bytes(int B, int Hq, int head_dim, int max_context);
@@ -150,7 +153,7 @@ int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E, fl
  * Segment list for the grouped GEMM: seg_expert/seg_offset/seg_count[0 .. *n_segments) list
  * the experts with at least one row in ascending order, then the shared expert.
  *   bias [E] fp32; E in {64,128,256,512}; E/n_group >= 2 and (E/n_group) % (E/64) == 0;
- *   top_k <= 32; topk_group <= n_group; 1 <= n_logit_parts <= 16.
+ *   top_k <= 32; topk_group <= n_group; 1 <= n_logit_parts <= 4.
  * Output sizes: topk_idx/topk_w/inv_perm [T*top_k]; expert_counts [E]; expert_offsets [E+1];
  * sorted_tokens [T*top_k + T]; seg_* [E+1]; n_segments [1].
  * One launch when T <= 64 (routing and permute in one workgroup), two otherwise.

@@ -15,6 +15,7 @@ import torch.nn.functional as F
 from oracle import route as R
 from oracle.paged_kv import paged_decode_ref
 from tt_symbiote_amd import hip_ops
+from tt_symbiote_amd.modules.kv_cache import HIPPagedAttentionKVCache, PagedAttentionConfig
 from tt_symbiote_amd.workloads import paged_context
 
 pytestmark = pytest.mark.gpu
@@ -300,6 +301,34 @@ def test_paged_decode_block_relabelling_is_bit_exact(device):
     vp2[relabel] = vp
     b = hip_ops.paged_gqa_decode(q, kp2, vp2, relabel[pt.long()].int(), pos, 0.09)
     assert torch.equal(a, b)
+
+
+def test_paged_decode_reused_workspace(device):
+    # A workspace reused across calls and batch sizes (the cache keeps one) gives identical
+    # results: nothing of a previous call's partial results may leak into the next.
+    ctx = paged_context(32, 128, 4096, block_size=32, num_kv_heads=4, seed=11)
+    kp, vp, pt, pos = _dev_ctx(ctx, device)
+    q = torch.randn(32, 16, 128, generator=torch.Generator().manual_seed(12)).bfloat16().to(device)
+    cap = pt.shape[1] * 32
+    need = hip_ops.paged_decode_workspace_bytes(32, 16, cap)
+    ws = torch.full((need,), 0x7F, dtype=torch.uint8, device=device)  # garbage contents
+    ref = paged_decode_ref(q.float().cpu(), ctx.k_pool.float(), ctx.v_pool.float(),
+                           ctx.page_table, ctx.positions, 0.08)
+    first = hip_ops.paged_gqa_decode(q, kp, vp, pt, pos, 0.08, workspace=ws)
+    _close(first, ref)
+    for _ in range(3):
+        again = hip_ops.paged_gqa_decode(q, kp, vp, pt, pos, 0.08, workspace=ws)
+        assert torch.equal(again, first)
+    # the cache-owned workspace, across batch sizes
+    cfg = PagedAttentionConfig(block_size=32, max_num_blocks=kp.shape[0], batch_size=1)
+    cache = HIPPagedAttentionKVCache(1, 4, 128, cfg)
+    cache.to_device(device)
+    cache.key_cache(0).copy_(kp)
+    cache.value_cache(0).copy_(vp)
+    cache.set_vllm_page_table(pt)
+    for bsz in (32, 5, 32, 7):
+        o = cache.paged_sdpa_decode(q[:bsz], 0, pos[:bsz], scale=0.08)
+        torch.testing.assert_close(o, first[:bsz], rtol=0, atol=0)
 
 
 def test_kv_write_and_fill(device):

@@ -30,12 +30,13 @@ namespace sym {
 
 // sigmoid(x) = 1 / (1 + exp(-x)); exp by round(x*log2e) range reduction with a two-part ln2 and a
 // degree-7 Taylor polynomial on |r| <= ln2/2 (relative error < 6e-8), scaled by ldexp.
+// Branch-free: the argument is clamped to [-88.5, 88.5] and the saturated results are selected
+// afterwards (0 for -x > 88.5, 1 for -x < -88.5), the same values as a branchy evaluation.
 __device__ __forceinline__ float route_sigmoid(float x) {
-  float z = -x;
-  if (z > 88.5f) return 0.0f;
-  if (z < -88.5f) return 1.0f;
-  float n = rintf(z * 1.44269502f);
-  float r = fmaf(n, -0.693145752f, z);
+  const float z = -x;
+  const float zc = fminf(fmaxf(z, -88.5f), 88.5f);
+  const float n = rintf(zc * 1.44269502f);
+  float r = fmaf(n, -0.693145752f, zc);
   r = fmaf(n, -1.42860677e-06f, r);
   float p = fmaf(r, 1.98412698e-04f, 1.38888889e-03f);
   p = fmaf(p, r, 8.33333333e-03f);
@@ -44,8 +45,9 @@ __device__ __forceinline__ float route_sigmoid(float x) {
   p = fmaf(p, r, 0.5f);
   p = fmaf(p, r, 1.0f);
   p = fmaf(p, r, 1.0f);
-  float e = ldexpf(p, (int)n);
-  return 1.0f / (1.0f + e);
+  const float e = ldexpf(p, (int)n);
+  const float sg = 1.0f / (1.0f + e);
+  return z > 88.5f ? 0.0f : (z < -88.5f ? 1.0f : sg);
 }
 
 // Order-preserving map float -> uint32 (larger float -> larger uint); -0.0 is folded onto +0.0.
@@ -108,34 +110,45 @@ __device__ __forceinline__ void top2_merge(float& t1, float& t2, float o1, float
 // Route one token with the calling wave (all 64 lanes). Lane l owns experts l*EPL .. l*EPL+EPL-1.
 // The partner patterns used for the group top-2 (xor 1, xor 2, half mirror, mirror, then xor 16
 // and xor 32) always pair disjoint lane sets, so no expert is counted twice.
+// Logits of token t for this lane's experts: all partial sums loaded unconditionally (one
+// batch of EPL * n_parts loads), then added left to right.
 template <int EPL>
-__device__ __forceinline__ void route_token(const float* __restrict__ logits, int n_parts,
-                                            size_t part_stride, const float* bv, int t, int E,
-                                            int n_group, int topk_group, int top_k,
-                                            float routed_scale, int renorm, int lane, int& my_idx,
-                                            float& my_w) {
+__device__ __forceinline__ void load_token_logits(const float* __restrict__ logits, int n_parts,
+                                                  size_t part_stride, int t, int E, int lane,
+                                                  float (&parts)[kLogitParts][EPL]) {
+#pragma unroll
+  for (int q = 0; q < kLogitParts; ++q)
+#pragma unroll
+    for (int j = 0; j < EPL; ++j)
+      parts[q][j] = q < n_parts ? logits[q * part_stride + (size_t)t * E + lane * EPL + j] : 0.f;
+}
+
+template <int EPL>
+__device__ __forceinline__ void route_token(const float (&parts)[kLogitParts][EPL], int n_parts,
+                                            const float* bv, int E, int n_group, int topk_group,
+                                            int top_k, float routed_scale, int renorm, int lane,
+                                            int& my_idx, float& my_w) {
   const int gsz = E / n_group;
   const int lpg = gsz / EPL;
   const int my_group = lane / lpg;
   float s[EPL], c[EPL];
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
-    const size_t o = (size_t)t * E + lane * EPL + j;
-    float x = logits[o];
-    for (int q = 1; q < n_parts; ++q) x = x + logits[q * part_stride + o];
+    float x = parts[0][j];
+#pragma unroll
+    for (int q = 1; q < kLogitParts; ++q) {
+      if (q < n_parts) x = x + parts[q][j];
+    }
     s[j] = route_sigmoid(x);
     c[j] = s[j] + bv[j];
   }
+  // largest and second largest c of this lane (branch-free; same values as a running update)
   float t1 = -INFINITY, t2 = -INFINITY;
 #pragma unroll
   for (int j = 0; j < EPL; ++j) {
     const float v = c[j];
-    if (v > t1) {
-      t2 = t1;
-      t1 = v;
-    } else if (v > t2) {
-      t2 = v;
-    }
+    t2 = fmaxf(t2, fminf(t1, v));
+    t1 = fmaxf(t1, v);
   }
   if (lpg >= 2) top2_merge(t1, t2, dppf<kDppXor1>(t1), dppf<kDppXor1>(t2));
   if (lpg >= 4) top2_merge(t1, t2, dppf<kDppXor2>(t1), dppf<kDppXor2>(t2));
@@ -325,12 +338,22 @@ __global__ __launch_bounds__(kRouteThreads) void moe_route_chunk_kernel(
   const int ntok = min(kChunk, T - tok0);
   const size_t part_stride = (size_t)T * E;
 
+  // each wave routes tokens wave, wave + nwaves, ...; the next token's logits are loaded
+  // while the current one is routed
+  float cur[kLogitParts][EPL], nxt[kLogitParts][EPL];
+  if (wave < ntok) load_token_logits<EPL>(logits, n_parts, part_stride, tok0 + wave, E, lane, cur);
   for (int tl = wave; tl < ntok; tl += nwaves) {
     const int t = tok0 + tl;
+    if (tl + nwaves < ntok)
+      load_token_logits<EPL>(logits, n_parts, part_stride, t + nwaves, E, lane, nxt);
     int my_idx;
     float my_w;
-    route_token<EPL>(logits, n_parts, part_stride, bv, t, E, n_group, topk_group, top_k,
-                     routed_scale, renorm, lane, my_idx, my_w);
+    route_token<EPL>(cur, n_parts, bv, E, n_group, topk_group, top_k, routed_scale, renorm,
+                     lane, my_idx, my_w);
+#pragma unroll
+    for (int q = 0; q < kLogitParts; ++q)
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) cur[q][j] = nxt[q][j];
     if (lane < top_k) {
       topk_idx[(size_t)t * top_k + lane] = my_idx;
       topk_w[(size_t)t * top_k + lane] = my_w;
@@ -459,8 +482,8 @@ extern "C" int sym_moe_route_permute(const float* logits, int n_logit_parts, con
                   sorted_tokens && inv_perm && seg_expert && seg_offset && seg_count &&
                   n_segments && workspace,
               SYM_ERR_INVALID, "moe_route_permute: null pointer argument");
-  SYM_REQUIRE(n_logit_parts >= 1 && n_logit_parts <= 16, SYM_ERR_INVALID,
-              "moe_route_permute: n_logit_parts=%d out of [1,16]", n_logit_parts);
+  SYM_REQUIRE(n_logit_parts >= 1 && n_logit_parts <= kLogitParts, SYM_ERR_INVALID,
+              "moe_route_permute: n_logit_parts=%d out of [1,%d]", n_logit_parts, kLogitParts);
   SYM_REQUIRE(E == 64 || E == 128 || E == 256 || E == 512, SYM_ERR_UNSUPPORTED,
               "moe_route_permute: E=%d not in {64,128,256,512}", E);
   SYM_REQUIRE(n_group >= 1 && E % n_group == 0, SYM_ERR_INVALID,

@@ -11,15 +11,13 @@
 //   split-half form TorchRotaryPositionEmbedding (ttnn_rope.py:23-62), partial rotary on the
 //   first rotary_dim dims, inv_freq = theta^-(2i/rotary_dim) (ttnn_rope.py:304).
 //
-// Decode kernel design (gfx950): split-K ("flash decoding"). One workgroup (4 waves) owns one
-// (sequence, kv head, 256-token split): it loads the G = Hq/Hkv query heads of that kv head once
-// and streams the split's K then V rows exactly once. A K/V row of 128 bf16 is 256 contiguous
-// bytes; 16 lanes x 16 bytes cover a row, so one wave-wide load covers 4 consecutive tokens of
-// a block (1 KB contiguous). QK dots reduce over the 16 lanes of a token with xor shuffles;
-// scores live in LDS (G x 256 fp32), softmax statistics are workgroup reductions, and P.V
-// accumulates per lane in registers with a final cross-lane/cross-wave reduction. Each split
-// writes an unnormalised partial output and its (max, sum) in the log2 domain; a merge kernel
-// combines the splits with the log-sum-exp rule. Splits past a sequence's length exit at once.
+// Decode kernel design (gfx950): split-K ("flash decoding"). One workgroup
+// (4 waves) owns one (sequence, kv head, 256-token split): it loads the G = Hq/Hkv query heads
+// of that kv head once and streams the split's K and V rows exactly once, all loads issued up
+// front. Scores come from MFMA (query heads as the rows of the A operand), live in LDS
+// (G x 256 fp32) for the workgroup softmax, and P.V accumulates per lane on the VALU. A merge
+// kernel combines the splits of each sequence with the log-sum-exp rule. Splits past a
+// sequence's length exit at once.
 #include "common.h"
 
 namespace sym {
@@ -152,96 +150,104 @@ __global__ __launch_bounds__(256) void paged_kv_fill_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
+// Split-K decode. Workgroup = (split of 256 tokens, kv head g, sequence b), 4 waves x 64 tokens.
+//   QK^T on MFMA: per 16-token tile, S[head][token] = Q[16 x 128] . K^T[128 x 16] as four
+//   v_mfma_f32_16x16x32_bf16 (query heads are rows 0..G-1 of the A operand; lane l streams
+//   dims 8*(l/16) + 32*j of token l%16, so one wave-wide load covers 64 contiguous bytes of 16
+//   K rows). P.V on the VALU: a lane owns 8 dims of one token per step (16 lanes per token).
+//   All K and V loads of the wave are issued before the first use.
+// Each split writes its unnormalised output and (max, sum) in the log2 domain for the merge
+// kernel; a sequence with a single split writes its normalised output directly. (Merging in the
+// last split to finish would need a device-scope release per workgroup; on this chip that
+// writes back the XCD's L2 each time and costs more than the separate merge launch.)
 template <int G>
-__global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
+__global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ positions, int Hkv, int block_size, int mbps, int num_blocks,
-    float scale_log2, float* __restrict__ ws_o, float* __restrict__ ws_ml, int max_splits) {
+    int max_context, float scale_log2, float* __restrict__ ws_o, float* __restrict__ ws_ml,
+    int max_splits, uint16_t* __restrict__ out) {
   constexpr int D = kHeadDim;
-  __shared__ float s_q[G][D];
   __shared__ float s_p[G][kSplit];
   __shared__ float s_red[4][G][D];
   __shared__ float s_stat[G][4];
-  __shared__ int s_bt[kSplit];   // physical block of each token (always a valid block)
-  __shared__ int s_ok[kSplit];   // token is inside the split and its page-table entry is valid
+  __shared__ float s_fin[2][G];
+  __shared__ unsigned s_row[kSplit];  // K/V pool row of each token (always an in-bounds row)
+  __shared__ int s_ok[kSplit];        // token is inside the split and its page-table entry is valid
 
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int Hq = Hkv * G;
-  const int ctx = positions[b] + 1;
+  const int tid = threadIdx.x;
+  const int ctx = min(positions[b] + 1, max_context);
+  if (ctx <= 0) {
+    // nothing cached (position < 0): the output is zero
+    if (split == 0)
+      for (int i = tid; i < G * D; i += kAttnThreads)
+        out[((size_t)b * Hq + g * G) * D + i] = 0;
+    return;
+  }
   const int t0 = split * kSplit;
   if (t0 >= ctx) return;
   const int t1 = min(ctx, t0 + kSplit);
-  const int tid = threadIdx.x;
+  const int nsplit = (ctx + kSplit - 1) / kSplit;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int sub = lane & 15;  // 8 dims: sub*8 .. sub*8+7
-  const int tq = lane >> 4;   // token within a group of 4
+  const int r16 = lane & 15;
+  const int kg = lane >> 4;
 
-  for (int i = tid; i < G * D; i += kAttnThreads) {
-    const int h = i / D, d = i - h * D;
-    s_q[h][d] = bf16_to_f32(q[((size_t)b * Hq + g * G + h) * D + d]) * scale_log2;
-  }
-  // Physical block of every token of the split. Tokens past the sequence read the split's
-  // last valid token instead (an in-bounds row already being loaded) and are masked out, so
-  // every K/V load below is unconditional.
   {
+    // Pool row of every token of the split. Tokens past the sequence read the split's last
+    // token instead, and tokens of an invalid page-table entry read block 0, so every K/V load
+    // below is unconditional and in bounds; both are masked out of the softmax.
     const int t = t0 + tid;
     const int tc = min(t, t1 - 1);
     const int blk = tc / block_size;
-    int p = blk < mbps ? block_tables[(size_t)b * mbps + blk] : -1;
-    const bool valid = t < t1 && p >= 0 && p < num_blocks;
-    if (p < 0 || p >= num_blocks) p = 0;
-    s_bt[tid] = p;
+    int pb = blk < mbps ? block_tables[(size_t)b * mbps + blk] : -1;
+    const bool valid = t < t1 && pb >= 0 && pb < num_blocks;
+    if (pb < 0 || pb >= num_blocks) pb = 0;
+    s_row[tid] = (unsigned)(((size_t)pb * Hkv + g) * block_size + (tc - blk * block_size));
     s_ok[tid] = valid;
+  }
+  // query fragments (A operand): head r16 (rows >= G are zero), dims 8*kg + 32*j
+  uint4 qa[4];
+  {
+    const uint16_t* qr = q + ((size_t)b * Hq + g * G + min(r16, G - 1)) * D + 8 * kg;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 32 * j);
+      qa[j] = r16 < G ? v : make_uint4(0, 0, 0, 0);
+    }
   }
   __syncthreads();
 
-  float qr[G][8];
+  auto row_offset = [&](int tl) -> size_t { return (size_t)s_row[tl] * D; };
+  // K in the MFMA B layout: tile tt of 16 tokens, token r16, dims 8*kg + 32*j
+  uint4 kb[4][4];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int tt = 0; tt < 4; ++tt) {
+    const uint16_t* kr = k_pool + row_offset(wave * 64 + tt * 16 + r16) + 8 * kg;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) qr[h][i] = s_q[h][sub * 8 + i];
-
-  // Issue every K and V load of this wave's 64 tokens up front (16 + 16 loads of 16 bytes per
-  // lane); V arrives while the scores and the softmax statistics are computed.
-  uint4 kreg[16], vreg[16];
-  size_t roff[16];
-#pragma unroll
-  for (int it = 0; it < 16; ++it) {
-    const int tl = wave * 64 + it * 4 + tq;
-    const int tc = min(t0 + tl, t1 - 1);
-    roff[it] = (((size_t)s_bt[tl] * Hkv + g) * block_size + (tc - (tc / block_size) * block_size)) *
-                   D + sub * 8;
+    for (int j = 0; j < 4; ++j) kb[tt][j] = *reinterpret_cast<const uint4*>(kr + 32 * j);
   }
+  // V for P.V: step it covers tokens it*4 + kg (4 per step), lane r16 owns dims r16*8 .. +8
+  uint4 vreg[16];
 #pragma unroll
-  for (int it = 0; it < 16; ++it) kreg[it] = *reinterpret_cast<const uint4*>(k_pool + roff[it]);
-#pragma unroll
-  for (int it = 0; it < 16; ++it) vreg[it] = *reinterpret_cast<const uint4*>(v_pool + roff[it]);
+  for (int it = 0; it < 16; ++it)
+    vreg[it] = *reinterpret_cast<const uint4*>(v_pool + row_offset(wave * 64 + it * 4 + kg) +
+                                               r16 * 8);
 
-  // ---- scores ----
+  // ---- scores on MFMA ----
 #pragma unroll
-  for (int it = 0; it < 16; ++it) {
-    const int tl = wave * 64 + it * 4 + tq;
-    float kf[8];
-    unpack8(kreg[it], kf);
-    float dot[G];
+  for (int tt = 0; tt < 4; ++tt) {
+    floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      float d = 0.f;
+    for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(qa[j], kb[tt][j], sacc);
+    const int tl = wave * 64 + tt * 16 + r16;
+    const bool valid = s_ok[tl] != 0;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) d = fmaf(qr[h][i], kf[i], d);
-      dot[h] = d;
-    }
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-#pragma unroll
-      for (int o = 8; o > 0; o >>= 1) dot[h] += __shfl_xor(dot[h], o);
-    }
-    if (sub == 0) {
-      const bool valid = s_ok[tl] != 0;
-#pragma unroll
-      for (int h = 0; h < G; ++h) s_p[h][tl] = valid ? dot[h] : -INFINITY;
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kg + i;
+      if (h < G) s_p[h][tl] = valid ? sacc[i] * scale_log2 : -INFINITY;
     }
   }
   __syncthreads();
@@ -261,9 +267,9 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const float v = s_p[h][tid];
-    const float p = (mx[h] == -INFINITY || v == -INFINITY) ? 0.f : exp2f(v - mx[h]);
-    s_p[h][tid] = p;
-    const float l = wave_sum(p);
+    const float pr = (mx[h] == -INFINITY || v == -INFINITY) ? 0.f : exp2f(v - mx[h]);
+    s_p[h][tid] = pr;
+    const float l = wave_sum(pr);
     if (lane == 0) s_stat[h][wave] = l;
   }
   __syncthreads();
@@ -276,14 +282,14 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
     for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
 #pragma unroll
   for (int it = 0; it < 16; ++it) {
-    const int tl = wave * 64 + it * 4 + tq;
+    const int tl = wave * 64 + it * 4 + kg;
     float vf[8];
     unpack8(vreg[it], vf);
 #pragma unroll
     for (int h = 0; h < G; ++h) {
-      const float p = s_p[h][tl];
+      const float pr = s_p[h][tl];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(p, vf[i], acc[h][i]);
+      for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(pr, vf[i], acc[h][i]);
     }
   }
 #pragma unroll
@@ -295,45 +301,91 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_split_kernel(
       v += __shfl_xor(v, 32);
       acc[h][i] = v;
     }
-  if (tq == 0) {
+  if (kg == 0) {
 #pragma unroll
     for (int h = 0; h < G; ++h)
 #pragma unroll
-      for (int i = 0; i < 8; ++i) s_red[wave][h][sub * 8 + i] = acc[h][i];
+      for (int i = 0; i < 8; ++i) s_red[wave][h][r16 * 8 + i] = acc[h][i];
+  }
+  if (tid < G) {
+    s_fin[0][tid] = mx[tid];
+    s_fin[1][tid] = (s_stat[tid][0] + s_stat[tid][1]) + (s_stat[tid][2] + s_stat[tid][3]);
   }
   __syncthreads();
+
+  if (nsplit == 1) {
+    for (int i = tid; i < G * D; i += kAttnThreads) {
+      const int h = i / D, d = i - h * D;
+      const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
+      const float L = s_fin[1][h];
+      out[((size_t)b * Hq + g * G + h) * D + d] = f32_to_bf16(L > 0.f ? o / L : 0.f);
+    }
+    return;
+  }
+
+  // this split's unnormalised output and (max, sum); the merge kernel combines the splits
   for (int i = tid; i < G * D; i += kAttnThreads) {
     const int h = i / D, d = i - h * D;
     const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
     ws_o[(((size_t)b * Hq + g * G + h) * max_splits + split) * D + d] = o;
   }
   if (tid < G) {
-    const float l = (s_stat[tid][0] + s_stat[tid][1]) + (s_stat[tid][2] + s_stat[tid][3]);
     float* ml = ws_ml + (((size_t)b * Hq + g * G + tid) * max_splits + split) * 2;
-    ml[0] = mx[tid];
-    ml[1] = l;
+    ml[0] = s_fin[0][tid];
+    ml[1] = s_fin[1][tid];
   }
 }
 
-__global__ __launch_bounds__(kHeadDim) void paged_decode_merge_kernel(
+// Merge of the splits of a sequence with more than one split (log-sum-exp rule), one wave per
+// (sequence, query head): lane l owns dims 2l, 2l+1; the split weights 2^(m_s - M) are computed
+// one split per lane and broadcast, and the partial-output loads of 8 splits are issued at once.
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-    const int32_t* __restrict__ positions, int Hq, int max_splits, uint16_t* __restrict__ out) {
-  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const int ctx = positions[b] + 1;
-  const int ns = min(max_splits, max(0, (ctx + kSplit - 1) / kSplit));
-  const size_t base = ((size_t)b * Hq + h) * max_splits;
+    const int32_t* __restrict__ positions, int B, int Hq, int max_context, int max_splits,
+    uint16_t* __restrict__ out) {
+  constexpr int D = kHeadDim;
+  const int lane = threadIdx.x & 63;
+  const int idx = blockIdx.x * 4 + (threadIdx.x >> 6);  // b * Hq + head
+  if (idx >= B * Hq) return;
+  const int ctx = min(positions[idx / Hq] + 1, max_context);
+  const int nsplit = ctx <= 0 ? 0 : (ctx + kSplit - 1) / kSplit;
+  if (nsplit <= 1) return;  // written directly by the split kernel
+  const float2* ml = reinterpret_cast<const float2*>(ws_ml) + (size_t)idx * max_splits;
+  const float2* po = reinterpret_cast<const float2*>(ws_o) + (size_t)idx * max_splits * (D / 2) + lane;
   float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = fmaxf(M, ws_ml[(base + s) * 2]);
-  float L = 0.f, o = 0.f;
-  if (M != -INFINITY) {
-    for (int s = 0; s < ns; ++s) {
-      const float m = ws_ml[(base + s) * 2];
-      const float w = m == -INFINITY ? 0.f : exp2f(m - M);
-      L += w * ws_ml[(base + s) * 2 + 1];
-      o += w * ws_o[(base + s) * kHeadDim + d];
+  for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, ml[s].x);
+  M = wave_max(M);
+  float L = 0.f, ox = 0.f, oy = 0.f;
+  for (int c = 0; c < nsplit; c += 64) {
+    float w = 0.f;
+    if (c + lane < nsplit) {
+      const float2 v = ml[c + lane];
+      w = (v.x == -INFINITY) ? 0.f : exp2f(v.x - M);
+      L = fmaf(w, v.y, L);
+    }
+    const int n = min(64, nsplit - c);
+    int j = 0;
+    for (; j + 8 <= n; j += 8) {
+      float2 pv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) pv[u] = po[(size_t)(c + j + u) * (D / 2)];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        const float wj = __shfl(w, j + u);
+        ox = fmaf(wj, pv[u].x, ox);
+        oy = fmaf(wj, pv[u].y, oy);
+      }
+    }
+    for (; j < n; ++j) {
+      const float2 pv = po[(size_t)(c + j) * (D / 2)];
+      const float wj = __shfl(w, j);
+      ox = fmaf(wj, pv.x, ox);
+      oy = fmaf(wj, pv.y, oy);
     }
   }
-  out[((size_t)b * Hq + h) * kHeadDim + d] = f32_to_bf16(L > 0.f ? o / L : 0.f);
+  L = wave_sum(L);
+  reinterpret_cast<uint32_t*>(out)[(size_t)idx * (D / 2) + lane] =
+      L > 0.f ? pack_bf16x2(ox / L, oy / L) : 0u;
 }
 
 }  // namespace sym
@@ -347,6 +399,9 @@ static int check_cache_args(const char* what, int B, int Hkv, int head_dim, int 
               what, B, Hkv, block_size, mbps, num_blocks);
   SYM_REQUIRE(head_dim == kHeadDim, SYM_ERR_UNSUPPORTED, "%s: head_dim=%d (only 128)", what,
               head_dim);
+  SYM_REQUIRE((unsigned long long)num_blocks * Hkv * block_size <= 0xFFFFFFFFull,
+              SYM_ERR_UNSUPPORTED, "%s: pool of %llu rows per K/V (at most 2^32 - 1)", what,
+              (unsigned long long)num_blocks * Hkv * block_size);
   return SYM_OK;
 }
 
@@ -427,7 +482,8 @@ extern "C" size_t sym_paged_gqa_decode_workspace_bytes(int B, int Hq, int head_d
                                                        int max_context) {
   if (B <= 0 || Hq <= 0 || head_dim <= 0 || max_context <= 0) return 0;
   const size_t splits = (size_t)(max_context + kSplit - 1) / kSplit;
-  return (size_t)B * Hq * splits * ((size_t)head_dim + 2) * sizeof(float) + 256;
+  // partial outputs and (max, sum) of every split
+  return (size_t)B * Hq * splits * ((size_t)head_dim + 2) * sizeof(float);
 }
 
 extern "C" int sym_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
@@ -465,9 +521,9 @@ extern "C" int sym_paged_gqa_decode(const void* q, const void* k_pool, const voi
   const uint16_t* kp = (const uint16_t*)k_pool;
   const uint16_t* vp = (const uint16_t*)v_pool;
 #define SYM_LAUNCH_DECODE(GG)                                                                   \
-  hipLaunchKernelGGL(paged_decode_split_kernel<GG>, grid, block, 0, s, qq, kp, vp, block_tables, \
-                     positions, Hkv, block_size, max_blocks_per_seq, num_blocks, scale_log2, ws_o, \
-                     ws_ml, max_splits)
+  hipLaunchKernelGGL(paged_decode_kernel<GG>, grid, block, 0, s, qq, kp, vp, block_tables,       \
+                     positions, Hkv, block_size, max_blocks_per_seq, num_blocks, max_context,    \
+                     scale_log2, ws_o, ws_ml, max_splits, (uint16_t*)out)
   switch (G) {
     case 1: SYM_LAUNCH_DECODE(1); break;
     case 2: SYM_LAUNCH_DECODE(2); break;
@@ -475,9 +531,9 @@ extern "C" int sym_paged_gqa_decode(const void* q, const void* k_pool, const voi
     default: SYM_LAUNCH_DECODE(8); break;
   }
 #undef SYM_LAUNCH_DECODE
-  rc = sym_host::check_launch("paged_decode_split_kernel");
-  if (rc) return rc;
-  hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(Hq, B), dim3(kHeadDim), 0, s, ws_o, ws_ml,
-                     positions, Hq, max_splits, (uint16_t*)out);
+  rc = sym_host::check_launch("paged_decode_kernel");
+  if (rc || max_splits == 1) return rc;
+  hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((B * Hq + 3) / 4), dim3(256), 0, s, ws_o,
+                     ws_ml, positions, B, Hq, max_context, max_splits, (uint16_t*)out);
   return sym_host::check_launch("paged_decode_merge_kernel");
 }

@@ -243,6 +243,7 @@ def paged_decode_workspace_bytes(batch: int, num_heads: int, max_context: int) -
                       max_context)
 
 
+
 def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                      block_tables: torch.Tensor, positions: torch.Tensor, scale: float,
                      max_context: Optional[int] = None, workspace: Optional[torch.Tensor] = None,

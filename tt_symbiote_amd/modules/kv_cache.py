@@ -207,6 +207,7 @@ class HIPPagedAttentionKVCache(_CacheBase):
         self._advance(layer_idx, 1)
 
     def decode_workspace(self, batch: int, num_heads: int) -> torch.Tensor:
+        """Per-split partial results of the decode kernel (grown on demand, reused)."""
         need = hip_ops.paged_decode_workspace_bytes(batch, num_heads, self.max_context)
         if self._decode_ws is None or self._decode_ws.numel() < need:
             self._decode_ws = torch.empty(need, dtype=torch.uint8, device=self._device)
