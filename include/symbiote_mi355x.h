@@ -156,7 +156,9 @@ int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E, fl
  *   top_k <= 32; topk_group <= n_group; 1 <= n_logit_parts <= 4.
  * Output sizes: topk_idx/topk_w/inv_perm [T*top_k]; expert_counts [E]; expert_offsets [E+1];
  * sorted_tokens [T*top_k + T]; seg_* [E+1]; n_segments [1].
- * One launch when T <= 64 (routing and permute in one workgroup), two otherwise.
+ * Two launches: routing (one wave per token) and the permute (one workgroup).
+ * workspace: sym_moe_route_workspace_bytes() is 0 (state lives in LDS); the arguments stay
+ * for interface stability and may be NULL / 0.
  */
 size_t sym_moe_route_workspace_bytes(int T, int E);
 int sym_moe_route_permute(const float* logits, int n_logit_parts, const float* bias, int T, int E,

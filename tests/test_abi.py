@@ -32,9 +32,9 @@ def test_workspace_queries():
     q = _lib.query
     assert q("sym_paged_gqa_decode_workspace_bytes", 32, 16, 128, 4128) >= 32 * 16 * 17 * 130 * 4
     assert q("sym_paged_gqa_decode_workspace_bytes", 0, 16, 128, 100) == 0
-    assert q("sym_moe_route_workspace_bytes", 32, 256) >= 256 * 16
-    assert q("sym_moe_route_workspace_bytes", 65, 256) >= 2 * 256 * 16
-    assert q("sym_moe_route_workspace_bytes", 0, 256) == 0
+    # routing keeps its intermediate state in LDS: no workspace at any size
+    assert q("sym_moe_route_workspace_bytes", 32, 256) == 0
+    assert q("sym_moe_route_workspace_bytes", 4096, 256) == 0
 
 
 def _call(name, *args):
@@ -73,8 +73,6 @@ def test_route_rejects_bad_configs():
     assert _call("sym_moe_route_permute", *args(4, 256, 8, 4, 33))[0] == 1    # top_k
     assert _call("sym_moe_route_permute", *args(4, 64, 64, 4, 2))[0] == 2     # group of 1
     assert _call("sym_moe_route_permute", *args(4, 64, 8, 1, 9))[0] == 1      # k > kept experts
-    rc, msg = _call("sym_moe_route_permute", *args(4, 256, 8, 4, 8)[:22], 8, None)
-    assert rc == 3 and "workspace" in msg
     bad_parts = list(args(4, 256, 8, 4, 8))
     bad_parts[1] = 0
     assert _call("sym_moe_route_permute", *bad_parts)[0] == 1

@@ -7,18 +7,16 @@
 //
 // Design (gfx950, wave64):
 //   router logits: fp32 MFMA (16x16x4) GEMM writing four partial sums over quarters of H.
-//   route kernel (one workgroup per chunk of 64 tokens, one wave per token at a time): each lane
-//     owns E/64 consecutive experts, so a group of E/n_group experts spans a power-of-two run of
-//     lanes. Group top-2 merges partners through DPP row operations; group ranking reads the
-//     n_group scores with readlane; the final top-k is k rounds of a wave-wide max over 64-bit
-//     keys (order-preserving float bits << 32 | (0xFFFF - expert)) -- DPP inside each 16-lane
-//     row, readlane across rows -- which makes ties pick the lower expert index. The chunk's
-//     routing is folded into one 64-bit token mask per expert (LDS atomic OR, order
-//     independent).
-//   permute (same workgroup when there is one chunk, else one extra workgroup): per-expert
-//     prefix over chunks, exclusive scan over experts, then every assignment's row = expert
-//     offset + earlier chunks + popcount of earlier tokens in its own chunk mask. The result does
-//     not depend on scheduling order: bit-exact across runs.
+//   route kernel (one wave per token, four tokens per workgroup): each lane owns E/64
+//     consecutive experts, so a group of E/n_group experts spans a power-of-two run of lanes.
+//     Group top-2 merges partners through DPP row operations; group ranking reads the n_group
+//     scores with readlane; the final top-k is k rounds of a wave-wide max of order-preserving
+//     value bits (DPP inside each 16-lane row, readlane across rows) followed by a ballot for
+//     the lowest lane holding it, so ties pick the lower expert index.
+//   permute kernel (one workgroup): per-expert counts and offsets, then each chunk of 64
+//     tokens folded into one 64-bit token mask per expert (LDS atomic OR, order independent);
+//     every assignment's row = expert offset + earlier chunks + popcount of earlier tokens in
+//     its own chunk mask. The result does not depend on scheduling order: bit-exact across runs.
 //
 // Floating point: contraction is disabled in this file so the sigmoid below (own Cody-Waite exp,
 // explicit fma) and every add/divide are the IEEE operations the CPU oracle performs.
@@ -56,8 +54,6 @@ __device__ __forceinline__ uint32_t order_bits(float v) {
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
 }
 
-constexpr int kChunk = 64;      // tokens per chunk (one bit each in a u64 mask)
-constexpr int kRouteThreads = 1024;
 constexpr int kMaxTopK = 32;
 constexpr int kLogitParts = 4;  // partial sums written by the router-logits kernel
 
@@ -74,30 +70,6 @@ constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within each 16
 template <int CTRL>
 __device__ __forceinline__ float dppf(float v) {
   return __uint_as_float(dpp32<CTRL>(__float_as_uint(v)));
-}
-template <int CTRL>
-__device__ __forceinline__ unsigned long long dpp64(unsigned long long v) {
-  const uint32_t lo = dpp32<CTRL>((uint32_t)v);
-  const uint32_t hi = dpp32<CTRL>((uint32_t)(v >> 32));
-  return ((unsigned long long)hi << 32) | lo;
-}
-__device__ __forceinline__ unsigned long long readlane64(unsigned long long v, int lane) {
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(v >> 32), lane);
-  return ((unsigned long long)hi << 32) | lo;
-}
-__device__ __forceinline__ unsigned long long umax64(unsigned long long a, unsigned long long b) {
-  return a > b ? a : b;
-}
-// Maximum over the 64 lanes (uniform result): within each 16-lane row with DPP, then across the
-// four rows with readlane.
-__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v) {
-  v = umax64(v, dpp64<kDppXor1>(v));
-  v = umax64(v, dpp64<kDppXor2>(v));
-  v = umax64(v, dpp64<kDppHalfMirror>(v));
-  v = umax64(v, dpp64<kDppMirror>(v));
-  return umax64(umax64(readlane64(v, 0), readlane64(v, 16)),
-                umax64(readlane64(v, 32), readlane64(v, 48)));
 }
 // (t1, t2) <- the two largest of the union of this lane's pair and the partner's pair.
 __device__ __forceinline__ void top2_merge(float& t1, float& t2, float o1, float o2) {
@@ -165,39 +137,46 @@ __device__ __forceinline__ void route_token(const float (&parts)[kLogitParts][EP
   }
   const bool keep = rank < topk_group;
 
-  unsigned long long key[EPL];
+  // top-k over the kept experts: k rounds of (largest value, lowest expert index on ties).
+  // Round: wave max of the order-preserving value bits (DPP in rows, readlane across rows),
+  // then the lowest lane holding that value (ballot + find-first-one) and the lowest of its
+  // experts with it; that expert's value is cleared to 0 (below every real value's bits).
+  uint32_t kv[EPL];
 #pragma unroll
-  for (int j = 0; j < EPL; ++j) {
-    const float m = keep ? c[j] : 0.0f;
-    key[j] = ((unsigned long long)order_bits(m) << 32) |
-             (unsigned long long)(0xFFFFu - (uint32_t)(lane * EPL + j));
-  }
+  for (int j = 0; j < EPL; ++j) kv[j] = order_bits(keep ? c[j] : 0.0f);
   float denom = 0.0f;
   my_idx = 0;
   my_w = 0.0f;
   for (int k = 0; k < top_k; ++k) {
-    unsigned long long best = 0ull;
+    uint32_t lb = kv[0];
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) best = umax64(best, key[j]);
-    best = wave_max_u64(best);
-    const int e = (int)(0xFFFFu - (uint32_t)(best & 0xFFFFull));
-    const int owner = e / EPL;
-    const int jj = e - owner * EPL;
-    float sv = 0.0f;
+    for (int j = 1; j < EPL; ++j) lb = max(lb, kv[j]);
+    uint32_t m = max(lb, dpp32<kDppXor1>(lb));
+    m = max(m, dpp32<kDppXor2>(m));
+    m = max(m, dpp32<kDppHalfMirror>(m));
+    m = max(m, dpp32<kDppMirror>(m));
+    const uint32_t best =
+        max(max((uint32_t)__builtin_amdgcn_readlane((int)m, 0),
+                (uint32_t)__builtin_amdgcn_readlane((int)m, 16)),
+            max((uint32_t)__builtin_amdgcn_readlane((int)m, 32),
+                (uint32_t)__builtin_amdgcn_readlane((int)m, 48)));
+    const unsigned long long holders = __ballot(lb == best);
+    const int owner = __ffsll((long long)holders) - 1;
+    int jl = EPL - 1;
 #pragma unroll
-    for (int j = 0; j < EPL; ++j) {
-      if (j == jj) sv = s[j];
-    }
+    for (int j = EPL - 2; j >= 0; --j) jl = kv[j] == best ? j : jl;
+    float sl = s[0];
+#pragma unroll
+    for (int j = 1; j < EPL; ++j) sl = jl == j ? s[j] : sl;
+    const int jj = __builtin_amdgcn_readlane(jl, owner);
+    const float sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sl), owner));
     if (lane == owner) {
 #pragma unroll
-      for (int j = 0; j < EPL; ++j) {
-        if (j == jj) key[j] = 0ull;
-      }
+      for (int j = 0; j < EPL; ++j) kv[j] = j == jj ? 0u : kv[j];
     }
-    sv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(sv), owner));
     denom = denom + sv;
     if (lane == k) {
-      my_idx = e;
+      my_idx = owner * EPL + jj;
       my_w = sv;
     }
   }
@@ -208,7 +187,32 @@ __device__ __forceinline__ void route_token(const float (&parts)[kLogitParts][EP
   my_w = my_w * routed_scale;
 }
 
-// Exclusive scan of one int per thread over a workgroup of up to 1024 threads.
+// Routes one token per wave (four per workgroup): writes the token's top-k experts (in
+// selection order) and their weights.
+template <int EPL>
+__global__ __launch_bounds__(256) void moe_route_kernel(
+    const float* __restrict__ logits, int n_parts, const float* __restrict__ bias, int T, int E,
+    int n_group, int topk_group, int top_k, float routed_scale, int renorm,
+    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  float parts[kLogitParts][EPL];
+  load_token_logits<EPL>(logits, n_parts, (size_t)T * E, t, E, lane, parts);
+  float bv[EPL];
+#pragma unroll
+  for (int j = 0; j < EPL; ++j) bv[j] = bias[lane * EPL + j];
+  int my_idx;
+  float my_w;
+  route_token<EPL>(parts, n_parts, bv, E, n_group, topk_group, top_k, routed_scale, renorm, lane,
+                   my_idx, my_w);
+  if (lane < top_k) {
+    topk_idx[(size_t)t * top_k + lane] = my_idx;
+    topk_w[(size_t)t * top_k + lane] = my_w;
+  }
+}
+
+// Exclusive scan of one int per thread over the workgroup (up to 1024 threads).
 __device__ int block_exclusive_scan(int v, int* s_wave, int* total) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -237,162 +241,99 @@ __device__ int block_exclusive_scan(int v, int* s_wave, int* total) {
   return before + x - v;
 }
 
-// Counting-sort permute of all assignments, by one workgroup. `mask(c, e)` / `cnt(c, e)` give
-// chunk c's token bitmask and count for expert e.
-struct PermuteOut {
-  int32_t* expert_counts;
-  int32_t* expert_offsets;
-  int32_t* sorted_tokens;
-  int32_t* inv_perm;
-  int32_t* seg_expert;
-  int32_t* seg_offset;
-  int32_t* seg_count;
-  int32_t* n_segments;
-};
+// Counting-sort permute of all (token, k) assignments by expert, in one workgroup of 1024
+// threads (thread e owns expert e for the per-expert steps):
+//   1. per-expert counts (LDS atomics), exclusive scan -> expert offsets; a second scan over
+//      "expert has tokens" gives the compacted segment list (routed experts ascending, then the
+//      shared-expert segment over rows T*K .. T*K+T-1 in token order);
+//   2. tokens in passes of kMaskWords / E chunks of 64: each chunk's routing folded into one
+//      64-bit token mask per expert (atomic OR, order independent); an assignment's row is its
+//      expert's offset + the expert's tokens in earlier chunks + popcount of the lower tokens of
+//      its own chunk mask, i.e. rows of an expert follow token order.
+// No step depends on scheduling order, so the result is bit-exact across runs.
+constexpr int kMaskWords = 4096;  // LDS mask words per pass
+constexpr int kPermuteThreads = 1024;
 
-template <typename MaskFn, typename CntFn>
-__device__ void permute_block(const int32_t* __restrict__ topk_idx, int T, int K, int E,
-                              int n_chunks, MaskFn mask, CntFn cnt_of,
-                              int32_t* __restrict__ chunk_pre, int with_shared, int* s_off,
-                              int* s_wave, const PermuteOut& o) {
+__global__ __launch_bounds__(kPermuteThreads) void moe_permute_kernel(
+    const int32_t* __restrict__ topk_idx, int T, int K, int E, int with_shared,
+    int32_t* __restrict__ expert_counts, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ sorted_tokens, int32_t* __restrict__ inv_perm,
+    int32_t* __restrict__ seg_expert, int32_t* __restrict__ seg_offset,
+    int32_t* __restrict__ seg_count, int32_t* __restrict__ n_segments) {
+  __shared__ unsigned long long s_mask[kMaskWords];
+  __shared__ int s_pre[kMaskWords];
+  __shared__ int s_base[kPermuteThreads];  // per expert: count, then next free row
+  __shared__ int s_wave[16];
   const int tid = threadIdx.x;
   const int e = tid;
-  int cnt = 0;
-  if (e < E) {
-    for (int c = 0; c < n_chunks; ++c) {
-      const int v = cnt_of(c, e);
-      if (chunk_pre) chunk_pre[(size_t)c * E + e] = cnt;
-      cnt += v;
-    }
-  }
+  const int TK = T * K;
+
+  if (e < E) s_base[e] = 0;
+  __syncthreads();
+  for (int a = tid; a < TK; a += kPermuteThreads) atomicAdd(&s_base[topk_idx[a]], 1);
+  __syncthreads();
+  const int cnt = e < E ? s_base[e] : 0;
   int total = 0;
   const int off = block_exclusive_scan(cnt, s_wave, &total);
   int n_routed = 0;
   const int flag = (e < E && cnt > 0) ? 1 : 0;
   const int slot = block_exclusive_scan(flag, s_wave, &n_routed);
   if (e < E) {
-    s_off[e] = off;
-    o.expert_counts[e] = cnt;
-    o.expert_offsets[e] = off;
+    s_base[e] = off;
+    expert_counts[e] = cnt;
+    expert_offsets[e] = off;
     if (flag) {
-      o.seg_expert[slot] = e;
-      o.seg_offset[slot] = off;
-      o.seg_count[slot] = cnt;
+      seg_expert[slot] = e;
+      seg_offset[slot] = off;
+      seg_count[slot] = cnt;
     }
   }
   if (tid == 0) {
-    o.expert_offsets[E] = total;
+    expert_offsets[E] = total;
     if (with_shared) {
-      o.seg_expert[n_routed] = E;
-      o.seg_offset[n_routed] = T * K;
-      o.seg_count[n_routed] = T;
+      seg_expert[n_routed] = E;
+      seg_offset[n_routed] = TK;
+      seg_count[n_routed] = T;
     }
-    o.n_segments[0] = n_routed + (with_shared ? 1 : 0);
+    n_segments[0] = n_routed + (with_shared ? 1 : 0);
   }
-  __syncthreads();
-  for (int a = tid; a < T * K; a += blockDim.x) {
-    const int t = a / K;
-    const int ex = topk_idx[a];
-    const int c = t >> 6;
-    const int bit = t & 63;
-    const unsigned long long m = mask(c, ex);
-    const unsigned long long lower = bit ? (m & ((1ull << bit) - 1ull)) : 0ull;
-    const int pre = n_chunks > 1 ? chunk_pre[(size_t)c * E + ex] : 0;
-    const int row = s_off[ex] + pre + __popcll(lower);
-    o.sorted_tokens[row] = t;
-    o.inv_perm[a] = row;
-  }
-  if (with_shared) {
-    for (int t = tid; t < T; t += blockDim.x) o.sorted_tokens[T * K + t] = t;
-  }
-}
+  if (with_shared)
+    for (int t = tid; t < T; t += kPermuteThreads) sorted_tokens[TK + t] = t;
 
-// Routes one chunk of 64 tokens (one wave per token at a time) and folds the chunk's routing
-// into per-expert token bitmasks. With a single chunk (T <= 64, the decode case) the same
-// workgroup then performs the permute, so routing is one launch.
-template <int EPL>
-__global__ __launch_bounds__(kRouteThreads) void moe_route_chunk_kernel(
-    const float* __restrict__ logits, int n_parts, const float* __restrict__ bias, int T, int E,
-    int n_group, int topk_group, int top_k, float routed_scale, int renorm,
-    int32_t* __restrict__ topk_idx, float* __restrict__ topk_w,
-    unsigned long long* __restrict__ chunk_mask, int32_t* __restrict__ chunk_cnt,
-    int with_shared, PermuteOut po) {
-  __shared__ unsigned long long s_mask[64 * EPL];
-  __shared__ int32_t s_idx[kChunk * kMaxTopK];
-  __shared__ int s_off[64 * EPL];
-  __shared__ int s_wave[16];
-
-  const int chunk = blockIdx.x;
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int nwaves = blockDim.x >> 6;
-
-  for (int e = tid; e < E; e += blockDim.x) s_mask[e] = 0ull;
-
-  float bv[EPL];
-#pragma unroll
-  for (int j = 0; j < EPL; ++j) bv[j] = bias[lane * EPL + j];
-
-  const int tok0 = chunk * kChunk;
-  const int ntok = min(kChunk, T - tok0);
-  const size_t part_stride = (size_t)T * E;
-
-  // each wave routes tokens wave, wave + nwaves, ...; the next token's logits are loaded
-  // while the current one is routed
-  float cur[kLogitParts][EPL], nxt[kLogitParts][EPL];
-  if (wave < ntok) load_token_logits<EPL>(logits, n_parts, part_stride, tok0 + wave, E, lane, cur);
-  for (int tl = wave; tl < ntok; tl += nwaves) {
-    const int t = tok0 + tl;
-    if (tl + nwaves < ntok)
-      load_token_logits<EPL>(logits, n_parts, part_stride, t + nwaves, E, lane, nxt);
-    int my_idx;
-    float my_w;
-    route_token<EPL>(cur, n_parts, bv, E, n_group, topk_group, top_k, routed_scale, renorm,
-                     lane, my_idx, my_w);
-#pragma unroll
-    for (int q = 0; q < kLogitParts; ++q)
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) cur[q][j] = nxt[q][j];
-    if (lane < top_k) {
-      topk_idx[(size_t)t * top_k + lane] = my_idx;
-      topk_w[(size_t)t * top_k + lane] = my_w;
-      s_idx[tl * top_k + lane] = my_idx;
+  const int cpp = kMaskWords / E;  // chunks per pass
+  for (int t0 = 0; t0 < T; t0 += cpp * 64) {
+    const int nt = min(T - t0, cpp * 64);
+    const int nch = (nt + 63) >> 6;
+    for (int i = tid; i < nch * E; i += kPermuteThreads) s_mask[i] = 0ull;
+    __syncthreads();
+    const int a0 = t0 * K, a1 = (t0 + nt) * K;
+    for (int a = a0 + tid; a < a1; a += kPermuteThreads) {
+      const int tl = a / K - t0;
+      atomicOr(&s_mask[(tl >> 6) * E + topk_idx[a]], 1ull << (tl & 63));
     }
+    __syncthreads();
+    if (e < E) {
+      int run = s_base[e];
+      for (int c = 0; c < nch; ++c) {
+        s_pre[c * E + e] = run;
+        run += __popcll(s_mask[c * E + e]);
+      }
+      s_base[e] = run;
+    }
+    __syncthreads();
+    for (int a = a0 + tid; a < a1; a += kPermuteThreads) {
+      const int t = a / K;
+      const int tl = t - t0;
+      const int ex = topk_idx[a];
+      const int bit = tl & 63;
+      const unsigned long long m = s_mask[(tl >> 6) * E + ex];
+      const unsigned long long lower = bit ? (m & ((1ull << bit) - 1ull)) : 0ull;
+      const int row = s_pre[(tl >> 6) * E + ex] + __popcll(lower);
+      sorted_tokens[row] = t;
+      inv_perm[a] = row;
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  for (int a = tid; a < ntok * top_k; a += blockDim.x) {
-    const int tl = a / top_k;
-    atomicOr(&s_mask[s_idx[a]], 1ull << tl);
-  }
-  __syncthreads();
-  if (gridDim.x == 1) {
-    // single chunk: permute straight from the LDS masks (topk_idx re-read from this block's
-    // own global writes, visible after the barrier)
-    permute_block(
-        topk_idx, T, top_k, E, 1, [&](int, int e) { return s_mask[e]; },
-        [&](int, int e) { return (int)__popcll(s_mask[e]); }, (int32_t*)nullptr, with_shared,
-        s_off, s_wave, po);
-    return;
-  }
-  for (int e = tid; e < E; e += blockDim.x) {
-    const unsigned long long m = s_mask[e];
-    chunk_mask[(size_t)chunk * E + e] = m;
-    chunk_cnt[(size_t)chunk * E + e] = __popcll(m);
-  }
-}
-
-__global__ __launch_bounds__(kRouteThreads) void moe_permute_kernel(
-    const int32_t* __restrict__ topk_idx, int T, int K, int E, int n_chunks,
-    const unsigned long long* __restrict__ chunk_mask, const int32_t* __restrict__ chunk_cnt,
-    int32_t* __restrict__ chunk_pre, int with_shared, PermuteOut po) {
-  __shared__ int s_off[1024];
-  __shared__ int s_wave[16];
-  permute_block(
-      topk_idx, T, K, E, n_chunks,
-      [&](int c, int e) { return chunk_mask[(size_t)c * E + e]; },
-      [&](int c, int e) { return (int)chunk_cnt[(size_t)c * E + e]; }, chunk_pre, with_shared,
-      s_off, s_wave, po);
 }
 
 // Router logits in fp32 with v_mfma_f32_16x16x4_f32: parts[q][t][e] = sum over the q-th
@@ -447,10 +388,10 @@ __global__ __launch_bounds__(256) void moe_router_logits_kernel(
 using namespace sym;
 
 extern "C" size_t sym_moe_route_workspace_bytes(int T, int E) {
-  if (T <= 0 || E <= 0) return 0;
-  const size_t chunks = (size_t)(T + kChunk - 1) / kChunk;
-  // chunk masks (u64) + chunk counts (i32) + chunk prefixes (i32), each [chunks, E]
-  return chunks * (size_t)E * (8 + 4 + 4) + 256;
+  // routing keeps its intermediate state in LDS
+  (void)T;
+  (void)E;
+  return 0;
 }
 
 extern "C" int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E,
@@ -480,7 +421,7 @@ extern "C" int sym_moe_route_permute(const float* logits, int n_logit_parts, con
   if (T == 0) return SYM_OK;
   SYM_REQUIRE(logits && bias && topk_idx && topk_w && expert_counts && expert_offsets &&
                   sorted_tokens && inv_perm && seg_expert && seg_offset && seg_count &&
-                  n_segments && workspace,
+                  n_segments,
               SYM_ERR_INVALID, "moe_route_permute: null pointer argument");
   SYM_REQUIRE(n_logit_parts >= 1 && n_logit_parts <= kLogitParts, SYM_ERR_INVALID,
               "moe_route_permute: n_logit_parts=%d out of [1,%d]", n_logit_parts, kLogitParts);
@@ -503,25 +444,15 @@ extern "C" int sym_moe_route_permute(const float* logits, int n_logit_parts, con
               "moe_route_permute: top_k=%d exceeds the experts of the kept groups", top_k);
   SYM_REQUIRE((long long)T * top_k + T < (1ll << 30), SYM_ERR_INVALID,
               "moe_route_permute: T=%d too large", T);
-  const size_t need = sym_moe_route_workspace_bytes(T, E);
-  SYM_REQUIRE(workspace_bytes >= need, SYM_ERR_WORKSPACE,
-              "moe_route_permute: workspace %zu < required %zu", workspace_bytes, need);
-
-  const int n_chunks = (T + kChunk - 1) / kChunk;
-  char* ws = (char*)workspace;
-  unsigned long long* chunk_mask = (unsigned long long*)ws;
-  int32_t* chunk_cnt = (int32_t*)(ws + (size_t)n_chunks * E * 8);
-  int32_t* chunk_pre = chunk_cnt + (size_t)n_chunks * E;
-  const PermuteOut po{expert_counts, expert_offsets, sorted_tokens, inv_perm,
-                      seg_expert,    seg_offset,     seg_count,     n_segments};
+  (void)workspace;
+  (void)workspace_bytes;
 
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
-  const dim3 grid(n_chunks), block(kRouteThreads);
+  const dim3 grid((T + 3) / 4), block(256);
 #define SYM_LAUNCH_ROUTE(EE)                                                                    \
-  hipLaunchKernelGGL(moe_route_chunk_kernel<EE>, grid, block, 0, s, logits, n_logit_parts, bias, \
-                     T, E, n_group, topk_group, top_k, routed_scale, renormalize, topk_idx,      \
-                     topk_w, chunk_mask, chunk_cnt, with_shared, po)
+  hipLaunchKernelGGL(moe_route_kernel<EE>, grid, block, 0, s, logits, n_logit_parts, bias, T, E, \
+                     n_group, topk_group, top_k, routed_scale, renormalize, topk_idx, topk_w)
   switch (epl) {
     case 1: SYM_LAUNCH_ROUTE(1); break;
     case 2: SYM_LAUNCH_ROUTE(2); break;
@@ -529,9 +460,10 @@ extern "C" int sym_moe_route_permute(const float* logits, int n_logit_parts, con
     default: SYM_LAUNCH_ROUTE(8); break;
   }
 #undef SYM_LAUNCH_ROUTE
-  int rc = sym_host::check_launch("moe_route_chunk_kernel");
-  if (rc || n_chunks == 1) return rc;
-  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(1024), 0, s, topk_idx, T, top_k, E,
-                     n_chunks, chunk_mask, chunk_cnt, chunk_pre, with_shared, po);
+  int rc = sym_host::check_launch("moe_route_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(kPermuteThreads), 0, s, topk_idx, T, top_k,
+                     E, with_shared, expert_counts, expert_offsets, sorted_tokens, inv_perm,
+                     seg_expert, seg_offset, seg_count, n_segments);
   return sym_host::check_launch("moe_permute_kernel");
 }

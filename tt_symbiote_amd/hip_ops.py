@@ -353,14 +353,15 @@ def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,
     if T == 0:
         return res
     ws_bytes = _lib.query("sym_moe_route_workspace_bytes", T, E)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes else None
     _timed("moe_route_permute", lambda: _lib.call(
               "sym_moe_route_permute", _ptr(logits), n_parts, _ptr(bias), T, E, int(n_group),
               int(topk_group), int(top_k), float(routed_scale), 1 if renormalize else 0,
               1 if with_shared else 0, _ptr(res.topk_idx), _ptr(res.topk_w),
               _ptr(res.expert_counts), _ptr(res.expert_offsets), _ptr(res.sorted_tokens),
               _ptr(res.inv_perm), _ptr(res.seg_expert), _ptr(res.seg_offset),
-              _ptr(res.seg_count), _ptr(res.n_segments), _ptr(ws), ws.numel(), _stream()))
+              _ptr(res.seg_count), _ptr(res.n_segments), _ptr(ws) if ws is not None else None,
+              ws_bytes, _stream()))
     return res
 
 
