@@ -211,6 +211,13 @@ int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm, const flo
                               int top_k, int H, int shared_row0, const float* residual, void* out,
                               void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Streaming-read bandwidth probe (measurement only; no counterpart in the reference): reads
+ * `bytes` (a multiple of 16) of `buf` once, with 2048 workgroups of 256 threads, 16 bytes per
+ * thread per step; `sink` [1] is written only for one specific xor of the data.
+ */
+int sym_hbm_read_probe(const void* buf, size_t bytes, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -401,3 +401,10 @@ def test_decode_prologue(device, rotary_dim, use_norm):
         phys = int(ctx.page_table[b, p // 32])
         _close(kpc[phys, :, p % 32], k_ref[b, :, 0], atol=2e-2, rtol=1e-2)
         assert torch.equal(vpc[phys, :, p % 32], vr[b].bfloat16())
+
+
+def test_hbm_read_probe(device):
+    # measurement kernel: must read every byte (a rate above the 8 TB/s HBM peak would mean
+    # skipped work) and launch cleanly
+    gbs = hip_ops.hbm_read_bandwidth(256 << 20, reps=3, device=device)
+    assert 100.0 < gbs < 8000.0

@@ -65,6 +65,7 @@ _SIGNATURES = {
     "sym_moe_unpermute_combine": (
         _c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]
     ),
+    "sym_hbm_read_probe": (_c_int, [_vp, _c_size, _vp, _vp]),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

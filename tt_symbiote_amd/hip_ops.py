@@ -429,3 +429,25 @@ def moe_unpermute_combine(y: torch.Tensor, route: RouteResult,
     _lib.call("sym_moe_unpermute_combine", _ptr(y), _ptr(route.inv_perm), _ptr(route.topk_w), T,
               K, H, shared_row0, _ptr(residual), _ptr(out), _stream())
     return out
+
+
+def hbm_read_bandwidth(nbytes: int = 1 << 30, reps: int = 10,
+                       device: Optional[torch.device] = None) -> float:
+    """Streaming-read bandwidth in GB/s of ``sym_hbm_read_probe`` over ``nbytes`` of HBM (HIP
+    events around ``reps`` launches on the current stream, after one untimed launch)."""
+    dev = device or torch.device("cuda", torch.cuda.current_device())
+    nbytes -= nbytes % 16
+    buf = torch.ones(nbytes, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    run = lambda: _lib.call("sym_hbm_read_probe", _ptr(buf), nbytes, _ptr(sink), _stream())
+    run()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    secs = e0.elapsed_time(e1) * 1e-3 / reps
+    del buf
+    return nbytes / secs / 1e9

@@ -1,0 +1,127 @@
+"""Text summaries of rocprofv3 output for the kernels of the decode step.
+
+  python -m tt_symbiote_amd.rocprof_summary trace <results.db> [--top N]
+      per-kernel dispatch count and average / min / max / total duration, from the SQLite
+      database written by ``rocprofv3 --kernel-trace``;
+
+  python -m tt_symbiote_amd.rocprof_summary pmc --kernel NAME --fetch F.csv --write W.csv
+          --calib-fetch CF.csv --calib-write CW.csv --calib-kernel NAME --calib-bytes N [--json]
+      HBM bytes per dispatch of kernel NAME from two ``rocprofv3 --pmc FETCH_SIZE`` /
+      ``--pmc WRITE_SIZE`` runs (counter values in KiB per dispatch), each scaled by what the
+      same counter reads per dispatch for a plain copy kernel that reads and writes N bytes.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import sqlite3
+import statistics
+import sys
+from collections import defaultdict
+
+
+def kernel_stats(db_path: str):
+    db = sqlite3.connect(db_path)
+    rows = db.execute(
+        "select s.kernel_name, count(*), avg(d.end - d.start), sum(d.end - d.start), "
+        "min(d.end - d.start), max(d.end - d.start) from rocpd_kernel_dispatch d "
+        "join rocpd_info_kernel_symbol s on d.kernel_id = s.id "
+        "group by s.kernel_name order by sum(d.end - d.start) desc").fetchall()
+    db.close()
+    return rows
+
+
+def print_trace(db_path: str, top: int) -> None:
+    print(f"{'calls':>6} {'avg us':>9} {'min us':>9} {'max us':>9} {'total ms':>9}  kernel")
+    for name, n, avg, tot, mn, mx in kernel_stats(db_path)[:top]:
+        print(f"{n:6d} {avg / 1e3:9.1f} {mn / 1e3:9.1f} {mx / 1e3:9.1f} {tot / 1e6:9.2f}  "
+              f"{name[:110]}")
+
+
+def counter_per_dispatch(csv_path: str, counter: str) -> dict:
+    """{kernel name: [counter value of each dispatch]} (values summed over the rows of one
+    dispatch, e.g. per-XCD instances)."""
+    per_dispatch = defaultdict(float)
+    names = {}
+    with open(csv_path, newline="") as f:
+        for row in csv.DictReader(f):
+            if row["Counter_Name"] != counter:
+                continue
+            key = row["Dispatch_Id"]
+            per_dispatch[key] += float(row["Counter_Value"])
+            names[key] = row["Kernel_Name"]
+    out = defaultdict(list)
+    for key, v in per_dispatch.items():
+        out[names[key]].append(v)
+    return out
+
+
+def _match(table: dict, needle: str) -> list:
+    hits = [k for k in table if needle in k]
+    if not hits:
+        raise SystemExit(f"no kernel matching {needle!r}")
+    if len(hits) > 1:
+        hits.sort(key=len)
+    return table[hits[0]]
+
+
+def pmc_traffic(args) -> dict:
+    fetch = statistics.median(_match(counter_per_dispatch(args.fetch, "FETCH_SIZE"), args.kernel))
+    write = statistics.median(_match(counter_per_dispatch(args.write, "WRITE_SIZE"), args.kernel))
+    cf = statistics.median(_match(counter_per_dispatch(args.calib_fetch, "FETCH_SIZE"),
+                                  args.calib_kernel))
+    cw = statistics.median(_match(counter_per_dispatch(args.calib_write, "WRITE_SIZE"),
+                                  args.calib_kernel))
+    f_fetch = args.calib_bytes / cf
+    f_write = args.calib_bytes / cw
+    return {
+        "kernel": args.kernel,
+        "fetch_size_kib_per_dispatch": fetch,
+        "write_size_kib_per_dispatch": write,
+        "calibration": {"kernel": args.calib_kernel, "bytes_read_and_written": args.calib_bytes,
+                        "fetch_size_kib": cf, "write_size_kib": cw,
+                        "fetch_bytes_per_unit": f_fetch, "write_bytes_per_unit": f_write},
+        "hbm_read_bytes": fetch * f_fetch,
+        "hbm_write_bytes": write * f_write,
+        "traffic_bytes": fetch * f_fetch + write * f_write,
+    }
+
+
+def main(argv=None) -> None:
+    ap = argparse.ArgumentParser()
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("trace")
+    t.add_argument("db")
+    t.add_argument("--top", type=int, default=25)
+    p = sub.add_parser("pmc")
+    p.add_argument("--kernel", required=True)
+    p.add_argument("--fetch", required=True)
+    p.add_argument("--write", required=True)
+    p.add_argument("--calib-fetch", required=True)
+    p.add_argument("--calib-write", required=True)
+    p.add_argument("--calib-kernel", required=True)
+    p.add_argument("--calib-bytes", type=float, required=True)
+    p.add_argument("--json", action="store_true")
+    args = ap.parse_args(argv)
+    if args.cmd == "trace":
+        print_trace(args.db, args.top)
+        return
+    res = pmc_traffic(args)
+    if args.json:
+        json.dump(res, sys.stdout, indent=1)
+        print()
+        return
+    c = res["calibration"]
+    print(f"kernel {res['kernel']}")
+    print(f"  FETCH_SIZE {res['fetch_size_kib_per_dispatch']:.0f} (nominal KiB) per dispatch x "
+          f"{c['fetch_bytes_per_unit']:.1f} B = {res['hbm_read_bytes'] / 1e6:.1f} MB read")
+    print(f"  WRITE_SIZE {res['write_size_kib_per_dispatch']:.0f} (nominal KiB) per dispatch x "
+          f"{c['write_bytes_per_unit']:.1f} B = {res['hbm_write_bytes'] / 1e6:.1f} MB written")
+    print(f"  traffic {res['traffic_bytes'] / 1e6:.1f} MB per dispatch")
+    print(f"calibration: {c['kernel']} moving {c['bytes_read_and_written'] / 2**20:.0f} MiB each "
+          f"way reads FETCH_SIZE {c['fetch_size_kib']:.0f} / WRITE_SIZE {c['write_size_kib']:.0f}")
+
+
+if __name__ == "__main__":
+    main()
