@@ -125,6 +125,25 @@ int sym_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                          size_t workspace_bytes, void* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Fused attention decode step: sym_attn_decode_prologue followed by sym_paged_gqa_decode in
+ * one split kernel (+ the merge kernel). Replaces the QK-norm, RoPE, paged_update_cache and
+ * paged SDPA decode of TTNNBailingMoEAttention._forward_decode_paged
+ * (ttnn_attention.py:2329-2443). Every workgroup normalises and rotates its q heads from qkv;
+ * the workgroup of each sequence's last split also normalises and rotates k, writes k and v into
+ * the pools at positions[b] (as the prologue) and uses them for the new token directly.
+ * Arguments as sym_attn_decode_prologue (qkv [B, (Hq+2Hkv)*head_dim]) and
+ * sym_paged_gqa_decode (workspace, max_context, scale, out [B, Hq, head_dim]); results are
+ * identical to the two calls in sequence.
+ */
+int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                         const float* rope_cs, int max_pos, const int32_t* positions, int B, int Hq,
+                         int Hkv, int head_dim, int rotary_dim, float eps, int use_qk_norm,
+                         void* k_pool, void* v_pool, const int32_t* block_tables,
+                         int max_blocks_per_seq, int block_size, int num_blocks, int max_context,
+                         float scale, void* workspace, size_t workspace_bytes, void* out,
+                         void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Router logits in fp32 (fp32 MFMA): replaces the fp32 gate GEMV of TTNNMoE.forward
  * (ttnn_moe.py:1438-1455; gate weight kept fp32, ttnn_moe.py:1542).
  *   x [T, H] bf16 (upcast exactly); w [E, H] fp32;
@@ -179,7 +198,7 @@ int sym_moe_route_permute(const float* logits, int n_logit_parts, const float* b
  *     y[r] = h[r] . Wd[e]^T                                    (fp32)
  *   x [T, H] bf16; w_gate_up [E+1, 2I, H] bf16; w_down [E+1, H, I] bf16;
  *   h [rows, I] bf16 and y [rows, H] fp32 with rows = T*top_k (+T with a shared expert).
- * The segment list is read on the device; no host synchronization. H % 128 == 0, I % 64 == 0.
+ * The segment list is read on the device; no host synchronization. H % 256 == 0, I % 64 == 0.
  * max_segments: the length of the segment list buffers (E+1).
  */
 int sym_moe_grouped_swiglu(const void* x, int T, int H, int I, const int32_t* sorted_tokens,

@@ -403,6 +403,45 @@ def test_decode_prologue(device, rotary_dim, use_norm):
         assert torch.equal(vpc[phys, :, p % 32], vr[b].bfloat16())
 
 
+@pytest.mark.parametrize("B,Hq,Hkv,rd,use_norm,lo,hi,bs,cap", [
+    (8, 16, 4, 64, True, 5, 3000, 32, None),
+    (5, 16, 2, 128, False, 0, 300, 16, None),      # 8 q heads per kv head
+    (6, 8, 8, 64, True, 250, 600, 64, None),       # 1 q head per kv head
+    (6, 16, 4, 64, True, 100, 700, 32, 512),       # some positions beyond the attention cap
+])
+def test_decode_step_matches_prologue_then_decode(device, B, Hq, Hkv, rd, use_norm, lo, hi, bs,
+                                                   cap):
+    """The fused step (QK-norm, RoPE, KV write and decode in the split kernel) gives exactly
+    the output and the pools of the prologue kernel followed by the decode kernel, including a
+    sequence with no position (-1) and one whose new slot has no page-table entry."""
+    D = 128
+    ctx = paged_context(B, lo, hi, block_size=bs, num_kv_heads=Hkv, seed=B * 7 + Hkv)
+    pt = ctx.page_table.clone()
+    pos = ctx.positions.clone()
+    pos[0] = -1
+    last = int(pos[1]) // bs
+    pt[1, last] = -1                                  # the new token's block is unmapped
+    g = torch.Generator().manual_seed(B + rd)
+    qkv = torch.randn(B, (Hq + 2 * Hkv) * D, generator=g).bfloat16().to(device)
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(device)
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(device)
+    inv = 1.0 / (1e6 ** (torch.arange(0, rd, 2).float() / rd))
+    fr = torch.arange(4096).float()[:, None] * inv[None]
+    table = torch.cat([fr.cos(), fr.sin()], 1).contiguous().to(device)
+    pt_d, pos_d = pt.to(device), pos.to(device)
+    kw = dict(num_heads=Hq, num_kv_heads=Hkv, rotary_dim=rd, rope_cs=table,
+              q_norm_w=qn if use_norm else None, k_norm_w=kn if use_norm else None, eps=1e-6)
+    max_context = cap or pt.shape[1] * bs
+    k1, v1 = ctx.k_pool.to(device), ctx.v_pool.to(device)
+    q = hip_ops.attn_decode_prologue(qkv, pos_d, k1, v1, pt_d, **kw)
+    ref = hip_ops.paged_gqa_decode(q, k1, v1, pt_d, pos_d, 0.09, max_context=max_context)
+    k2, v2 = ctx.k_pool.to(device), ctx.v_pool.to(device)
+    out = hip_ops.attn_decode_step(qkv, pos_d, k2, v2, pt_d, 0.09, max_context=max_context, **kw)
+    assert torch.equal(out, ref)
+    assert torch.equal(k2, k1) and torch.equal(v2, v1)
+    assert not bool(out[0].any())                    # no position: zero output
+
+
 def test_hbm_read_probe(device):
     # measurement kernel: must read every byte (a rate above the 8 TB/s HBM peak would mean
     # skipped work) and launch cleanly

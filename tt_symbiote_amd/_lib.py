@@ -44,6 +44,12 @@ _SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_float, _vp, _c_size, _vp, _vp],
     ),
+    "sym_attn_decode_step": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+         _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _vp, _c_size, _vp,
+         _vp],
+    ),
     "sym_linear_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]),
     "sym_moe_router_logits": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "sym_moe_route_workspace_bytes": (_c_size, [_c_int, _c_int]),

@@ -27,225 +27,233 @@ __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// One pass of gate/up over 16 rows of a segment, for this wave's K-step range [s_beg, s_end)
+// (a multiple of U steps). Per batch of U K-steps: the weight loads, then the activation loads,
+// then the MFMAs, kept in that order by scheduling barriers. The 16 token indices of the pass
+// are read with scalar loads after the first weight batch is issued: waiting for them (lgkmcnt)
+// does not wait for the weights in flight (vmcnt).
+template <int U>
+__device__ __forceinline__ void gate_up_pass(const uint16_t* __restrict__ x, int H,
+                                             const int32_t* __restrict__ tok_rows, int rows,
+                                             const uint16_t* __restrict__ wg,
+                                             const uint16_t* __restrict__ wu, int s_beg, int s_end,
+                                             int r16, int kq, floatx4& accg, floatx4& accu) {
+  accg = floatx4{0.f, 0.f, 0.f, 0.f};
+  accu = floatx4{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xr = nullptr;
+  for (int st = s_beg; st < s_end; st += U) {
+    uint4 bg[U][2], bu[U][2], a[U][2];
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      const int k = (st + s) << 6;
+      bg[s][0] = ld16(wg + k);
+      bg[s][1] = ld16(wg + k + 8);
+      bu[s][0] = ld16(wu + k);
+      bu[s][1] = ld16(wu + k + 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (st == s_beg) {
+      // rows past the pass read its last row (in bounds); their outputs are dropped
+      int tok = tok_rows[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) {
+        const int ti = tok_rows[min(i, rows - 1)];
+        tok = r16 == i ? ti : tok;
+      }
+      xr = x + (size_t)tok * H + kq * 16;
+    }
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      const int k = (st + s) << 6;
+      a[s][0] = ld16(xr + k);
+      a[s][1] = ld16(xr + k + 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      accg = mfma16x16x32(a[s][0], bg[s][0], accg);
+      accg = mfma16x16x32(a[s][1], bg[s][1], accg);
+      accu = mfma16x16x32(a[s][0], bu[s][0], accu);
+      accu = mfma16x16x32(a[s][1], bu[s][1], accu);
+    }
+  }
+}
+
+// Partial accumulators of the 4 waves -> LDS -> sum, SwiGLU, bf16 h rows of the pass.
+template <int MT>
+__device__ __forceinline__ void gate_up_epilogue(float (*s_red)[MT][2][4][64],
+                                                 const floatx4 (&accg)[MT],
+                                                 const floatx4 (&accu)[MT], int wave, int lane,
+                                                 int rows, size_t h_row0, int I, int col0,
+                                                 uint16_t* __restrict__ h) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      s_red[wave][mt][0][i][lane] = accg[mt][i];
+      s_red[wave][mt][1][i][lane] = accu[mt][i];
+    }
+  __syncthreads();
+  // thread -> element i of lane l's 16x16 fragment: row 4*(l/16)+i, column l%16
+  const int l = threadIdx.x & 63;
+  const int i = threadIdx.x >> 6;
+  const int row = 4 * (l >> 4) + i;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const float g = (s_red[0][mt][0][i][l] + s_red[1][mt][0][i][l]) +
+                    (s_red[2][mt][0][i][l] + s_red[3][mt][0][i][l]);
+    const float u = (s_red[0][mt][1][i][l] + s_red[1][mt][1][i][l]) +
+                    (s_red[2][mt][1][i][l] + s_red[3][mt][1][i][l]);
+    const int r = mt * 16 + row;
+    if (r < rows) {
+      const float hv = g / (1.0f + expf(-g)) * u;
+      h[(h_row0 + r) * I + col0 + (l & 15)] = f32_to_bf16(hv);
+    }
+  }
+  __syncthreads();
+}
+
 // gate/up + SwiGLU. One workgroup per (segment, 16 columns of h); its 4 waves split the
-// reduction over H into contiguous K-step ranges. Each batch of U K-steps issues all of its
-// weight loads (gate and up rows) and activation loads (MT row tiles) before the MFMAs; the
-// waves' partial accumulators reduce through LDS before the SwiGLU epilogue.
-template <int MT, int U>
+// reduction over H into contiguous K-step ranges and reduce through LDS. The segment's metadata
+// (count, expert, offset, row count) is loaded in one round trip before the exit test; rows are
+// processed in passes of 16 (a routed expert at decode has a few rows; the shared expert's
+// second pass finds its weight rows in L2).
+template <int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
     const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
     const int32_t* __restrict__ seg_expert, const int32_t* __restrict__ seg_offset,
     const int32_t* __restrict__ seg_count, const int32_t* __restrict__ n_segments,
     const uint16_t* __restrict__ w_gu, uint16_t* __restrict__ h, int tiles_per_seg) {
-  __shared__ float s_red[4][MT][2][4][64];
+  __shared__ float s_red[4][1][2][4][64];
   const int seg = blockIdx.x / tiles_per_seg;
-  if (seg >= n_segments[0]) return;
+  const int nseg = n_segments[0];
+  const int e = seg_expert[seg];
+  const int row0 = seg_offset[seg];
+  const int cnt = seg_count[seg];
+  // used here (an empty asm), so the loads, and those of the kernel arguments, issue together
+  // in one round trip instead of being sunk past the exit test
+  asm volatile("" ::"s"(nseg), "s"(e), "s"(row0), "s"(cnt), "s"(x), "s"(sorted_tokens),
+               "s"(w_gu), "s"(h));
+  if (seg >= nseg) return;
   const int tile = blockIdx.x - seg * tiles_per_seg;
   const int col0 = tile * 16;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
-  const int e = seg_expert[seg];
-  const int row0 = seg_offset[seg];
-  const int cnt = seg_count[seg];
   const int nsteps = H >> 6;
   const int s_beg = (wave * nsteps) >> 2;
   const int s_end = ((wave + 1) * nsteps) >> 2;
-
   const uint16_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * 16;
   const uint16_t* wu = wg + (size_t)I * H;
 
-  for (int mb = 0; mb < cnt; mb += 16 * MT) {
-    const int nmt = min(MT, (cnt - mb + 15) >> 4);
-    floatx4 accg[MT], accu[MT];
-    const uint16_t* xr[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      accg[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      accu[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      // rows past the segment read its last row (in bounds, finite); their outputs are dropped
-      const int r = min(mb + mt * 16 + r16, cnt - 1);
-      xr[mt] = x + (size_t)sorted_tokens[row0 + r] * H + kq * 16;
-    }
-    int st = s_beg;
-    for (; st + U <= s_end; st += U) {
-      uint4 bg[U][2], bu[U][2], a[MT][U][2];
-#pragma unroll
-      for (int s = 0; s < U; ++s) {
-        const int k = (st + s) << 6;
-        bg[s][0] = ld16(wg + k);
-        bg[s][1] = ld16(wg + k + 8);
-        bu[s][0] = ld16(wu + k);
-        bu[s][1] = ld16(wu + k + 8);
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int s = 0; s < U; ++s) {
-          const int k = (st + s) << 6;
-          a[mt][s][0] = ld16(xr[mt] + k);
-          a[mt][s][1] = ld16(xr[mt] + k + 8);
-        }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if (mt < nmt) {
-#pragma unroll
-          for (int s = 0; s < U; ++s) {
-            accg[mt] = mfma16x16x32(a[mt][s][0], bg[s][0], accg[mt]);
-            accg[mt] = mfma16x16x32(a[mt][s][1], bg[s][1], accg[mt]);
-            accu[mt] = mfma16x16x32(a[mt][s][0], bu[s][0], accu[mt]);
-            accu[mt] = mfma16x16x32(a[mt][s][1], bu[s][1], accu[mt]);
-          }
-        }
-      }
-    }
-    for (; st < s_end; ++st) {
-      const int k = st << 6;
-      const uint4 g0 = ld16(wg + k), g1 = ld16(wg + k + 8);
-      const uint4 u0 = ld16(wu + k), u1 = ld16(wu + k + 8);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint4 a0 = ld16(xr[mt] + k);
-        const uint4 a1 = ld16(xr[mt] + k + 8);
-        if (mt < nmt) {
-          accg[mt] = mfma16x16x32(a0, g0, accg[mt]);
-          accg[mt] = mfma16x16x32(a1, g1, accg[mt]);
-          accu[mt] = mfma16x16x32(a0, u0, accu[mt]);
-          accu[mt] = mfma16x16x32(a1, u1, accu[mt]);
-        }
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (mt < nmt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          s_red[wave][mt][0][i][lane] = accg[mt][i];
-          s_red[wave][mt][1][i][lane] = accu[mt][i];
-        }
-      }
-    }
-    __syncthreads();
-    {
-      // thread -> element i of lane l's 16x16 fragment: row 4*(l/16)+i, column l%16
-      const int l = threadIdx.x & 63;
-      const int i = threadIdx.x >> 6;
-      const int row = 4 * (l >> 4) + i;
-      for (int mt = 0; mt < nmt; ++mt) {
-        const float g = (s_red[0][mt][0][i][l] + s_red[1][mt][0][i][l]) +
-                        (s_red[2][mt][0][i][l] + s_red[3][mt][0][i][l]);
-        const float u = (s_red[0][mt][1][i][l] + s_red[1][mt][1][i][l]) +
-                        (s_red[2][mt][1][i][l] + s_red[3][mt][1][i][l]);
-        const int r = mb + mt * 16 + row;
-        if (r < cnt) {
-          const float hv = g / (1.0f + expf(-g)) * u;
-          h[(size_t)(row0 + r) * I + col0 + (l & 15)] = f32_to_bf16(hv);
-        }
-      }
-    }
-    __syncthreads();
+  for (int mb = 0; mb < cnt; mb += 16) {
+    const int rows = min(16, cnt - mb);
+    floatx4 accg[1], accu[1];
+    gate_up_pass<U>(x, H, sorted_tokens + row0 + mb, rows, wg, wu, s_beg, s_end, r16, kq,
+                    accg[0], accu[0]);
+    gate_up_epilogue<1>(s_red, accg, accu, wave, lane, rows, (size_t)row0 + mb, I, col0, h);
   }
 }
 
-// down projection. One wave per (segment, 32 output columns = two 16-column tiles sharing the
-// activation fragments) over the full reduction dim I, loads issued in batches of U K-steps.
+// One pass of the down projection over MT row tiles: this wave's 32 output columns (two
+// 16-column tiles sharing the activation fragments) over the full reduction dim I, in batches
+// of U K-steps (weights first, then activations, then MFMAs).
 template <int MT, int U>
+__device__ __forceinline__ void down_pass(const uint16_t* __restrict__ hrow, int I, int rows,
+                                          const uint16_t* __restrict__ wd0,
+                                          const uint16_t* __restrict__ wd1, int r16, int kq,
+                                          floatx4 (&acc0)[MT], floatx4 (&acc1)[MT]) {
+  const int nsteps = I >> 6;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    acc0[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    acc1[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+  for (int st = 0; st < nsteps; st += U) {
+    uint4 b0[U][2], b1[U][2], a[MT][U][2];
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      const int k = (st + s) << 6;
+      b0[s][0] = ld16(wd0 + k);
+      b0[s][1] = ld16(wd0 + k + 8);
+      b1[s][0] = ld16(wd1 + k);
+      b1[s][1] = ld16(wd1 + k + 8);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint16_t* hr = hrow + (size_t)min(mt * 16 + r16, rows - 1) * I + kq * 16;
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        const int k = (st + s) << 6;
+        a[mt][s][0] = ld16(hr + k);
+        a[mt][s][1] = ld16(hr + k + 8);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < U; ++s)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc0[mt] = mfma16x16x32(a[mt][s][0], b0[s][0], acc0[mt]);
+        acc0[mt] = mfma16x16x32(a[mt][s][1], b0[s][1], acc0[mt]);
+        acc1[mt] = mfma16x16x32(a[mt][s][0], b1[s][0], acc1[mt]);
+        acc1[mt] = mfma16x16x32(a[mt][s][1], b1[s][1], acc1[mt]);
+      }
+  }
+}
+
+template <int MT>
+__device__ __forceinline__ void down_store(const floatx4 (&acc0)[MT], const floatx4 (&acc1)[MT],
+                                           int rows, float* __restrict__ yrow, int H, int r16,
+                                           int kq) {
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = mt * 16 + kq * 4 + i;
+      if (r < rows) {
+        float* yr = yrow + (size_t)r * H + r16;
+        yr[0] = acc0[mt][i];
+        yr[16] = acc1[mt][i];
+      }
+    }
+}
+
+// down projection. One wave per (segment, 32 output columns); segment metadata in one round
+// trip before the exit test; rows in passes of 16.
+template <int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
     const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
     const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
     const int32_t* __restrict__ n_segments, const uint16_t* __restrict__ w_d,
     float* __restrict__ y, int tiles_per_seg) {
   const int seg = blockIdx.x / tiles_per_seg;
-  if (seg >= n_segments[0]) return;
+  const int nseg = n_segments[0];
+  const int e = seg_expert[seg];
+  const int row0 = seg_offset[seg];
+  const int cnt = seg_count[seg];
+  // used here (an empty asm), so the loads, and those of the kernel arguments, issue together
+  // in one round trip instead of being sunk past the exit test
+  asm volatile("" ::"s"(nseg), "s"(e), "s"(row0), "s"(cnt), "s"(hbuf), "s"(w_d), "s"(y),
+               "s"(H), "s"(I));
+  if (seg >= nseg) return;
   const int tile = blockIdx.x - seg * tiles_per_seg;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int col0 = (tile * 4 + wave) * 32;
   if (col0 >= H) return;
-  const int e = seg_expert[seg];
-  const int row0 = seg_offset[seg];
-  const int cnt = seg_count[seg];
   const int r16 = lane & 15;
   const int kq = lane >> 4;
-  const int nsteps = I >> 6;
-
   const uint16_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 16;
   const uint16_t* wd1 = wd0 + (size_t)16 * I;
 
-  for (int mb = 0; mb < cnt; mb += 16 * MT) {
-    const int nmt = min(MT, (cnt - mb + 15) >> 4);
-    floatx4 acc0[MT], acc1[MT];
-    const uint16_t* hr[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      acc0[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      acc1[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-      const int r = min(mb + mt * 16 + r16, cnt - 1);
-      hr[mt] = hbuf + (size_t)(row0 + r) * I + kq * 16;
-    }
-    int st = 0;
-    for (; st + U <= nsteps; st += U) {
-      uint4 b0[U][2], b1[U][2], a[MT][U][2];
-#pragma unroll
-      for (int s = 0; s < U; ++s) {
-        const int k = (st + s) << 6;
-        b0[s][0] = ld16(wd0 + k);
-        b0[s][1] = ld16(wd0 + k + 8);
-        b1[s][0] = ld16(wd1 + k);
-        b1[s][1] = ld16(wd1 + k + 8);
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int s = 0; s < U; ++s) {
-          const int k = (st + s) << 6;
-          a[mt][s][0] = ld16(hr[mt] + k);
-          a[mt][s][1] = ld16(hr[mt] + k + 8);
-        }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if (mt < nmt) {
-#pragma unroll
-          for (int s = 0; s < U; ++s) {
-            acc0[mt] = mfma16x16x32(a[mt][s][0], b0[s][0], acc0[mt]);
-            acc0[mt] = mfma16x16x32(a[mt][s][1], b0[s][1], acc0[mt]);
-            acc1[mt] = mfma16x16x32(a[mt][s][0], b1[s][0], acc1[mt]);
-            acc1[mt] = mfma16x16x32(a[mt][s][1], b1[s][1], acc1[mt]);
-          }
-        }
-      }
-    }
-    for (; st < nsteps; ++st) {
-      const int k = st << 6;
-      const uint4 p0 = ld16(wd0 + k), p1 = ld16(wd0 + k + 8);
-      const uint4 q0 = ld16(wd1 + k), q1 = ld16(wd1 + k + 8);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint4 a0 = ld16(hr[mt] + k);
-        const uint4 a1 = ld16(hr[mt] + k + 8);
-        if (mt < nmt) {
-          acc0[mt] = mfma16x16x32(a0, p0, acc0[mt]);
-          acc0[mt] = mfma16x16x32(a1, p1, acc0[mt]);
-          acc1[mt] = mfma16x16x32(a0, q0, acc1[mt]);
-          acc1[mt] = mfma16x16x32(a1, q1, acc1[mt]);
-        }
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (mt < nmt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int r = mb + mt * 16 + kq * 4 + i;
-          if (r < cnt) {
-            float* yr = y + (size_t)(row0 + r) * H + col0 + r16;
-            yr[0] = acc0[mt][i];
-            yr[16] = acc1[mt][i];
-          }
-        }
-      }
-    }
+  for (int mb = 0; mb < cnt; mb += 16) {
+    const int rows = min(16, cnt - mb);
+    floatx4 acc0[1], acc1[1];
+    down_pass<1, U>(hbuf + (size_t)(row0 + mb) * I, I, rows, wd0, wd1, r16, kq, acc0, acc1);
+    down_store<1>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
   }
 }
 
@@ -293,8 +301,8 @@ using namespace sym;
 
 static int check_gemm_args(const char* what, int T, int H, int I, int max_segments) {
   SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "%s: T=%d < 0", what, T);
-  SYM_REQUIRE(H > 0 && H % 128 == 0, SYM_ERR_UNSUPPORTED,
-              "%s: H=%d must be a positive multiple of 128", what, H);
+  SYM_REQUIRE(H > 0 && H % 256 == 0, SYM_ERR_UNSUPPORTED,
+              "%s: H=%d must be a positive multiple of 256", what, H);
   SYM_REQUIRE(I > 0 && I % 64 == 0, SYM_ERR_UNSUPPORTED,
               "%s: I=%d must be a positive multiple of 64", what, I);
   SYM_REQUIRE(max_segments >= 1 && max_segments <= 4096, SYM_ERR_INVALID,
@@ -314,10 +322,16 @@ extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t
               SYM_ERR_INVALID, "moe_gate_up: null pointer argument");
   (void)hipGetLastError();
   const int tiles = I / 16;
-  hipLaunchKernelGGL((moe_gate_up_kernel<2, 4>), dim3(max_segments * tiles), dim3(kGemmThreads), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, H, I, sorted_tokens, seg_expert,
-                     seg_offset, seg_count, n_segments, (const uint16_t*)w_gate_up, (uint16_t*)h,
-                     tiles);
+  const int wave_steps = H / 256;  // K-steps of 64 per wave (4 waves split H)
+  const dim3 grid(max_segments * tiles), block(kGemmThreads);
+#define SYM_LAUNCH_GATE_UP(UU)                                                                  \
+  hipLaunchKernelGGL((moe_gate_up_kernel<UU>), grid, block, 0, (hipStream_t)stream,              \
+                     (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
+                     n_segments, (const uint16_t*)w_gate_up, (uint16_t*)h, tiles)
+  if (wave_steps % 4 == 0) SYM_LAUNCH_GATE_UP(4);
+  else if (wave_steps % 2 == 0) SYM_LAUNCH_GATE_UP(2);
+  else SYM_LAUNCH_GATE_UP(1);
+#undef SYM_LAUNCH_GATE_UP
   return sym_host::check_launch("moe_gate_up_kernel");
 }
 
@@ -332,9 +346,16 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
               SYM_ERR_INVALID, "moe_down: null pointer argument");
   (void)hipGetLastError();
   const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
-  hipLaunchKernelGGL((moe_down_kernel<2, 4>), dim3(max_segments * tiles), dim3(kGemmThreads), 0,
-                     (hipStream_t)stream, (const uint16_t*)h, H, I, seg_expert, seg_offset,
-                     seg_count, n_segments, (const uint16_t*)w_down, y, tiles);
+  const int steps = I / 64;  // K-steps of 64 per wave (one wave covers all of I)
+  const dim3 grid(max_segments * tiles), block(kGemmThreads);
+#define SYM_LAUNCH_DOWN(UU)                                                                     \
+  hipLaunchKernelGGL((moe_down_kernel<UU>), grid, block, 0, (hipStream_t)stream,                 \
+                     (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
+                     (const uint16_t*)w_down, y, tiles)
+  if (steps % 4 == 0) SYM_LAUNCH_DOWN(4);
+  else if (steps % 2 == 0) SYM_LAUNCH_DOWN(2);
+  else SYM_LAUNCH_DOWN(1);
+#undef SYM_LAUNCH_DOWN
   return sym_host::check_launch("moe_down_kernel");
 }
 

@@ -23,10 +23,99 @@
 namespace sym {
 
 constexpr int kHeadDim = 128;
-constexpr int kSplit = 256;  // tokens per split
+constexpr int kTPW = 64;           // tokens per wave in the split kernel
+constexpr int kSplit = 4 * kTPW;  // tokens per split (one workgroup of 4 waves)
 constexpr int kAttnThreads = 256;
 
 // ---------------------------------------------------------------------------------------------
+// QK RMSNorm (optional) and split-half partial RoPE of one head, held by a wave as
+// x0 = dim `lane`, x1 = dim `lane + 64`. norm: x * rsqrt(mean(x^2) + eps) * w in fp32 (one
+// rounding at the end, by the caller); RoPE over dims [0, rd): for i < rd/2,
+// y_i = x_i cos - x_{i+rd/2} sin and y_{i+rd/2} = x_{i+rd/2} cos + x_i sin, with
+// cs = [cos(pos f_0..) | sin(pos f_0..)] the table row of the position.
+// The per-lane operands (norm weights, cos/sin of the lane's two dims) are loaded separately
+// from the arithmetic, so a kernel can issue those loads early.
+struct RopeLane {
+  float c0, s0, c1, s1;  // cos/sin for dims lane and lane + 64 (unused past rd)
+};
+
+__device__ __forceinline__ RopeLane load_rope_lane(const float* __restrict__ cs, int rd,
+                                                   int lane) {
+  RopeLane r{1.f, 0.f, 1.f, 0.f};
+  if (cs && rd > 0) {
+    const int half = rd >> 1;
+    const int i0 = lane, i1 = lane + 64;
+    const int f0 = i0 < half ? i0 : i0 - half;
+    const int f1 = i1 < half ? i1 : i1 - half;
+    if (i0 < rd) { r.c0 = cs[f0]; r.s0 = cs[half + f0]; }
+    if (i1 < rd) { r.c1 = cs[f1]; r.s1 = cs[half + f1]; }
+  }
+  return r;
+}
+
+// Branch-free form for a kernel that issues these loads early: cs must point at rd readable
+// floats (a table row, or any rd floats when RoPE is off; the values are then not used).
+__device__ __forceinline__ RopeLane load_rope_lane_nobranch(const float* __restrict__ cs,
+                                                            int rd, int lane) {
+  const int half = max(rd >> 1, 1);
+  const int i0 = lane, i1 = lane + 64;
+  const int f0 = min(i0 < half ? i0 : i0 - half, half - 1);
+  const int f1 = min(i1 < half ? i1 : i1 - half, half - 1);
+  return RopeLane{cs[f0], cs[half + f0], cs[f1], cs[half + f1]};
+}
+
+// Stand-ins the fused kernel reads when QK-norm or RoPE is off, so its early loads need no
+// branches (1.0 in bf16; 256 zero floats).
+__device__ const uint16_t kOnesBf16[kHeadDim] = {
+#define SYM_ONE8 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80, 0x3F80
+    SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8,
+    SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8, SYM_ONE8
+#undef SYM_ONE8
+};
+__device__ const float kZeroRope[2 * kHeadDim] = {};
+
+__device__ __forceinline__ void qk_norm_rope(float& x0, float& x1, bool norm, float w0, float w1,
+                                             float eps, bool rope, const RopeLane& rl, int rd,
+                                             int lane) {
+  // no contraction: the prologue kernel and the fused decode step round identically
+#pragma clang fp contract(off)
+  if (norm) {
+    const float ss = wave_sum(x0 * x0 + x1 * x1);
+    const float r = rsqrtf(ss * (1.0f / kHeadDim) + eps);
+    x0 = x0 * r * w0;
+    x1 = x1 * r * w1;
+  }
+  if (rope && rd > 0) {
+    const int half = rd >> 1;
+    // element i lives in lane i % 64, slot i / 64
+    const int i0 = lane, i1 = lane + 64;
+    const int p0 = i0 < half ? i0 + half : i0 - half;
+    const int p1 = i1 < half ? i1 + half : i1 - half;
+    const float a0 = __shfl(x0, p0 & 63), b0 = __shfl(x1, p0 & 63);
+    const float a1 = __shfl(x0, p1 & 63), b1 = __shfl(x1, p1 & 63);
+    const float y0 = (p0 >> 6) ? b0 : a0;  // value of element p0
+    const float y1 = (p1 >> 6) ? b1 : a1;
+    float n0 = x0, n1 = x1;
+    if (i0 < rd) n0 = i0 < half ? x0 * rl.c0 - y0 * rl.s0 : x0 * rl.c0 + y0 * rl.s0;
+    if (i1 < rd) n1 = i1 < half ? x1 * rl.c1 - y1 * rl.s1 : x1 * rl.c1 + y1 * rl.s1;
+    x0 = n0;
+    x1 = n1;
+  }
+}
+
+// Physical block of the slot of `pos` in sequence b, or -1 (position < 0, beyond the page table,
+// or an entry outside [0, num_blocks)); *off gets the slot's offset in the block.
+__device__ __forceinline__ int slot_block(const int32_t* __restrict__ block_tables, int b,
+                                          int pos, int mbps, int block_size, int num_blocks,
+                                          int* off) {
+  if (pos < 0) return -1;
+  const int blk = pos / block_size;
+  *off = pos - blk * block_size;
+  if (blk >= mbps) return -1;
+  const int p = block_tables[(size_t)b * mbps + blk];
+  return (p >= 0 && p < num_blocks) ? p : -1;
+}
+
 __global__ __launch_bounds__(256) void attn_decode_prologue_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, const float* __restrict__ rope_cs, int max_pos,
@@ -39,19 +128,10 @@ __global__ __launch_bounds__(256) void attn_decode_prologue_kernel(
   const int nwaves = blockDim.x >> 6;
   const int nh = Hq + 2 * Hkv;
   const int pos = positions[b];
-  const int half = rd >> 1;
-
-  int phys = -1;
   int off = 0;
-  if (pos >= 0) {
-    const int blk = pos / block_size;
-    off = pos - blk * block_size;
-    if (blk < mbps) {
-      const int p = block_tables[(size_t)b * mbps + blk];
-      if (p >= 0 && p < num_blocks) phys = p;
-    }
-  }
-  const bool rope_ok = pos >= 0 && pos < max_pos;
+  const int phys = slot_block(block_tables, b, pos, mbps, block_size, num_blocks, &off);
+  const bool rope = pos >= 0 && pos < max_pos;
+  const RopeLane rl = load_rope_lane(rope ? rope_cs + (size_t)pos * rd : nullptr, rd, lane);
 
   for (int h = wave; h < nh; h += nwaves) {
     const uint16_t* src = qkv + ((size_t)b * nh + h) * kHeadDim;
@@ -60,37 +140,10 @@ __global__ __launch_bounds__(256) void attn_decode_prologue_kernel(
     const bool is_q = h < Hq;
     const bool is_v = h >= Hq + Hkv;
     if (!is_v) {
-      if (use_qk_norm) {
-        const float ss = wave_sum(x0 * x0 + x1 * x1);
-        const float r = rsqrtf(ss * (1.0f / kHeadDim) + eps);
-        const uint16_t* w = is_q ? qn_w : kn_w;
-        x0 = x0 * r * bf16_to_f32(w[lane]);
-        x1 = x1 * r * bf16_to_f32(w[lane + 64]);
-      }
-      if (rope_ok && rd > 0) {
-        // element i lives in lane i % 64, slot i / 64
-        const int i0 = lane, i1 = lane + 64;
-        const int p0 = i0 < half ? i0 + half : i0 - half;
-        const int p1 = i1 < half ? i1 + half : i1 - half;
-        const float a0 = __shfl(x0, p0 & 63), b0 = __shfl(x1, p0 & 63);
-        const float a1 = __shfl(x0, p1 & 63), b1 = __shfl(x1, p1 & 63);
-        const float y0 = (p0 >> 6) ? b0 : a0;  // value of element p0
-        const float y1 = (p1 >> 6) ? b1 : a1;
-        const float* cs = rope_cs + (size_t)pos * rd;  // [cos(half) | sin(half)]
-        float n0 = x0, n1 = x1;
-        if (i0 < rd) {
-          const int f = i0 < half ? i0 : i0 - half;
-          const float c = cs[f], s = cs[half + f];
-          n0 = i0 < half ? x0 * c - y0 * s : x0 * c + y0 * s;
-        }
-        if (i1 < rd) {
-          const int f = i1 < half ? i1 : i1 - half;
-          const float c = cs[f], s = cs[half + f];
-          n1 = i1 < half ? x1 * c - y1 * s : x1 * c + y1 * s;
-        }
-        x0 = n0;
-        x1 = n1;
-      }
+      const uint16_t* w = is_q ? qn_w : kn_w;
+      const float w0 = use_qk_norm ? bf16_to_f32(w[lane]) : 1.f;
+      const float w1 = use_qk_norm ? bf16_to_f32(w[lane + 64]) : 1.f;
+      qk_norm_rope(x0, x1, use_qk_norm != 0, w0, w1, eps, rope, rl, rd, lane);
     }
     if (is_q) {
       uint16_t* dst = q_out + ((size_t)b * Hq + h) * kHeadDim;
@@ -160,25 +213,43 @@ __global__ __launch_bounds__(256) void paged_kv_fill_kernel(
 // kernel; a sequence with a single split writes its normalised output directly. (Merging in the
 // last split to finish would need a device-scope release per workgroup; on this chip that
 // writes back the XCD's L2 each time and costs more than the separate merge launch.)
-template <int G>
+// Inputs of the fused decode step: q, k and v of the new token come packed in qkv [B, Hq+2Hkv,
+// 128] (bf16) and go through QK-norm and RoPE inside the attention kernel.
+struct FusedQKV {
+  const uint16_t* qkv;
+  const uint16_t* qn_w;  // null: no QK-norm
+  const uint16_t* kn_w;
+  const float* rope_cs;  // [max_pos, rd] = [cos | sin]
+  int max_pos;
+  int rd;
+  float eps;
+};
+
+template <int G, int TPW, bool FUSED>
 __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
-    const uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
+    const uint16_t* __restrict__ q, FusedQKV fq, uint16_t* __restrict__ k_pool,
+    uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ positions, int Hkv, int block_size, int mbps, int num_blocks,
     int max_context, float scale_log2, float* __restrict__ ws_o, float* __restrict__ ws_ml,
     int max_splits, uint16_t* __restrict__ out) {
   constexpr int D = kHeadDim;
-  __shared__ float s_p[G][kSplit];
+  constexpr int SPLIT = 4 * TPW;   // tokens per workgroup
+  constexpr int KT = TPW / 16;     // 16-token MFMA tiles per wave
+  constexpr int VS = TPW / 4;      // P.V steps per wave (4 tokens per step)
+  __shared__ __align__(16) uint16_t s_q[FUSED ? G : 1][D];     // normalised, rotated q heads
+  __shared__ __align__(16) uint16_t s_new[FUSED ? 2 : 1][D];   // new token's k and v
+  __shared__ float s_p[G][SPLIT];
   __shared__ float s_red[4][G][D];
   __shared__ float s_stat[G][4];
   __shared__ float s_fin[2][G];
-  __shared__ unsigned s_row[kSplit];  // K/V pool row of each token (always an in-bounds row)
-  __shared__ int s_ok[kSplit];        // token is inside the split and its page-table entry is valid
+  __shared__ unsigned s_row[SPLIT];  // K/V pool row of each token (always an in-bounds row)
+  __shared__ int s_ok[SPLIT];        // token is inside the split and its page-table entry is valid
 
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int Hq = Hkv * G;
   const int tid = threadIdx.x;
-  const int ctx = min(positions[b] + 1, max_context);
+  const int pos = positions[b];
+  const int ctx = min(pos + 1, max_context);
   if (ctx <= 0) {
     // nothing cached (position < 0): the output is zero
     if (split == 0)
@@ -186,16 +257,45 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
         out[((size_t)b * Hq + g * G) * D + i] = 0;
     return;
   }
-  const int t0 = split * kSplit;
+  const int t0 = split * SPLIT;
   if (t0 >= ctx) return;
-  const int t1 = min(ctx, t0 + kSplit);
-  const int nsplit = (ctx + kSplit - 1) / kSplit;
+  const int t1 = min(ctx, t0 + SPLIT);
+  const int nsplit = (ctx + SPLIT - 1) / SPLIT;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int r16 = lane & 15;
   const int kg = lane >> 4;
 
-  {
+  // Fused step: this wave's heads of the new token (q heads g*G .. g*G+G-1 and, in the
+  // workgroup of the sequence's last split, k and v of kv head g). Their qkv rows are loaded
+  // first, so that waiting for them later does not wait for the K/V rows issued after them.
+  constexpr int JPW = FUSED ? (G + 2 + 3) / 4 : 1;  // head jobs per wave
+  const bool writer = FUSED && split == (ctx - 1) / SPLIT;
+  const int n_jobs = writer ? G + 2 : G;
+  float hx[JPW][2];
+  float wq[2] = {1.f, 1.f}, wk[2] = {1.f, 1.f};
+  RopeLane rl{1.f, 0.f, 1.f, 0.f};
+  const bool rope = FUSED && pos < fq.max_pos;
+  if constexpr (FUSED) {
+    const int nh = Hq + 2 * Hkv;
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) {
+      const int job = min(wave + 4 * jj, n_jobs - 1);
+      const int h = job < G ? g * G + job : (job == G ? Hq + g : Hq + Hkv + g);
+      const uint16_t* src = fq.qkv + ((size_t)b * nh + h) * D;
+      hx[jj][0] = bf16_to_f32(src[lane]);
+      hx[jj][1] = bf16_to_f32(src[lane + 64]);
+    }
+    const uint16_t* qw = fq.qn_w ? fq.qn_w : kOnesBf16;
+    const uint16_t* kw = fq.qn_w ? fq.kn_w : kOnesBf16;
+    wq[0] = bf16_to_f32(qw[lane]);
+    wq[1] = bf16_to_f32(qw[lane + 64]);
+    wk[0] = bf16_to_f32(kw[lane]);
+    wk[1] = bf16_to_f32(kw[lane + 64]);
+    rl = load_rope_lane_nobranch(rope ? fq.rope_cs + (size_t)pos * fq.rd : kZeroRope, fq.rd,
+                                 lane);
+  }
+  if (tid < SPLIT) {
     // Pool row of every token of the split. Tokens past the sequence read the split's last
     // token instead, and tokens of an invalid page-table entry read block 0, so every K/V load
     // below is unconditional and in bounds; both are masked out of the softmax.
@@ -208,9 +308,10 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
     s_row[tid] = (unsigned)(((size_t)pb * Hkv + g) * block_size + (tc - blk * block_size));
     s_ok[tid] = valid;
   }
-  // query fragments (A operand): head r16 (rows >= G are zero), dims 8*kg + 32*j
+  // query fragments (A operand) of the plain kernel: head r16 (rows >= G are zero), dims
+  // 8*kg + 32*j
   uint4 qa[4];
-  {
+  if constexpr (!FUSED) {
     const uint16_t* qr = q + ((size_t)b * Hq + g * G + min(r16, G - 1)) * D + 8 * kg;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -218,31 +319,87 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
       qa[j] = r16 < G ? v : make_uint4(0, 0, 0, 0);
     }
   }
+  if constexpr (FUSED) {
+    // the head rows and norm/RoPE operands arrive with the page table (one round trip), before
+    // the K/V loads are issued
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) asm volatile("" ::"v"(hx[jj][0]), "v"(hx[jj][1]));
+    asm volatile("" ::"v"(wq[0]), "v"(wq[1]), "v"(wk[0]), "v"(wk[1]), "v"(rl.c0), "v"(rl.s0),
+                 "v"(rl.c1), "v"(rl.s1));
+  }
   __syncthreads();
 
+  const int wt0 = wave * TPW;  // this wave's first token in the split
   auto row_offset = [&](int tl) -> size_t { return (size_t)s_row[tl] * D; };
   // K in the MFMA B layout: tile tt of 16 tokens, token r16, dims 8*kg + 32*j
-  uint4 kb[4][4];
+  uint4 kb[KT][4];
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
-    const uint16_t* kr = k_pool + row_offset(wave * 64 + tt * 16 + r16) + 8 * kg;
+  for (int tt = 0; tt < KT; ++tt) {
+    const uint16_t* kr = k_pool + row_offset(wt0 + tt * 16 + r16) + 8 * kg;
 #pragma unroll
     for (int j = 0; j < 4; ++j) kb[tt][j] = *reinterpret_cast<const uint4*>(kr + 32 * j);
   }
   // V for P.V: step it covers tokens it*4 + kg (4 per step), lane r16 owns dims r16*8 .. +8
-  uint4 vreg[16];
+  uint4 vreg[VS];
 #pragma unroll
-  for (int it = 0; it < 16; ++it)
-    vreg[it] = *reinterpret_cast<const uint4*>(v_pool + row_offset(wave * 64 + it * 4 + kg) +
-                                               r16 * 8);
+  for (int it = 0; it < VS; ++it)
+    vreg[it] = *reinterpret_cast<const uint4*>(v_pool + row_offset(wt0 + it * 4 + kg) + r16 * 8);
+  if constexpr (FUSED) {
+    // QK-norm + RoPE of this wave's heads (K/V loads in flight), into LDS; the writer also
+    // stores k and v into the pool slot of the new token
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) {
+      const int job = wave + 4 * jj;
+      if (job < n_jobs) {
+        float x0 = hx[jj][0], x1 = hx[jj][1];
+        if (job <= G)
+          qk_norm_rope(x0, x1, fq.qn_w != nullptr, job < G ? wq[0] : wk[0],
+                       job < G ? wq[1] : wk[1], fq.eps, rope, rl, fq.rd, lane);
+        const uint16_t y0 = f32_to_bf16(x0), y1 = f32_to_bf16(x1);
+        uint16_t* dst = job < G ? s_q[job] : s_new[job - G];
+        dst[lane] = y0;
+        dst[lane + 64] = y1;
+        if (job >= G) {
+          int off = 0;
+          const int phys = slot_block(block_tables, b, pos, mbps, block_size, num_blocks, &off);
+          if (phys >= 0) {
+            uint16_t* pool = job == G ? k_pool : v_pool;
+            uint16_t* pd = pool + (((size_t)phys * Hkv + g) * block_size + off) * D;
+            pd[lane] = y0;
+            pd[lane + 64] = y1;
+          }
+        }
+      }
+    }
+    __syncthreads();
+    const uint16_t* qr = &s_q[min(r16, G - 1)][8 * kg];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 32 * j);
+      qa[j] = r16 < G ? v : make_uint4(0, 0, 0, 0);
+    }
+  }
+  if (FUSED && writer && pos < t1) {
+    // the new token's rows come from LDS (the pool slot is being written by this workgroup)
+    const int tn = pos - t0;
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt)
+      if (wt0 + tt * 16 + r16 == tn)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          kb[tt][j] = *reinterpret_cast<const uint4*>(&s_new[0][8 * kg + 32 * j]);
+#pragma unroll
+    for (int it = 0; it < VS; ++it)
+      if (wt0 + it * 4 + kg == tn) vreg[it] = *reinterpret_cast<const uint4*>(&s_new[1][r16 * 8]);
+  }
 
   // ---- scores on MFMA ----
 #pragma unroll
-  for (int tt = 0; tt < 4; ++tt) {
+  for (int tt = 0; tt < KT; ++tt) {
     floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(qa[j], kb[tt][j], sacc);
-    const int tl = wave * 64 + tt * 16 + r16;
+    const int tl = wt0 + tt * 16 + r16;
     const bool valid = s_ok[tl] != 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -252,11 +409,13 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
   }
   __syncthreads();
 
-  // ---- softmax statistics over the split (log2 domain) ----
+  // ---- softmax statistics over the split (log2 domain); lane l < TPW owns token wt0 + l ----
+  const bool mine = lane < TPW;
+  const int tm = wt0 + (lane & (TPW - 1));
   float mx[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float m = wave_max(s_p[h][tid]);
+    const float m = wave_max(mine ? s_p[h][tm] : -INFINITY);
     if (lane == 0) s_stat[h][wave] = m;
   }
   __syncthreads();
@@ -266,10 +425,10 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
   __syncthreads();
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float v = s_p[h][tid];
+    const float v = s_p[h][tm];
     const float pr = (mx[h] == -INFINITY || v == -INFINITY) ? 0.f : exp2f(v - mx[h]);
-    s_p[h][tid] = pr;
-    const float l = wave_sum(pr);
+    if (mine) s_p[h][tm] = pr;
+    const float l = wave_sum(mine ? pr : 0.f);
     if (lane == 0) s_stat[h][wave] = l;
   }
   __syncthreads();
@@ -281,8 +440,8 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
 #pragma unroll
-  for (int it = 0; it < 16; ++it) {
-    const int tl = wave * 64 + it * 4 + kg;
+  for (int it = 0; it < VS; ++it) {
+    const int tl = wt0 + it * 4 + kg;
     float vf[8];
     unpack8(vreg[it], vf);
 #pragma unroll
@@ -486,30 +645,30 @@ extern "C" size_t sym_paged_gqa_decode_workspace_bytes(int B, int Hq, int head_d
   return (size_t)B * Hq * splits * ((size_t)head_dim + 2) * sizeof(float);
 }
 
-extern "C" int sym_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
-                                    const int32_t* block_tables, const int32_t* positions, int B,
-                                    int Hq, int Hkv, int head_dim, int block_size,
-                                    int max_blocks_per_seq, int num_blocks, int max_context,
-                                    float scale, void* workspace, size_t workspace_bytes,
-                                    void* out, void* stream) {
-  int rc = check_cache_args("paged_gqa_decode", B, Hkv, head_dim, block_size, max_blocks_per_seq,
-                            num_blocks);
+// Argument checks and launch of the split kernel (plain or fused with the prologue) and the
+// merge kernel.
+static int launch_decode(const char* what, const void* q, const FusedQKV* fq, void* k_pool,
+                         void* v_pool, const int32_t* block_tables, const int32_t* positions,
+                         int B, int Hq, int Hkv, int head_dim, int block_size,
+                         int max_blocks_per_seq, int num_blocks, int max_context, float scale,
+                         void* workspace, size_t workspace_bytes, void* out, void* stream) {
+  int rc = check_cache_args(what, B, Hkv, head_dim, block_size, max_blocks_per_seq, num_blocks);
   if (rc) return rc;
   if (B == 0) return SYM_OK;
-  SYM_REQUIRE(q && k_pool && v_pool && block_tables && positions && workspace && out,
-              SYM_ERR_INVALID, "paged_gqa_decode: null pointer argument");
-  SYM_REQUIRE(Hq >= Hkv && Hq % Hkv == 0, SYM_ERR_INVALID,
-              "paged_gqa_decode: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+  SYM_REQUIRE((q || fq) && k_pool && v_pool && block_tables && positions && workspace && out,
+              SYM_ERR_INVALID, "%s: null pointer argument", what);
+  SYM_REQUIRE(Hq >= Hkv && Hq % Hkv == 0, SYM_ERR_INVALID, "%s: Hq=%d not a multiple of Hkv=%d",
+              what, Hq, Hkv);
   const int G = Hq / Hkv;
   SYM_REQUIRE(G == 1 || G == 2 || G == 4 || G == 8, SYM_ERR_UNSUPPORTED,
-              "paged_gqa_decode: group size %d not in {1,2,4,8}", G);
+              "%s: group size %d not in {1,2,4,8}", what, G);
   SYM_REQUIRE(max_context >= 1 && (long long)max_context <= (long long)max_blocks_per_seq * block_size,
-              SYM_ERR_INVALID, "paged_gqa_decode: max_context=%d outside (0, %d]", max_context,
+              SYM_ERR_INVALID, "%s: max_context=%d outside (0, %d]", what, max_context,
               max_blocks_per_seq * block_size);
-  SYM_REQUIRE(B <= 65535 && Hkv <= 65535, SYM_ERR_INVALID, "paged_gqa_decode: grid too large");
+  SYM_REQUIRE(B <= 65535 && Hkv <= 65535, SYM_ERR_INVALID, "%s: grid too large", what);
   const size_t need = sym_paged_gqa_decode_workspace_bytes(B, Hq, head_dim, max_context);
-  SYM_REQUIRE(workspace_bytes >= need, SYM_ERR_WORKSPACE,
-              "paged_gqa_decode: workspace %zu < required %zu", workspace_bytes, need);
+  SYM_REQUIRE(workspace_bytes >= need, SYM_ERR_WORKSPACE, "%s: workspace %zu < required %zu",
+              what, workspace_bytes, need);
   const int max_splits = (max_context + kSplit - 1) / kSplit;
   float* ws_o = (float*)workspace;
   float* ws_ml = ws_o + (size_t)B * Hq * max_splits * head_dim;
@@ -518,22 +677,71 @@ extern "C" int sym_paged_gqa_decode(const void* q, const void* k_pool, const voi
   (void)hipGetLastError();
   const dim3 grid(max_splits, Hkv, B), block(kAttnThreads);
   const uint16_t* qq = (const uint16_t*)q;
-  const uint16_t* kp = (const uint16_t*)k_pool;
-  const uint16_t* vp = (const uint16_t*)v_pool;
-#define SYM_LAUNCH_DECODE(GG)                                                                   \
-  hipLaunchKernelGGL(paged_decode_kernel<GG>, grid, block, 0, s, qq, kp, vp, block_tables,       \
-                     positions, Hkv, block_size, max_blocks_per_seq, num_blocks, max_context,    \
-                     scale_log2, ws_o, ws_ml, max_splits, (uint16_t*)out)
-  switch (G) {
-    case 1: SYM_LAUNCH_DECODE(1); break;
-    case 2: SYM_LAUNCH_DECODE(2); break;
-    case 4: SYM_LAUNCH_DECODE(4); break;
-    default: SYM_LAUNCH_DECODE(8); break;
+  uint16_t* kp = (uint16_t*)k_pool;
+  uint16_t* vp = (uint16_t*)v_pool;
+  const FusedQKV f = fq ? *fq : FusedQKV{};
+#define SYM_LAUNCH_DECODE(GG, FF)                                                               \
+  hipLaunchKernelGGL((paged_decode_kernel<GG, kTPW, FF>), grid, block, 0, s, qq, f, kp, vp,     \
+                     block_tables, positions, Hkv, block_size, max_blocks_per_seq, num_blocks,  \
+                     max_context, scale_log2, ws_o, ws_ml, max_splits, (uint16_t*)out)
+#define SYM_LAUNCH_DECODE_G(FF)               \
+  switch (G) {                                \
+    case 1: SYM_LAUNCH_DECODE(1, FF); break;  \
+    case 2: SYM_LAUNCH_DECODE(2, FF); break;  \
+    case 4: SYM_LAUNCH_DECODE(4, FF); break;  \
+    default: SYM_LAUNCH_DECODE(8, FF); break; \
   }
+  if (fq) {
+    SYM_LAUNCH_DECODE_G(true);
+  } else {
+    SYM_LAUNCH_DECODE_G(false);
+  }
+#undef SYM_LAUNCH_DECODE_G
 #undef SYM_LAUNCH_DECODE
   rc = sym_host::check_launch("paged_decode_kernel");
   if (rc || max_splits == 1) return rc;
   hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((B * Hq + 3) / 4), dim3(256), 0, s, ws_o,
                      ws_ml, positions, B, Hq, max_context, max_splits, (uint16_t*)out);
   return sym_host::check_launch("paged_decode_merge_kernel");
+}
+
+extern "C" int sym_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
+                                    const int32_t* block_tables, const int32_t* positions, int B,
+                                    int Hq, int Hkv, int head_dim, int block_size,
+                                    int max_blocks_per_seq, int num_blocks, int max_context,
+                                    float scale, void* workspace, size_t workspace_bytes,
+                                    void* out, void* stream) {
+  SYM_REQUIRE(B <= 0 || q, SYM_ERR_INVALID, "paged_gqa_decode: null pointer argument");
+  // the plain kernel only reads the pools
+  return launch_decode("paged_gqa_decode", q, nullptr, const_cast<void*>(k_pool),
+                       const_cast<void*>(v_pool), block_tables, positions, B, Hq, Hkv, head_dim,
+                       block_size, max_blocks_per_seq, num_blocks, max_context, scale, workspace,
+                       workspace_bytes, out, stream);
+}
+
+extern "C" int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                                    const float* rope_cs, int max_pos, const int32_t* positions,
+                                    int B, int Hq, int Hkv, int head_dim, int rotary_dim,
+                                    float eps, int use_qk_norm, void* k_pool, void* v_pool,
+                                    const int32_t* block_tables, int max_blocks_per_seq,
+                                    int block_size, int num_blocks, int max_context, float scale,
+                                    void* workspace, size_t workspace_bytes, void* out,
+                                    void* stream) {
+  SYM_REQUIRE(B <= 0 || qkv, SYM_ERR_INVALID, "attn_decode_step: null pointer argument");
+  SYM_REQUIRE(rotary_dim >= 0 && rotary_dim <= head_dim && rotary_dim % 2 == 0, SYM_ERR_INVALID,
+              "attn_decode_step: rotary_dim=%d", rotary_dim);
+  SYM_REQUIRE(rotary_dim == 0 || (rope_cs && max_pos > 0), SYM_ERR_INVALID,
+              "attn_decode_step: rope table missing");
+  SYM_REQUIRE(!use_qk_norm || (q_norm_w && k_norm_w), SYM_ERR_INVALID,
+              "attn_decode_step: QK-norm weights missing");
+  const FusedQKV fq{(const uint16_t*)qkv,
+                    use_qk_norm ? (const uint16_t*)q_norm_w : nullptr,
+                    use_qk_norm ? (const uint16_t*)k_norm_w : nullptr,
+                    rotary_dim ? rope_cs : nullptr,
+                    rotary_dim ? max_pos : 0,
+                    rotary_dim,
+                    eps};
+  return launch_decode("attn_decode_step", nullptr, &fq, k_pool, v_pool, block_tables, positions,
+                       B, Hq, Hkv, head_dim, block_size, max_blocks_per_seq, num_blocks,
+                       max_context, scale, workspace, workspace_bytes, out, stream);
 }

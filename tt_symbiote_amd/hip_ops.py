@@ -207,6 +207,57 @@ def attn_decode_prologue(qkv: torch.Tensor, positions: torch.Tensor, k_pool: tor
     return q_out
 
 
+def attn_decode_step(qkv: torch.Tensor, positions: torch.Tensor, k_pool: torch.Tensor,
+                     v_pool: torch.Tensor, block_tables: torch.Tensor, scale: float, *,
+                     num_heads: int, num_kv_heads: int, rotary_dim: int,
+                     rope_cs: Optional[torch.Tensor], q_norm_w: Optional[torch.Tensor],
+                     k_norm_w: Optional[torch.Tensor], eps: float,
+                     max_context: Optional[int] = None, workspace: Optional[torch.Tensor] = None,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The fused decode step: :func:`attn_decode_prologue` (QK-norm, RoPE, k/v written into the
+    pools at ``positions``) and :func:`paged_gqa_decode` in one pass; returns the attention
+    output [B, Hq, D]."""
+    _check(qkv, "qkv", torch.bfloat16)
+    B = qkv.shape[0]
+    _check_shape(qkv, "qkv", (B, (num_heads + 2 * num_kv_heads) * HEAD_DIM))
+    _check(positions, "positions", torch.int32, qkv.device)
+    _check_shape(positions, "positions", (B,))
+    lay = _check_pools(k_pool, v_pool, block_tables, B)
+    if lay.num_kv_heads != num_kv_heads:
+        raise ValueError(f"pool has {lay.num_kv_heads} kv heads, module {num_kv_heads}")
+    use_norm = q_norm_w is not None
+    if use_norm:
+        for t, n in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+            _check(t, n, torch.bfloat16, qkv.device)
+            _check_shape(t, n, (HEAD_DIM,))
+    max_pos = 0
+    if rotary_dim:
+        _check(rope_cs, "rope_cs", torch.float32, qkv.device)
+        if rope_cs.dim() != 2 or rope_cs.shape[1] != rotary_dim:
+            raise ValueError(f"rope_cs must be [max_pos, {rotary_dim}], got {tuple(rope_cs.shape)}")
+        max_pos = rope_cs.shape[0]
+    cap = lay.max_blocks_per_seq * lay.block_size
+    if max_context is None:
+        max_context = cap
+    if not 0 < max_context <= cap:
+        raise ValueError(f"max_context {max_context} outside (0, {cap}]")
+    need = paged_decode_workspace_bytes(B, num_heads, max_context)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=qkv.device)
+    _check(workspace, "workspace", torch.uint8, qkv.device)
+    if out is None:
+        out = torch.empty(B, num_heads, HEAD_DIM, dtype=torch.bfloat16, device=qkv.device)
+    _check(out, "out", torch.bfloat16, qkv.device)
+    _check_shape(out, "out", (B, num_heads, HEAD_DIM))
+    _timed("paged_gqa_decode", lambda: _lib.call(
+        "sym_attn_decode_step", _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope_cs),
+        max_pos, _ptr(positions), B, num_heads, num_kv_heads, HEAD_DIM, rotary_dim, float(eps),
+        1 if use_norm else 0, _ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
+        lay.max_blocks_per_seq, lay.block_size, lay.num_blocks, int(max_context), float(scale),
+        _ptr(workspace), workspace.numel(), _ptr(out), _stream()))
+    return out
+
+
 def paged_kv_write(k_new: torch.Tensor, v_new: torch.Tensor, k_pool: torch.Tensor,
                    v_pool: torch.Tensor, block_tables: torch.Tensor,
                    positions: torch.Tensor) -> None:

@@ -10,8 +10,8 @@ layout (no Meta-interleave permutation: that layout exists for TT's rotary kerne
 
 Decode step (``seq_len == 1`` with a paged cache; ttnn_attention.py:2308-2466):
   qkv  = x W_qkv^T (+b)                          skinny-GEMM kernel
-  q, K/V slot write = one prologue kernel         QK RMSNorm, partial RoPE, paged KV write
-  o    = paged GQA decode kernel (split-K + merge)
+  o    = fused decode step (split-K + merge)     QK RMSNorm, partial RoPE, paged KV write and
+                                                  paged GQA decode in one pass
   out  = o W_dense^T (+b)                         skinny-GEMM kernel
 Positions are per-sequence device int32 (``cache_position`` / ``position_ids`` per row); when
 absent, the cache's host counter is used for every row, as in the reference.
@@ -179,12 +179,10 @@ class HIPBailingMoEAttention(StatefulHIPModule):
         vp = cache.value_cache(self.layer_idx)
         pt = cache.page_table_device
         qkv = hip_ops.linear(x, d["qkv_w"], d["qkv_b"])
-        q = hip_ops.attn_decode_prologue(
-            qkv, pos, kp, vp, pt, num_heads=self.num_heads, num_kv_heads=self.num_kv_heads,
-            rotary_dim=self.rotary_dim, rope_cs=d["rope"], q_norm_w=d["q_norm"],
-            k_norm_w=d["k_norm"], eps=self.norm_eps)
-        o = hip_ops.paged_gqa_decode(q, kp, vp, pt, pos, self.scaling,
-                                     max_context=cache.max_context,
-                                     workspace=cache.decode_workspace(B, self.num_heads))
+        o = hip_ops.attn_decode_step(
+            qkv, pos, kp, vp, pt, self.scaling, num_heads=self.num_heads,
+            num_kv_heads=self.num_kv_heads, rotary_dim=self.rotary_dim, rope_cs=d["rope"],
+            q_norm_w=d["q_norm"], k_norm_w=d["k_norm"], eps=self.norm_eps,
+            max_context=cache.max_context, workspace=cache.decode_workspace(B, self.num_heads))
         out = hip_ops.linear(o.view(B, self.num_heads * self.head_dim), d["dense_w"], d["dense_b"])
         return out.view(B, 1, H), None, cache
