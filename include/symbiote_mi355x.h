@@ -65,6 +65,27 @@ int sym_rmsnorm_bf16(const void* x, const void* residual, const void* weight, in
 int sym_linear_bf16(const void* x, const void* w, const void* bias, int M, int N, int K,
                     void* out, int out_fp32, void* stream);
 
+/* Projection with the RMSNorm of x fused in front (the decoder layer's input_layernorm,
+ * modeling_bailing_moe_v2.py:440-442, feeding the query_key_value linear):
+ *   out = bf16(x * rsqrt(mean(x^2) + eps) * gamma) . w^T (+ bias), gamma [K] bf16; the
+ *   normalised operand is rounded to bf16 as a separate RMSNorm pass would.
+ * Constraints as sym_linear_bf16.
+ */
+int sym_rmsnorm_linear_bf16(const void* x, const void* gamma, float eps, const void* w,
+                            const void* bias, int M, int N, int K, void* out, int out_fp32,
+                            void* stream);
+
+/* Projection with the residual add fused behind (the dense linear plus the decoder layer's
+ * first residual add, ttnn_attention.py:2459 and modeling_bailing_moe_v2.py:457-460):
+ *   out [M, N] fp32 = x . w^T (+ bias) + residual (bf16 [M, N]), with no intermediate rounding;
+ *   sumsq_parts [N/16, M] fp32: sum over each 16-column block of out's row of out^2, the
+ *   statistics of the following RMSNorm (see sym_moe_router_logits_norm).
+ * Constraints as sym_linear_bf16.
+ */
+int sym_linear_residual_bf16(const void* x, const void* w, const void* bias,
+                             const void* residual, int M, int N, int K, float* out,
+                             float* sumsq_parts, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Decode prologue: per-head QK RMSNorm, partial split-half RoPE, paged KV write.
  * Replaces TTNNBailingMoEAttention._forward_decode_paged's split / _apply_qk_norm / RoPE /
@@ -150,10 +171,22 @@ int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const void* k_no
  *   parts [4, T, E] fp32: parts[q] = x[:, Hq] . w[:, Hq]^T over the q-th quarter of H.
  * The logits are ((parts[0] + parts[1]) + parts[2]) + parts[3], summed in that order by
  * sym_moe_route_permute (n_logit_parts = 4), so routing does not depend on launch order.
- * H % 256 == 0, E % 16 == 0.
+ * H % 512 == 0, E % 16 == 0.
  */
 int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E, float* parts,
                           void* stream);
+
+/* Router logits with the post-attention RMSNorm fused in front (the decoder layer's
+ * post_attention_layernorm, modeling_bailing_moe_v2.py:463-465, feeding TTNNMoE.forward):
+ *   h [T, H] fp32 residual stream; ss_parts [n_ss, T] fp32 partial sums of squares of h's rows
+ *   (sum over all n_ss gives sum_k h[t,k]^2; as written by sym_linear_residual_bf16);
+ *   xn = bf16(h * rsqrt(sum/H + eps) * gamma) (gamma [H] bf16) is the operand of the logits, as
+ *   sym_moe_router_logits on xn; when xn_out (bf16 [T, H]) is non-NULL it also receives xn,
+ *   the input of the expert GEMMs.
+ */
+int sym_moe_router_logits_norm(const float* h, const float* ss_parts, int n_ss,
+                               const void* gamma, float eps, const float* w, int T, int H, int E,
+                               float* parts, void* xn_out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Fused MoE router + top-k + permute.

@@ -145,7 +145,8 @@ def test_route_from_logit_parts_bit_exact(device):
     assert np.array_equal(res.topk_w.cpu().numpy(), w_ref)
 
 
-@pytest.mark.parametrize("T,H,E", [(1, 2048, 256), (32, 2048, 256), (40, 512, 64), (128, 2048, 512)])
+@pytest.mark.parametrize("T,H,E", [(1, 2048, 256), (32, 2048, 256), (40, 512, 64), (128, 2048, 512),
+                                   (16, 4096, 128)])
 def test_router_logits(device, T, H, E):
     g = torch.Generator().manual_seed(T + E)
     x = torch.randn(T, H, generator=g).bfloat16()
@@ -180,6 +181,62 @@ def test_linear(device, M, N, K, bias, out_dtype):
         torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=1e-4)
     else:
         _close(out, ref, atol=2e-3, rtol=8e-3)
+
+
+def _rmsnorm_bf16(x, gamma, eps):
+    xf = x.float()
+    r = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * r * gamma.float()).bfloat16()
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(32, 3072, 2048, False), (1, 256, 2048, True),
+                                        (70, 128, 192, True)])
+def test_rmsnorm_linear(device, M, N, K, bias):
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    x = (torch.randn(M, K, generator=g) * 1.5).bfloat16()
+    gamma = (1 + 0.1 * torch.randn(K, generator=g)).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(N, generator=g) * 0.1).bfloat16() if bias else None
+    out = hip_ops.rmsnorm_linear(x.to(device), gamma.to(device), 1e-6, w.to(device),
+                                 None if b is None else b.to(device), out_dtype=torch.float32)
+    xn = _rmsnorm_bf16(x, gamma, 1e-6)     # the operand a separate RMSNorm pass would write
+    ref = xn.float() @ w.float().T + (b.float() if b is not None else 0.0)
+    # the row statistics are summed in another order, which can move an operand by one bf16
+    # ulp (2^-8 relative) now and then
+    torch.testing.assert_close(out.cpu(), ref, rtol=2e-3, atol=2e-3)
+    out_bf = hip_ops.rmsnorm_linear(x.to(device), gamma.to(device), 1e-6, w.to(device),
+                                    None if b is None else b.to(device))
+    _close(out_bf, ref, atol=3e-3, rtol=8e-3)
+
+
+@pytest.mark.parametrize("M,N,K", [(32, 2048, 2048), (5, 256, 512), (40, 128, 192)])
+def test_linear_residual(device, M, N, K):
+    g = torch.Generator().manual_seed(M + 7 * N + K)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(N, generator=g) * 0.1).bfloat16()
+    res = torch.randn(M, N, generator=g).bfloat16()
+    out, parts = hip_ops.linear_residual(x.to(device), w.to(device), res.to(device),
+                                         b.to(device))
+    ref = x.float() @ w.float().T + b.float() + res.float()
+    torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=1e-4)
+    ss = out.cpu().double().pow(2).view(M, N // 16, 16).sum(-1).T
+    torch.testing.assert_close(parts.cpu().double(), ss, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("T,H,E", [(32, 2048, 256), (1, 2048, 256), (20, 4096, 64)])
+def test_router_logits_norm(device, T, H, E):
+    g = torch.Generator().manual_seed(T + H + E)
+    h = torch.randn(T, H, generator=g) * 1.3
+    gamma = (1 + 0.1 * torch.randn(H, generator=g)).bfloat16()
+    w = (torch.randn(E, H, generator=g) * 0.02).float()
+    ss = h.double().pow(2).view(T, H // 16, 16).sum(-1).T.float().contiguous()
+    parts, xn = hip_ops.moe_router_logits_norm(h.to(device), ss.to(device), gamma.to(device),
+                                               1e-6, w.to(device))
+    xn_ref = _rmsnorm_bf16(h, gamma, 1e-6)
+    _close(xn, xn_ref.float(), atol=1e-6, rtol=8e-3)  # at most one bf16 ulp apart
+    ref = xn.cpu().double() @ w.double().T            # logits of the operand actually used
+    torch.testing.assert_close(parts.cpu().double().sum(0), ref, rtol=1e-5, atol=1e-5)
 
 
 # ------------------------------------------------------------------------------- grouped GEMM

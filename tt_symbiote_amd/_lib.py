@@ -51,6 +51,15 @@ _SIGNATURES = {
          _vp],
     ),
     "sym_linear_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]),
+    "sym_rmsnorm_linear_bf16": (
+        _c_int, [_vp, _vp, _c_float, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]
+    ),
+    "sym_linear_residual_bf16": (
+        _c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]
+    ),
+    "sym_moe_router_logits_norm": (
+        _c_int, [_vp, _vp, _c_int, _vp, _c_float, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]
+    ),
     "sym_moe_router_logits": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "sym_moe_route_workspace_bytes": (_c_size, [_c_int, _c_int]),
     "sym_moe_route_permute": (

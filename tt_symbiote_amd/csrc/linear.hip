@@ -1,107 +1,282 @@
-// Skinny bf16 GEMM for the decode projections: out[M, N] = x[M, K] . w[N, K]^T (+ bias[N]).
+// Skinny bf16 GEMMs for the decode projections: out[M, N] = x[M, K] . w[N, K]^T (+ bias[N]),
+// optionally with the RMSNorm of x fused in front and the residual add + the next RMSNorm's
+// statistics fused behind.
 //
 // Reference: the fused query_key_value projection and the dense output projection of
 // TTNNBailingMoEAttention._forward_decode_paged (ttnn_attention.py:2324, 2459), weights built at
-// ttnn_attention.py:2001-2011.
+// ttnn_attention.py:2001-2011; the decoder layer's input_layernorm before the attention and the
+// residual add + post_attention_layernorm after it (modeling_bailing_moe_v2.py:440-468;
+// RMSNorm of DeepseekV2RMSNorm, ttnn_normalization.py:54-68).
 //
-// Design (gfx950): at decode sizes (M = batch <= 64) the GEMM streams its weights once. One
-// workgroup owns 16 output columns; its 4 waves split K into contiguous K-step ranges, issue the
-// weight and activation loads of U K-steps per batch before their MFMAs
-// (v_mfma_f32_16x16x32_bf16, weight rows as the B operand, up to MT 16-row tiles of x as A), and
-// reduce their partial accumulators through LDS. Output in bf16 or fp32.
+// Design (gfx950): at decode sizes (M = batch <= 64) a projection streams its weights once. One
+// workgroup of 8 waves owns 16 output columns; the waves split K into contiguous K-step ranges
+// (K = 2048: 4 steps of 64 each, one batch of loads), issue the weight loads and then the
+// activation loads of a batch before its v_mfma_f32_16x16x32_bf16 (weight rows as the B
+// operand, MT 16-row tiles of x as A), and reduce their partial accumulators through LDS.
+//   NORM: the workgroup first reads its rows' activations once more for the sum of squares
+//         (8 waves x their K range, reduced through LDS), then forms the MFMA operand
+//         bf16(x * r * gamma) in registers: the same rounding as a separate RMSNorm pass.
+//   RES:  the epilogue adds bias and the bf16 residual in fp32, writes the fp32 row and each
+//         row's sum of squares over the workgroup's 16 columns (the statistics of the next
+//         RMSNorm, finished by its consumer).
 #include "common.h"
 
 namespace sym {
 
-template <int MT, int U>
-__global__ __launch_bounds__(256) void linear_bf16_kernel(
+constexpr int kLinWaves = 8;
+constexpr int kLinThreads = kLinWaves * 64;
+
+__device__ __forceinline__ uint4 ldg16(const uint16_t* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// bf16(x * r * g) for 8 packed bf16 x and g values (left-to-right products, as the RMSNorm
+// kernel).
+__device__ __forceinline__ uint4 scale8(uint4 xv, uint4 gv, float r) {
+  float xf[8], gf[8];
+  unpack8(xv, xf);
+  unpack8(gv, gf);
+  uint4 o;
+  o.x = pack_bf16x2(xf[0] * r * gf[0], xf[1] * r * gf[1]);
+  o.y = pack_bf16x2(xf[2] * r * gf[2], xf[3] * r * gf[3]);
+  o.z = pack_bf16x2(xf[4] * r * gf[4], xf[5] * r * gf[5]);
+  o.w = pack_bf16x2(xf[6] * r * gf[6], xf[7] * r * gf[7]);
+  return o;
+}
+
+__device__ __forceinline__ float sumsq8(uint4 v) {
+  float f[8];
+  unpack8(v, f);
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) s = fmaf(f[i], f[i], s);
+  return s;
+}
+
+// One batch of S K-steps starting at step st: weight loads, activation loads (and gamma when
+// NORM), then the MFMAs.
+template <int MT, int S, bool NORM>
+__device__ __forceinline__ void proj_batch(const uint16_t* __restrict__ wr,
+                                           const uint16_t* const (&xr)[MT],
+                                           const uint16_t* __restrict__ gr, const float (&rr)[MT],
+                                           int st, int nmt, floatx4 (&acc)[MT]) {
+  uint4 b[S][2], a[MT][S][2], gm[NORM ? S : 1][2];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int k = (st + s) << 6;
+    b[s][0] = ldg16(wr + k);
+    b[s][1] = ldg16(wr + k + 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int k = (st + s) << 6;
+      a[mt][s][0] = ldg16(xr[mt] + k);
+      a[mt][s][1] = ldg16(xr[mt] + k + 8);
+    }
+  if constexpr (NORM) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int k = (st + s) << 6;
+      gm[s][0] = ldg16(gr + k);
+      gm[s][1] = ldg16(gr + k + 8);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // every tile is computed (rows past M repeat row M-1; their results are dropped): a branch
+  // on the tile count would let the compiler sink the tile's loads behind the first MFMAs
+  (void)nmt;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      uint4 a0 = a[mt][s][0], a1 = a[mt][s][1];
+      if constexpr (NORM) {
+        a0 = scale8(a0, gm[s][0], rr[mt]);
+        a1 = scale8(a1, gm[s][1], rr[mt]);
+      }
+      acc[mt] = mfma16x16x32(a0, b[s][0], acc[mt]);
+      acc[mt] = mfma16x16x32(a1, b[s][1], acc[mt]);
+    }
+  }
+}
+
+// Sum of squares of this lane's row (tile mt) over S K-steps starting at st (loads batched).
+template <int MT, int S>
+__device__ __forceinline__ void sumsq_batch(const uint16_t* const (&xr)[MT], int st,
+                                            float (&ss)[MT]) {
+  uint4 a[MT][S][2];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const int k = (st + s) << 6;
+      a[mt][s][0] = ldg16(xr[mt] + k);
+      a[mt][s][1] = ldg16(xr[mt] + k + 8);
+    }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int s = 0; s < S; ++s) ss[mt] += sumsq8(a[mt][s][0]) + sumsq8(a[mt][s][1]);
+}
+
+template <int MT, int U, bool NORM, bool RES>
+__global__ __launch_bounds__(kLinThreads) void proj_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
-    const uint16_t* __restrict__ bias, int M, int N, int K, uint16_t* __restrict__ out_bf16,
-    float* __restrict__ out_f32) {
-  __shared__ float s_red[4][MT][4][64];
+    const uint16_t* __restrict__ bias, int M, int N, int K, const uint16_t* __restrict__ gamma,
+    float eps, const uint16_t* __restrict__ residual, float* __restrict__ sumsq_parts,
+    uint16_t* __restrict__ out_bf16, float* __restrict__ out_f32) {
+  __shared__ float s_red[kLinWaves][MT][4][64];
+  __shared__ float s_ss[NORM ? kLinWaves : 1][16 * MT];
+  __shared__ float s_r[16 * MT];
   const int col0 = blockIdx.x * 16;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
   const int nsteps = K >> 6;
-  const int s_beg = (wave * nsteps) >> 2;
-  const int s_end = ((wave + 1) * nsteps) >> 2;
+  const int s_beg = (wave * nsteps) / kLinWaves;
+  const int s_end = ((wave + 1) * nsteps) / kLinWaves;
   const uint16_t* wr = w + (size_t)(col0 + r16) * K + kq * 16;
+  const uint16_t* gr = NORM ? gamma + kq * 16 : nullptr;
 
   for (int mb = 0; mb < M; mb += 16 * MT) {
     const int nmt = min(MT, (M - mb + 15) >> 4);
     floatx4 acc[MT];
     const uint16_t* xr[MT];
+    float rr[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
       // rows past M read row M-1 (in bounds); their outputs are dropped
       xr[mt] = x + (size_t)min(mb + mt * 16 + r16, M - 1) * K + kq * 16;
+      rr[mt] = 1.f;
     }
-    int st = s_beg;
-    for (; st + U <= s_end; st += U) {
-      uint4 b[U][2], a[MT][U][2];
-#pragma unroll
-      for (int s = 0; s < U; ++s) {
-        const int k = (st + s) << 6;
-        b[s][0] = *reinterpret_cast<const uint4*>(wr + k);
-        b[s][1] = *reinterpret_cast<const uint4*>(wr + k + 8);
-      }
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+    bool done = false;
+    if constexpr (NORM) {
+      if (nsteps == U * kLinWaves) {
+        // one batch per wave: weights, activations and gamma in flight together; the sums of
+        // squares come from the activation registers, and the same registers feed the MFMAs
+        uint4 b[U][2], a[MT][U][2], gm[U][2];
 #pragma unroll
         for (int s = 0; s < U; ++s) {
-          const int k = (st + s) << 6;
-          a[mt][s][0] = *reinterpret_cast<const uint4*>(xr[mt] + k);
-          a[mt][s][1] = *reinterpret_cast<const uint4*>(xr[mt] + k + 8);
+          const int k = (s_beg + s) << 6;
+          b[s][0] = ldg16(wr + k);
+          b[s][1] = ldg16(wr + k + 8);
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        if (mt < nmt) {
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
           for (int s = 0; s < U; ++s) {
-            acc[mt] = mfma16x16x32(a[mt][s][0], b[s][0], acc[mt]);
-            acc[mt] = mfma16x16x32(a[mt][s][1], b[s][1], acc[mt]);
+            const int k = (s_beg + s) << 6;
+            a[mt][s][0] = ldg16(xr[mt] + k);
+            a[mt][s][1] = ldg16(xr[mt] + k + 8);
+          }
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          const int k = (s_beg + s) << 6;
+          gm[s][0] = ldg16(gr + k);
+          gm[s][1] = ldg16(gr + k + 8);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          float v = 0.f;
+#pragma unroll
+          for (int s = 0; s < U; ++s) v += sumsq8(a[mt][s][0]) + sumsq8(a[mt][s][1]);
+          v += __shfl_xor(v, 16);
+          v += __shfl_xor(v, 32);
+          if (kq == 0) s_ss[wave][mt * 16 + r16] = v;
+        }
+        __syncthreads();
+        if (threadIdx.x < 16 * MT) {
+          float t = 0.f;
+#pragma unroll
+          for (int i = 0; i < kLinWaves; ++i) t += s_ss[i][threadIdx.x];
+          s_r[threadIdx.x] = rsqrtf(t / (float)K + eps);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const float r = s_r[mt * 16 + r16];
+#pragma unroll
+          for (int s = 0; s < U; ++s) {
+            acc[mt] = mfma16x16x32(scale8(a[mt][s][0], gm[s][0], r), b[s][0], acc[mt]);
+            acc[mt] = mfma16x16x32(scale8(a[mt][s][1], gm[s][1], r), b[s][1], acc[mt]);
           }
         }
+        done = true;
       }
     }
-    for (; st < s_end; ++st) {
-      const int k = st << 6;
-      const uint4 b0 = *reinterpret_cast<const uint4*>(wr + k);
-      const uint4 b1 = *reinterpret_cast<const uint4*>(wr + k + 8);
+    if (!done) {
+      if constexpr (NORM) {
+        // sum of squares of each row over this wave's K range, then over the 8 waves
+        float ss[MT];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint4 a0 = *reinterpret_cast<const uint4*>(xr[mt] + k);
-        const uint4 a1 = *reinterpret_cast<const uint4*>(xr[mt] + k + 8);
-        if (mt < nmt) {
-          acc[mt] = mfma16x16x32(a0, b0, acc[mt]);
-          acc[mt] = mfma16x16x32(a1, b1, acc[mt]);
+        for (int mt = 0; mt < MT; ++mt) ss[mt] = 0.f;
+        {
+          int st = s_beg;
+          for (; st + U <= s_end; st += U) sumsq_batch<MT, U>(xr, st, ss);
+          for (; st < s_end; ++st) sumsq_batch<MT, 1>(xr, st, ss);
         }
-      }
-    }
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      if (mt < nmt) {
+        for (int mt = 0; mt < MT; ++mt) {
+          float v = ss[mt];
+          v += __shfl_xor(v, 16);
+          v += __shfl_xor(v, 32);
+          if (kq == 0) s_ss[wave][mt * 16 + r16] = v;
+        }
+        __syncthreads();
+        if (threadIdx.x < 16 * MT) {
+          float t = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) s_red[wave][mt][i][lane] = acc[mt][i];
+          for (int i = 0; i < kLinWaves; ++i) t += s_ss[i][threadIdx.x];
+          s_r[threadIdx.x] = rsqrtf(t / (float)K + eps);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) rr[mt] = s_r[mt * 16 + r16];
       }
+      int st = s_beg;
+      for (; st + U <= s_end; st += U) proj_batch<MT, U, NORM>(wr, xr, gr, rr, st, nmt, acc);
+      for (; st < s_end; ++st) proj_batch<MT, 1, NORM>(wr, xr, gr, rr, st, nmt, acc);
     }
+
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_red[wave][mt][i][lane] = acc[mt][i];
     __syncthreads();
-    {
+    if (threadIdx.x < 256 * MT) {
+      // thread -> element i of lane l's fragment of tile mt: row 4*(l/16)+i, column l%16
+      const int mt = threadIdx.x >> 8;
       const int l = threadIdx.x & 63;
-      const int i = threadIdx.x >> 6;
+      const int i = (threadIdx.x >> 6) & 3;
+      const int row = mb + mt * 16 + 4 * (l >> 4) + i;
       const int col = col0 + (l & 15);
-      const float bv = bias ? bf16_to_f32(bias[col]) : 0.f;
-      for (int mt = 0; mt < nmt; ++mt) {
-        const int row = mb + mt * 16 + 4 * (l >> 4) + i;
-        const float v = (s_red[0][mt][i][l] + s_red[1][mt][i][l]) +
-                        (s_red[2][mt][i][l] + s_red[3][mt][i][l]) + bv;
-        if (row < M) {
-          if (out_f32) out_f32[(size_t)row * N + col] = v;
-          else out_bf16[(size_t)row * N + col] = f32_to_bf16(v);
+      float v = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < kLinWaves; ++wv) v += s_red[wv][mt][i][l];
+      if (bias) v += bf16_to_f32(bias[col]);
+      const bool ok = row < M;
+      if constexpr (RES) {
+        if (ok) {
+          v += bf16_to_f32(residual[(size_t)row * N + col]);
+          out_f32[(size_t)row * N + col] = v;
         }
+        // sum of squares over the 16 columns of this row (16 consecutive lanes)
+        float q = ok ? v * v : 0.f;
+        q += __shfl_xor(q, 1);
+        q += __shfl_xor(q, 2);
+        q += __shfl_xor(q, 4);
+        q += __shfl_xor(q, 8);
+        if (ok && (l & 15) == 0) sumsq_parts[(size_t)blockIdx.x * M + row] = q;
+      } else if (ok) {
+        if (out_f32) out_f32[(size_t)row * N + col] = v;
+        else out_bf16[(size_t)row * N + col] = f32_to_bf16(v);
       }
     }
     __syncthreads();
@@ -112,18 +287,60 @@ __global__ __launch_bounds__(256) void linear_bf16_kernel(
 
 using namespace sym;
 
+static int check_proj(const char* what, const void* x, const void* w, int M, int N, int K) {
+  SYM_REQUIRE(M >= 0, SYM_ERR_INVALID, "%s: M=%d < 0", what, M);
+  SYM_REQUIRE(M == 0 || (x && w), SYM_ERR_INVALID, "%s: null pointer argument", what);
+  SYM_REQUIRE(N > 0 && N % 16 == 0 && N / 16 <= 2147483647, SYM_ERR_UNSUPPORTED,
+              "%s: N=%d must be a positive multiple of 16", what, N);
+  SYM_REQUIRE(K > 0 && K % 64 == 0, SYM_ERR_UNSUPPORTED,
+              "%s: K=%d must be a positive multiple of 64", what, K);
+  return SYM_OK;
+}
+
+template <bool NORM, bool RES>
+static void launch_proj(const void* x, const void* w, const void* bias, int M, int N, int K,
+                        const void* gamma, float eps, const void* residual, float* sumsq_parts,
+                        void* out_bf16, float* out_f32, hipStream_t s) {
+  hipLaunchKernelGGL((proj_kernel<2, 4, NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
+                     (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
+                     (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
+                     (uint16_t*)out_bf16, out_f32);
+}
+
 extern "C" int sym_linear_bf16(const void* x, const void* w, const void* bias, int M, int N,
                                int K, void* out, int out_fp32, void* stream) {
-  SYM_REQUIRE(M >= 0, SYM_ERR_INVALID, "linear_bf16: M=%d < 0", M);
-  if (M == 0) return SYM_OK;
-  SYM_REQUIRE(x && w && out, SYM_ERR_INVALID, "linear_bf16: null pointer argument");
-  SYM_REQUIRE(N > 0 && N % 16 == 0, SYM_ERR_UNSUPPORTED,
-              "linear_bf16: N=%d must be a positive multiple of 16", N);
-  SYM_REQUIRE(K > 0 && K % 64 == 0, SYM_ERR_UNSUPPORTED,
-              "linear_bf16: K=%d must be a positive multiple of 64", K);
+  int rc = check_proj("linear_bf16", x, w, M, N, K);
+  if (rc || M == 0) return rc;
+  SYM_REQUIRE(out, SYM_ERR_INVALID, "linear_bf16: null pointer argument");
   (void)hipGetLastError();
-  hipLaunchKernelGGL((linear_bf16_kernel<2, 4>), dim3(N / 16), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
-                     out_fp32 ? nullptr : (uint16_t*)out, out_fp32 ? (float*)out : nullptr);
-  return sym_host::check_launch("linear_bf16_kernel");
+  launch_proj<false, false>(x, w, bias, M, N, K, nullptr, 0.f, nullptr, nullptr,
+                            out_fp32 ? nullptr : out, out_fp32 ? (float*)out : nullptr,
+                            (hipStream_t)stream);
+  return sym_host::check_launch("proj_kernel");
+}
+
+extern "C" int sym_rmsnorm_linear_bf16(const void* x, const void* gamma, float eps,
+                                       const void* w, const void* bias, int M, int N, int K,
+                                       void* out, int out_fp32, void* stream) {
+  int rc = check_proj("rmsnorm_linear_bf16", x, w, M, N, K);
+  if (rc || M == 0) return rc;
+  SYM_REQUIRE(gamma && out, SYM_ERR_INVALID, "rmsnorm_linear_bf16: null pointer argument");
+  (void)hipGetLastError();
+  launch_proj<true, false>(x, w, bias, M, N, K, gamma, eps, nullptr, nullptr,
+                           out_fp32 ? nullptr : out, out_fp32 ? (float*)out : nullptr,
+                           (hipStream_t)stream);
+  return sym_host::check_launch("proj_kernel");
+}
+
+extern "C" int sym_linear_residual_bf16(const void* x, const void* w, const void* bias,
+                                        const void* residual, int M, int N, int K, float* out,
+                                        float* sumsq_parts, void* stream) {
+  int rc = check_proj("linear_residual_bf16", x, w, M, N, K);
+  if (rc || M == 0) return rc;
+  SYM_REQUIRE(residual && out && sumsq_parts, SYM_ERR_INVALID,
+              "linear_residual_bf16: null pointer argument");
+  (void)hipGetLastError();
+  launch_proj<false, true>(x, w, bias, M, N, K, nullptr, 0.f, residual, sumsq_parts, nullptr,
+                           out, (hipStream_t)stream);
+  return sym_host::check_launch("proj_kernel");
 }

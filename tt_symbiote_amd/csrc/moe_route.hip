@@ -337,46 +337,152 @@ __global__ __launch_bounds__(kPermuteThreads) void moe_permute_kernel(
 }
 
 // Router logits in fp32 with v_mfma_f32_16x16x4_f32: parts[q][t][e] = sum over the q-th
-// quarter of H of x[t][k] * w[e][k]. One workgroup per (16 experts, quarter of H); its 4 waves
-// split the quarter again and reduce through LDS; every wave covers all token tiles, so each
-// weight element is read once. Lane l streams 4 consecutive k of weight row l%16 (16 bytes)
-// and the matching 4 activations; the 4 MFMAs of a 16-wide k chunk use one element each, so A
-// and B agree on the k order.
-__global__ __launch_bounds__(256) void moe_router_logits_kernel(
-    const uint16_t* __restrict__ x, const float* __restrict__ w, int T, int H, int E,
-    float* __restrict__ parts) {
-  __shared__ float s_red[4][4][64];
+// quarter of H of x[t][k] * w[e][k]. One workgroup of 8 waves per (16 experts, quarter of H);
+// each wave owns H/32 consecutive k of the quarter and issues its weight loads (16 bytes per lane
+// per 16-wide k chunk: 4 consecutive k of weight row l%16) four chunks at a time ahead of the
+// activation loads; the 8 partial accumulators reduce through LDS. The 4 MFMAs of a 16-wide
+// k chunk use one element each of the lane's 4 consecutive k, so A and B agree on the k order.
+// NORM: the activations are the fp32 residual stream h [T, H] and the kernel applies the
+// RMSNorm in front: r[t] = rsqrt(sum(ss_parts[:, t]) / H + eps) from the per-16-column sums of
+// squares written by the producer of h, and the operand is bf16(h * r * gamma) (the rounding of
+// a separate RMSNorm pass), upcast. The workgroups of the first expert tile also store that
+// normalised row (bf16) for the expert GEMMs.
+constexpr int kLogitWaves = 8;
+constexpr int kLogitRows = 32;  // token rows per pass (two 16-row tiles)
+
+template <bool NORM>
+__global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
+    const uint16_t* __restrict__ x, const float* __restrict__ hres,
+    const float* __restrict__ ss_parts, int n_ss, const uint16_t* __restrict__ gamma, float eps,
+    const float* __restrict__ w, int T, int H, int E, float* __restrict__ parts,
+    uint16_t* __restrict__ xn_out) {
+  __shared__ float s_red[kLogitWaves][2][4][64];
+  __shared__ float s_r[kLogitRows];
   const int ntile = blockIdx.x;
   const int q = blockIdx.y;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
-  const int quarter = H >> 2;            // H % 256 == 0
-  const int sub = quarter >> 2;           // this wave's share, a multiple of 16
-  const int k_beg = q * quarter + wave * sub;
-  const float* wr = w + (size_t)(ntile * 16 + r16) * H + kq * 4;
-  for (int mb = 0; mb < T; mb += 16) {
-    const int m = min(mb + r16, T - 1);  // rows past T repeat the last row; dropped below
-    const uint16_t* xr = x + (size_t)m * H + kq * 4;
-    floatx4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 4
-    for (int k = k_beg; k < k_beg + sub; k += 16) {
-      const float4 b = *reinterpret_cast<const float4*>(wr + k);
-      const uint2 av = *reinterpret_cast<const uint2*>(xr + k);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bf16_lo(av.x), b.x, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bf16_hi(av.x), b.y, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bf16_lo(av.y), b.z, acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(bf16_hi(av.y), b.w, acc, 0, 0, 0);
+  const int quarter = H >> 2;
+  const int sub = quarter / kLogitWaves;              // a multiple of 16 (H % 512 == 0)
+  const int k_beg = q * quarter + wave * sub + kq * 4;
+  const int nk = sub >> 4;                            // 16-wide k chunks of this wave
+  const float* wr = w + (size_t)(ntile * 16 + r16) * H + k_beg;
+  for (int mb = 0; mb < T; mb += kLogitRows) {
+    float rm[2] = {1.f, 1.f};
+    // rows past T repeat the last row; their results are dropped
+    const int m0 = min(mb + r16, T - 1), m1 = min(mb + 16 + r16, T - 1);
+    floatx4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    for (int kc = 0; kc < nk; kc += 4) {
+      // a group of up to 4 chunks: weights, activations (and gamma) issued first; chunks past
+      // the range repeat the last chunk's loads and contribute zero (no branch, which would let
+      // the compiler sink their loads behind the first MFMAs)
+      float4 b[4];
+      float4 hv[2][4];
+      uint2 xv[2][4], gv[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        b[c] = *reinterpret_cast<const float4*>(wr + 16 * min(kc + c, nk - 1));
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const size_t off = (size_t)(t ? m1 : m0) * H + k_beg + 16 * min(kc + c, nk - 1);
+          if constexpr (NORM) hv[t][c] = *reinterpret_cast<const float4*>(hres + off);
+          else xv[t][c] = *reinterpret_cast<const uint2*>(x + off);
+        }
+      if constexpr (NORM) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          gv[c] = *reinterpret_cast<const uint2*>(gamma + k_beg + 16 * min(kc + c, nk - 1));
+        if (kc == 0) {
+          // r of the pass's rows: 16 threads per row, each summing every 16th partial sum
+          const int row = min(mb + (threadIdx.x >> 4), T - 1);
+          const int c = threadIdx.x & 15;
+          float t = 0.f;
+          for (int i0 = c; i0 < n_ss; i0 += 128) {
+            float v[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int i = i0 + 16 * j;
+              v[j] = ss_parts[(size_t)min(i, n_ss - 1) * T + row];
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) t += i0 + 16 * j < n_ss ? v[j] : 0.f;
+          }
+          t += __shfl_xor(t, 1);
+          t += __shfl_xor(t, 2);
+          t += __shfl_xor(t, 4);
+          t += __shfl_xor(t, 8);
+          if (c == 0) s_r[threadIdx.x >> 4] = rsqrtf(t / (float)H + eps);
+          __syncthreads();
+          rm[0] = s_r[r16];
+          rm[1] = s_r[16 + r16];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      float a[2][4][4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          if constexpr (NORM) {
+            const float r = rm[t];
+            a[t][c][0] = bf16_to_f32(f32_to_bf16(hv[t][c].x * r * bf16_lo(gv[c].x)));
+            a[t][c][1] = bf16_to_f32(f32_to_bf16(hv[t][c].y * r * bf16_hi(gv[c].x)));
+            a[t][c][2] = bf16_to_f32(f32_to_bf16(hv[t][c].z * r * bf16_lo(gv[c].y)));
+            a[t][c][3] = bf16_to_f32(f32_to_bf16(hv[t][c].w * r * bf16_hi(gv[c].y)));
+          } else {
+            a[t][c][0] = bf16_lo(xv[t][c].x);
+            a[t][c][1] = bf16_hi(xv[t][c].x);
+            a[t][c][2] = bf16_lo(xv[t][c].y);
+            a[t][c][3] = bf16_hi(xv[t][c].y);
+          }
+        }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float z = kc + c < nk ? 1.f : 0.f;
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][c][0] * z, b[c].x, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][c][1] * z, b[c].y, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][c][2] * z, b[c].z, acc[t], 0, 0, 0);
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t][c][3] * z, b[c].w, acc[t], 0, 0, 0);
+        }
+      if constexpr (NORM) {
+        if (xn_out && ntile == 0) {
+          // the normalised rows, for the expert GEMMs
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              if (kc + c < nk && mb + t * 16 + r16 < T) {
+                const int k = k_beg + 16 * (kc + c);
+                uint2 o;
+                o.x = pack_bf16x2(a[t][c][0], a[t][c][1]);
+                o.y = pack_bf16x2(a[t][c][2], a[t][c][3]);
+                *reinterpret_cast<uint2*>(xn_out + (size_t)(t ? m1 : m0) * H + k) = o;
+              }
+            }
+        }
+      }
     }
 #pragma unroll
-    for (int i = 0; i < 4; ++i) s_red[wave][i][lane] = acc[i];
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_red[wave][t][i][lane] = acc[t][i];
     __syncthreads();
     {
+      // 512 threads: tile t = tid / 256, element i of lane l's fragment
+      const int t = threadIdx.x >> 8;
       const int l = threadIdx.x & 63;
-      const int i = threadIdx.x >> 6;
-      const int row = mb + 4 * (l >> 4) + i;
-      const float v = (s_red[0][i][l] + s_red[1][i][l]) + (s_red[2][i][l] + s_red[3][i][l]);
+      const int i = (threadIdx.x >> 6) & 3;
+      const int row = mb + t * 16 + 4 * (l >> 4) + i;
+      float v = 0.f;
+#pragma unroll
+      for (int wv = 0; wv < kLogitWaves; ++wv) v += s_red[wv][t][i][l];
       if (row < T) parts[((size_t)q * T + row) * E + ntile * 16 + (l & 15)] = v;
     }
     __syncthreads();
@@ -394,18 +500,42 @@ extern "C" size_t sym_moe_route_workspace_bytes(int T, int E) {
   return 0;
 }
 
+static int check_router_logits(const char* what, int T, int H, int E) {
+  SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "%s: T=%d < 0", what, T);
+  SYM_REQUIRE(H > 0 && H % 512 == 0, SYM_ERR_UNSUPPORTED,
+              "%s: H=%d must be a positive multiple of 512", what, H);
+  SYM_REQUIRE(E > 0 && E % 16 == 0 && E / 16 <= 65535, SYM_ERR_UNSUPPORTED,
+              "%s: E=%d must be a positive multiple of 16", what, E);
+  return SYM_OK;
+}
+
 extern "C" int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E,
                                      float* parts, void* stream) {
-  SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "moe_router_logits: T=%d < 0", T);
-  if (T == 0) return SYM_OK;
+  int rc = check_router_logits("moe_router_logits", T, H, E);
+  if (rc || T == 0) return rc;
   SYM_REQUIRE(x && w && parts, SYM_ERR_INVALID, "moe_router_logits: null pointer argument");
-  SYM_REQUIRE(H > 0 && H % 256 == 0, SYM_ERR_UNSUPPORTED,
-              "moe_router_logits: H=%d must be a positive multiple of 256", H);
-  SYM_REQUIRE(E > 0 && E % 16 == 0 && E / 16 <= 65535, SYM_ERR_UNSUPPORTED,
-              "moe_router_logits: E=%d must be a positive multiple of 16", E);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(moe_router_logits_kernel, dim3(E / 16, kLogitParts), dim3(256), 0,
-                     (hipStream_t)stream, (const uint16_t*)x, w, T, H, E, parts);
+  hipLaunchKernelGGL((moe_router_logits_kernel<false>), dim3(E / 16, kLogitParts),
+                     dim3(kLogitWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)x,
+                     (const float*)nullptr, (const float*)nullptr, 0, (const uint16_t*)nullptr,
+                     0.f, w, T, H, E, parts, (uint16_t*)nullptr);
+  return sym_host::check_launch("moe_router_logits_kernel");
+}
+
+extern "C" int sym_moe_router_logits_norm(const float* h, const float* ss_parts, int n_ss,
+                                          const void* gamma, float eps, const float* w, int T,
+                                          int H, int E, float* parts, void* xn_out,
+                                          void* stream) {
+  int rc = check_router_logits("moe_router_logits_norm", T, H, E);
+  if (rc || T == 0) return rc;
+  SYM_REQUIRE(h && ss_parts && gamma && w && parts, SYM_ERR_INVALID,
+              "moe_router_logits_norm: null pointer argument");
+  SYM_REQUIRE(n_ss >= 1, SYM_ERR_INVALID, "moe_router_logits_norm: n_ss=%d", n_ss);
+  (void)hipGetLastError();
+  hipLaunchKernelGGL((moe_router_logits_kernel<true>), dim3(E / 16, kLogitParts),
+                     dim3(kLogitWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)nullptr, h,
+                     ss_parts, n_ss, (const uint16_t*)gamma, eps, w, T, H, E, parts,
+                     (uint16_t*)xn_out);
   return sym_host::check_launch("moe_router_logits_kernel");
 }
 

@@ -141,6 +141,62 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None
     return out
 
 
+def rmsnorm_linear(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor,
+                   bias: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16(RMSNorm(x) * gamma) [M, K] . w [N, K]^T (+ bias) in one kernel."""
+    _check(x, "x", torch.bfloat16)
+    if x.dim() != 2:
+        raise ValueError(f"x must be [M, K], got {tuple(x.shape)}")
+    M, K = x.shape
+    _check(gamma, "gamma", torch.bfloat16, x.device)
+    _check_shape(gamma, "gamma", (K,))
+    _check(w, "w", torch.bfloat16, x.device)
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError(f"w must be [N, {K}], got {tuple(w.shape)}")
+    N = w.shape[0]
+    if bias is not None:
+        _check(bias, "bias", torch.bfloat16, x.device)
+        _check_shape(bias, "bias", (N,))
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype {out_dtype} (bf16 or fp32)")
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype, device=x.device)
+    _check(out, "out", out_dtype, x.device)
+    _check_shape(out, "out", (M, N))
+    _timed("linear", lambda: _lib.call(
+        "sym_rmsnorm_linear_bf16", _ptr(x), _ptr(gamma), float(eps), _ptr(w), _ptr(bias), M, N,
+        K, _ptr(out), 1 if out_dtype == torch.float32 else 0, _stream()))
+    return out
+
+
+def linear_residual(x: torch.Tensor, w: torch.Tensor, residual: torch.Tensor,
+                    bias: Optional[torch.Tensor] = None):
+    """(x . w^T + bias + residual) in fp32 [M, N], and the per-16-column sums of squares of its
+    rows [N/16, M] (the statistics of the RMSNorm that follows)."""
+    _check(x, "x", torch.bfloat16)
+    if x.dim() != 2:
+        raise ValueError(f"x must be [M, K], got {tuple(x.shape)}")
+    M, K = x.shape
+    _check(w, "w", torch.bfloat16, x.device)
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError(f"w must be [N, {K}], got {tuple(w.shape)}")
+    N = w.shape[0]
+    _check(residual, "residual", torch.bfloat16, x.device)
+    _check_shape(residual, "residual", (M, N))
+    if bias is not None:
+        _check(bias, "bias", torch.bfloat16, x.device)
+        _check_shape(bias, "bias", (N,))
+    if N % 16:
+        raise ValueError(f"N={N} must be a multiple of 16")
+    out = torch.empty(M, N, dtype=torch.float32, device=x.device)
+    parts = torch.empty(N // 16, M, dtype=torch.float32, device=x.device)
+    _timed("linear", lambda: _lib.call(
+        "sym_linear_residual_bf16", _ptr(x), _ptr(w), _ptr(bias), _ptr(residual), M, N, K,
+        _ptr(out), _ptr(parts), _stream()))
+    return out, parts
+
+
 # -------------------------------------------------------------------------------------------
 @dataclass
 class PagedLayout:
@@ -368,6 +424,35 @@ def moe_router_logits(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     _timed("moe_router_logits", lambda: _lib.call(
         "sym_moe_router_logits", _ptr(x), _ptr(w), T, H, E, _ptr(parts), _stream()))
     return parts
+
+
+def moe_router_logits_norm(h: torch.Tensor, ss_parts: torch.Tensor, gamma: torch.Tensor,
+                           eps: float, w: torch.Tensor, xn_out: Optional[torch.Tensor] = None):
+    """Router logits (four partial sums [4, T, E]) of xn = bf16(RMSNorm(h) * gamma), with h the
+    fp32 residual stream [T, H] and ss_parts [n, T] the partial sums of squares of its rows;
+    also returns xn (bf16 [T, H]) for the expert GEMMs."""
+    _check(h, "h", torch.float32)
+    if h.dim() != 2:
+        raise ValueError(f"h must be [T, H], got {tuple(h.shape)}")
+    T, H = h.shape
+    _check(ss_parts, "ss_parts", torch.float32, h.device)
+    if ss_parts.dim() != 2 or ss_parts.shape[1] != T:
+        raise ValueError(f"ss_parts must be [n, {T}], got {tuple(ss_parts.shape)}")
+    _check(gamma, "gamma", torch.bfloat16, h.device)
+    _check_shape(gamma, "gamma", (H,))
+    _check(w, "w", torch.float32, h.device)
+    if w.dim() != 2 or w.shape[1] != H:
+        raise ValueError(f"w must be [E, {H}], got {tuple(w.shape)}")
+    E = w.shape[0]
+    parts = torch.empty(LOGIT_PARTS, T, E, dtype=torch.float32, device=h.device)
+    if xn_out is None:
+        xn_out = torch.empty(T, H, dtype=torch.bfloat16, device=h.device)
+    _check(xn_out, "xn_out", torch.bfloat16, h.device)
+    _check_shape(xn_out, "xn_out", (T, H))
+    _timed("moe_router_logits", lambda: _lib.call(
+        "sym_moe_router_logits_norm", _ptr(h), _ptr(ss_parts), ss_parts.shape[0], _ptr(gamma),
+        float(eps), _ptr(w), T, H, E, _ptr(parts), _ptr(xn_out), _stream()))
+    return parts, xn_out
 
 
 def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,

@@ -159,14 +159,49 @@ class HIPBailingMoEAttention(StatefulHIPModule):
             pos = pos.to(device=self.device, dtype=torch.int32)
         return pos.contiguous()
 
-    def forward(self, hidden_states: torch.Tensor, position_embeddings=None,
-                attention_mask=None, past_key_values=None, past_key_value=None,
-                cache_position=None, position_ids=None, **kwargs):
+    @staticmethod
+    def _cache_of(past_key_values, past_key_value) -> HIPPagedAttentionKVCache:
         cache = past_key_values if past_key_values is not None else past_key_value
         if not isinstance(cache, HIPPagedAttentionKVCache):
             raise NotImplementedError(
                 "HIPBailingMoEAttention needs the paged KV cache (model._tt_kv_cache) as "
                 "past_key_values")
+        return cache
+
+    def qkv_projection(self, x: torch.Tensor, norm_weight: Optional[torch.Tensor] = None,
+                       norm_eps: float = 1e-6) -> torch.Tensor:
+        """qkv [B, (Hq+2Hkv)*D] of x [B, H] (bf16); with ``norm_weight`` the preceding RMSNorm
+        (the decoder layer's input_layernorm) runs inside the projection kernel."""
+        d = self._dev
+        if norm_weight is None:
+            return hip_ops.linear(x, d["qkv_w"], d["qkv_b"])
+        return hip_ops.rmsnorm_linear(x, norm_weight, norm_eps, d["qkv_w"], d["qkv_b"])
+
+    def decode_from_qkv(self, qkv: torch.Tensor, cache: HIPPagedAttentionKVCache,
+                        cache_position=None, position_ids=None) -> torch.Tensor:
+        """QK-norm, RoPE, KV write and paged decode of one token per sequence: the attention
+        output [B, Hq*D] (bf16) before the dense projection."""
+        d = self._dev
+        B = qkv.shape[0]
+        pos = self._positions(cache, cache_position, position_ids, B)
+        o = hip_ops.attn_decode_step(
+            qkv, pos, cache.key_cache(self.layer_idx), cache.value_cache(self.layer_idx),
+            cache.page_table_device, self.scaling, num_heads=self.num_heads,
+            num_kv_heads=self.num_kv_heads, rotary_dim=self.rotary_dim, rope_cs=d["rope"],
+            q_norm_w=d["q_norm"], k_norm_w=d["k_norm"], eps=self.norm_eps,
+            max_context=cache.max_context, workspace=cache.decode_workspace(B, self.num_heads))
+        return o.view(B, self.num_heads * self.head_dim)
+
+    def dense_residual(self, o: torch.Tensor, residual: torch.Tensor):
+        """h = residual + o W_dense^T (+b) in fp32 [B, H], and the per-16-column sums of squares
+        of h's rows (the statistics of the post-attention RMSNorm)."""
+        d = self._dev
+        return hip_ops.linear_residual(o, d["dense_w"], residual, d["dense_b"])
+
+    def forward(self, hidden_states: torch.Tensor, position_embeddings=None,
+                attention_mask=None, past_key_values=None, past_key_value=None,
+                cache_position=None, position_ids=None, **kwargs):
+        cache = self._cache_of(past_key_values, past_key_value)
         B, S, H = hidden_states.shape
         if S != 1:
             raise NotImplementedError("prefill (seq_len > 1) is not implemented on the HIP path")
@@ -174,15 +209,7 @@ class HIPBailingMoEAttention(StatefulHIPModule):
         x = hidden_states.reshape(B, H)
         if x.dtype != torch.bfloat16:
             x = x.to(torch.bfloat16)
-        pos = self._positions(cache, cache_position, position_ids, B)
-        kp = cache.key_cache(self.layer_idx)
-        vp = cache.value_cache(self.layer_idx)
-        pt = cache.page_table_device
-        qkv = hip_ops.linear(x, d["qkv_w"], d["qkv_b"])
-        o = hip_ops.attn_decode_step(
-            qkv, pos, kp, vp, pt, self.scaling, num_heads=self.num_heads,
-            num_kv_heads=self.num_kv_heads, rotary_dim=self.rotary_dim, rope_cs=d["rope"],
-            q_norm_w=d["q_norm"], k_norm_w=d["k_norm"], eps=self.norm_eps,
-            max_context=cache.max_context, workspace=cache.decode_workspace(B, self.num_heads))
-        out = hip_ops.linear(o.view(B, self.num_heads * self.head_dim), d["dense_w"], d["dense_b"])
+        qkv = self.qkv_projection(x.contiguous())
+        o = self.decode_from_qkv(qkv, cache, cache_position, position_ids)
+        out = hip_ops.linear(o, d["dense_w"], d["dense_b"])
         return out.view(B, 1, H), None, cache

@@ -6,8 +6,10 @@ MoE block or the dense MLP by ``first_k_dense_replace`` (modeling_bailing_moe_v2
 Forward keeps the reference's residual structure
   h1  = x + attention(rmsnorm(x))
   out = h1 + mlp(rmsnorm(h1))
-with the residual adds fused into the kernels: the post-attention RMSNorm kernel also emits
-h1 = x + attn in fp32 (the residual stream inside the layer is never rounded), and the MoE
+with the norms and residual adds fused into the kernels (MoE layers): the QKV projection applies
+the input RMSNorm, the dense projection adds x and emits h1 = x + attn in fp32 with its rows'
+sums of squares (the residual stream inside the layer is never rounded), the router-logits
+kernel applies the post-attention RMSNorm, and the MoE
 combine kernel adds h1 into its output, which is rounded to bf16 once.
 """
 from __future__ import annotations
@@ -90,13 +92,33 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
         x = hidden_states
         if x.dtype != torch.bfloat16:
             x = x.to(torch.bfloat16)
+        if x.dim() == 2:
+            x = x.unsqueeze(1)
         x = x.contiguous()
-        xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
-        attn_out = self.attention(
-            xn, position_embeddings=position_embeddings, attention_mask=attention_mask,
-            past_key_values=cache, cache_position=cache_position, position_ids=position_ids)[0]
-        xn2, h1 = hip_ops.rmsnorm(attn_out.contiguous(), self._dev["ln2"], self.eps, residual=x)
-        out = self.mlp(xn2, residual=h1)
+        B, S, H = x.shape
+        if S != 1:
+            raise NotImplementedError("prefill (seq_len > 1) is not implemented on the HIP path")
+        attn = self.attention
+        if self.is_dense_layer:
+            xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
+            attn_out = attn(
+                xn, position_embeddings=position_embeddings, attention_mask=attention_mask,
+                past_key_values=cache, cache_position=cache_position,
+                position_ids=position_ids)[0]
+            xn2, h1 = hip_ops.rmsnorm(attn_out.contiguous(), self._dev["ln2"], self.eps,
+                                      residual=x)
+            out = self.mlp(xn2, residual=h1)
+        else:
+            # input RMSNorm inside the QKV projection; residual add and the post-attention
+            # RMSNorm's statistics inside the dense projection; that RMSNorm itself inside the
+            # router-logits kernel
+            x2 = x.view(B, H)
+            qkv = attn.qkv_projection(x2, self._dev["ln1"], self.eps)
+            o = attn.decode_from_qkv(qkv, attn._cache_of(cache, None), cache_position,
+                                     position_ids)
+            h1, ss = attn.dense_residual(o, x2)
+            out = self.mlp.forward_from_residual(h1, ss, self._dev["ln2"], self.eps)
+            out = out.view(B, S, H)
         outputs = (out,)
         if output_attentions:
             outputs += (None,)

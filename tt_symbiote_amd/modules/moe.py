@@ -159,6 +159,23 @@ class HIPBailingMoE(StatelessHIPModule):
         return out.view(shape)
 
 
+    def forward_from_residual(self, h: torch.Tensor, ss_parts: torch.Tensor,
+                              norm_weight: torch.Tensor, norm_eps: float) -> torch.Tensor:
+        """h + MoE(RMSNorm(h) * norm_weight) (bf16 [T, H]) for the fp32 residual stream h
+        [T, H]; ss_parts [n, T] are the partial sums of squares of h's rows. The RMSNorm runs
+        inside the router-logits kernel, which also hands the normalised rows to the experts."""
+        parts, xn = hip_ops.moe_router_logits_norm(h, ss_parts, norm_weight, norm_eps,
+                                                   self._dev["gate_w"])
+        route = hip_ops.moe_route_permute(
+            parts, self._dev["bias"], n_group=self.n_group, topk_group=self.topk_group,
+            top_k=self.top_k, routed_scale=self.routed_scaling_factor, renormalize=True,
+            with_shared=self.has_shared)
+        if self.keep_last_route:
+            self.last_route = route
+        _, y = hip_ops.moe_grouped_swiglu(xn, route, self._dev["gate_up"], self._dev["down"])
+        return hip_ops.moe_unpermute_combine(y, route, residual=h)
+
+
 class HIPBailingMoeV2MLP(StatelessHIPModule):
     """Dense SwiGLU MLP (layers < first_k_dense_replace), run as one segment of the grouped
     kernels. Replaces TTNNBailingMoeV2MLP (ttnn_moe.py; chosen at
