@@ -105,6 +105,28 @@ int sym_attn_decode_prologue(const void* qkv, const void* q_norm_w, const void* 
                              const int32_t* block_tables, int max_blocks_per_seq, int block_size,
                              int num_blocks, void* stream);
 
+/* Prefill prologue: the same per-token QK-norm + RoPE + paged KV write for T packed tokens of
+ * several sequences (prefill branch of TTNNBailingMoEAttention, ttnn_attention.py:2153-2230;
+ * paged_fill_on_device, 202-233): token t has position positions[t] and page-table row
+ * seq_ids[t]; q -> q_out [T, Hq, 128]; k, v -> the pools and k_out / v_out [T, Hkv, 128]
+ * (the operands of sym_prefill_attention).
+ */
+int sym_attn_prefill_prologue(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                              const float* rope_cs, int max_pos, const int32_t* positions,
+                              const int32_t* seq_ids, int T, int Hq, int Hkv, int head_dim,
+                              int rotary_dim, float eps, int use_qk_norm, void* q_out, void* k_out,
+                              void* v_out, void* k_pool, void* v_pool, const int32_t* block_tables,
+                              int max_blocks_per_seq, int block_size, int num_blocks, void* stream);
+
+/* Causal GQA attention over packed sequences (prefill SDPA, ttnn_attention.py:2153-2230):
+ *   q [T, Hq, 128], k, v [T, Hkv, 128] bf16, sequence s = rows cu_seqlens[s] .. cu_seqlens[s+1]-1
+ *   at positions 0 .. L-1; out [T, Hq, 128] bf16 = softmax(q k^T * scale, causal) v within each
+ *   sequence; max_seqlen >= every sequence length. fp32 accumulation, P rounded to bf16.
+ */
+int sym_prefill_attention(const void* q, const void* k, const void* v, const int32_t* cu_seqlens,
+                          int n_seqs, int max_seqlen, int Hq, int Hkv, int head_dim, float scale,
+                          void* out, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Paged KV write of one token per sequence: replaces TTNNPagedAttentionKVCache.
  * paged_update_on_device -> ttnn.experimental.paged_update_cache (ttnn_attention.py:235-269).
@@ -248,6 +270,28 @@ int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t* sorted_to
 int sym_moe_down(const void* h, int T, int H, int I, const int32_t* seg_expert,
                  const int32_t* seg_offset, const int32_t* seg_count, const int32_t* n_segments,
                  int max_segments, const void* w_down, float* y, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Tiled GEMMs for prefill-size batches (MFMA-bound; 128 x 128 output tiles).
+ * sym_gemm_bf16: out[M, N] = a[M, K] . w[N, K]^T (+ bias[N] bf16) (+ residual[M, N] fp32),
+ *   bf16 out, or fp32 when out_fp32 != 0. Replaces the QKV / dense projections at sequence length
+ *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 128 == 0, K % 64 == 0.
+ * sym_moe_gate_up_tiled / sym_moe_down_tiled: the grouped expert GEMMs of sym_moe_gate_up /
+ *   sym_moe_down (same arguments and results; TTNNExperts.forward, ttnn_moe.py:1250-1289) for
+ *   segments of many rows; rows = total rows of the segment list (T*top_k + T with the shared
+ *   expert). H % 128 == 0, I % 64 == 0.
+ */
+int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
+                  int N, int K, void* out, int out_fp32, void* stream);
+int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int rows,
+                          const int32_t* sorted_tokens, const int32_t* seg_expert,
+                          const int32_t* seg_offset, const int32_t* seg_count,
+                          const int32_t* n_segments, int max_segments, const void* w_gate_up,
+                          void* h, void* stream);
+int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows, const int32_t* seg_expert,
+                       const int32_t* seg_offset, const int32_t* seg_count,
+                       const int32_t* n_segments, int max_segments, const void* w_down, float* y,
+                       void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Unpermute + weighted combine (+ shared expert, + residual).

@@ -255,15 +255,18 @@ def _gemm_case(T, E, H, I, top_k, seed, device, with_shared=True, skew=False):
     return x, wgu, wd, res
 
 
+@pytest.mark.parametrize("kernel", ["stream", "tiled"])
 @pytest.mark.parametrize("T,E,H,I,top_k,skew", [
     (1, 64, 256, 128, 4, False),
     (32, 256, 2048, 512, 8, False),
     (7, 64, 512, 192, 4, False),
     (200, 64, 256, 128, 6, True),       # segments of > 64 rows (several passes)
+    (700, 64, 512, 256, 8, True),       # segments of several 128-row tiles
 ])
-def test_grouped_swiglu(device, T, E, H, I, top_k, skew):
+def test_grouped_swiglu(device, T, E, H, I, top_k, skew, kernel):
     x, wgu, wd, res = _gemm_case(T, E, H, I, top_k, seed=T + E, device=device, skew=skew)
-    h, y = hip_ops.moe_grouped_swiglu(x.to(device), res, wgu.to(device), wd.to(device))
+    h, y = hip_ops.moe_grouped_swiglu(x.to(device), res, wgu.to(device), wd.to(device),
+                                      kernel=kernel)
     torch.cuda.synchronize()
     st = res.sorted_tokens.cpu().long()
     ns = int(res.n_segments.item())
@@ -282,6 +285,31 @@ def test_grouped_swiglu(device, T, E, H, I, top_k, skew):
         _close(hk[rows], h_ref, atol=2e-3, rtol=8e-3)
         y_ref = hk[rows].float() @ wd[e].float().T
         torch.testing.assert_close(yk[rows], y_ref, rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("M,N,K,bias,res,out_dtype", [
+    (1000, 3072, 2048, False, False, torch.bfloat16),   # ragged last row tile
+    (256, 2048, 2048, True, True, torch.float32),
+    (1, 128, 64, False, False, torch.float32),
+    (130, 256, 576, True, False, torch.bfloat16),
+])
+def test_gemm_tiled(device, M, N, K, bias, res, out_dtype):
+    g = torch.Generator().manual_seed(M + N + K)
+    a = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    b = (torch.randn(N, generator=g) * 0.1).bfloat16() if bias else None
+    r = torch.randn(M, N, generator=g) if res else None
+    out = hip_ops.gemm(a.to(device), w.to(device), None if b is None else b.to(device),
+                       None if r is None else r.to(device), out_dtype=out_dtype)
+    ref = a.float() @ w.float().T
+    if b is not None:
+        ref = ref + b.float()
+    if r is not None:
+        ref = ref + r
+    if out_dtype == torch.float32:
+        torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=1e-4)
+    else:
+        _close(out, ref, atol=2e-3, rtol=8e-3)
 
 
 def test_combine(device):
@@ -497,6 +525,75 @@ def test_decode_step_matches_prologue_then_decode(device, B, Hq, Hkv, rd, use_no
     assert torch.equal(out, ref)
     assert torch.equal(k2, k1) and torch.equal(v2, v1)
     assert not bool(out[0].any())                    # no position: zero output
+
+
+@pytest.mark.parametrize("lens,Hq,Hkv", [
+    ([1, 5, 64, 127, 128, 129, 300], 16, 4),
+    ([200, 77], 8, 8),
+    ([513], 16, 2),
+])
+def test_prefill_attention(device, lens, Hq, Hkv):
+    g = torch.Generator().manual_seed(sum(lens) + Hq)
+    T = sum(lens)
+    q = torch.randn(T, Hq, 128, generator=g).bfloat16()
+    k = torch.randn(T, Hkv, 128, generator=g).bfloat16()
+    v = torch.randn(T, Hkv, 128, generator=g).bfloat16()
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)
+    out = hip_ops.prefill_attention(q.to(device), k.to(device), v.to(device), cu.to(device),
+                                    max(lens), 0.0884).cpu()
+    rep = Hq // Hkv
+    for s, L in enumerate(lens):
+        a, b = int(cu[s]), int(cu[s + 1])
+        qs = q[a:b].float().transpose(0, 1)                       # [Hq, L, D]
+        ks = k[a:b].float().transpose(0, 1).repeat_interleave(rep, 0)
+        vs = v[a:b].float().transpose(0, 1).repeat_interleave(rep, 0)
+        ref = F.scaled_dot_product_attention(qs[None], ks[None], vs[None], is_causal=True,
+                                             scale=0.0884)[0].transpose(0, 1)
+        _close(out[a:b], ref, atol=1e-2, rtol=1e-2)
+
+
+def test_prefill_prologue_matches_decode_prologue(device):
+    """The packed prefill prologue applies, per token, exactly the decode prologue's arithmetic
+    (same kernel); tokens of sequence s land in the pool slots of their positions."""
+    lens = [37, 70, 5]
+    T = sum(lens)
+    Hq, Hkv, D, bs = 16, 4, 128, 32
+    nblk = [(L + bs - 1) // bs for L in lens]
+    nb = sum(nblk) + 3
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(3)).int()
+    pt = torch.zeros(len(lens), max(nblk), dtype=torch.int32)
+    o = 0
+    for s, n in enumerate(nblk):
+        pt[s, :n] = perm[o:o + n]
+        o += n
+    pos = torch.cat([torch.arange(L) for L in lens]).int()
+    sid = torch.cat([torch.full((L,), s) for s, L in enumerate(lens)]).int()
+    g = torch.Generator().manual_seed(4)
+    qkv = torch.randn(T, (Hq + 2 * Hkv) * D, generator=g).bfloat16().to(device)
+    qn = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(device)
+    kn = (1 + 0.1 * torch.randn(D, generator=g)).bfloat16().to(device)
+    inv = 1.0 / (1e6 ** (torch.arange(0, 64, 2).float() / 64))
+    fr = torch.arange(512).float()[:, None] * inv[None]
+    table = torch.cat([fr.cos(), fr.sin()], 1).contiguous().to(device)
+    kw = dict(num_heads=Hq, num_kv_heads=Hkv, rotary_dim=64, rope_cs=table, q_norm_w=qn,
+              k_norm_w=kn, eps=1e-6)
+    kp = torch.zeros(nb, Hkv, bs, D, dtype=torch.bfloat16, device=device)
+    vp = torch.zeros_like(kp)
+    q, k, v = hip_ops.attn_prefill_prologue(qkv, pos.to(device), sid.to(device), kp, vp,
+                                            pt.to(device), **kw)
+    # reference: the decode prologue with one "sequence" per token (its own page-table row)
+    kp2 = torch.zeros_like(kp)
+    vp2 = torch.zeros_like(kp)
+    q2 = hip_ops.attn_decode_prologue(qkv, pos.to(device), kp2, vp2,
+                                      pt[sid.long()].contiguous().to(device), **kw)
+    assert torch.equal(q, q2)
+    assert torch.equal(kp, kp2) and torch.equal(vp, vp2)
+    kpc = kp.cpu()
+    for t in range(T):
+        s, p = int(sid[t]), int(pos[t])
+        phys = int(pt[s, p // bs])
+        assert torch.equal(kpc[phys, :, p % bs], k[t].cpu())
+    assert torch.equal(v.cpu(), qkv.cpu().view(T, Hq + 2 * Hkv, D)[:, Hq + Hkv:])
 
 
 def test_hbm_read_probe(device):

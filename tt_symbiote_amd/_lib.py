@@ -81,6 +81,24 @@ _SIGNATURES = {
         _c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]
     ),
     "sym_hbm_read_probe": (_c_int, [_vp, _c_size, _vp, _vp]),
+    "sym_attn_prefill_prologue": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+         _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp],
+    ),
+    "sym_prefill_attention": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp, _vp],
+    ),
+    "sym_gemm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]),
+    "sym_moe_gate_up_tiled": (
+        _c_int,
+        [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp],
+    ),
+    "sym_moe_down_tiled": (
+        _c_int,
+        [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp],
+    ),
 }
 
 EXPORTED_SYMBOLS = tuple(_SIGNATURES)

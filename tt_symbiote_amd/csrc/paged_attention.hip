@@ -116,20 +116,26 @@ __device__ __forceinline__ int slot_block(const int32_t* __restrict__ block_tabl
   return (p >= 0 && p < num_blocks) ? p : -1;
 }
 
+// Row b of qkv is one token: its position is positions[b], its page-table row is
+// bt_rows[b] (or b when bt_rows is null: one token per sequence, the decode case). q goes to
+// q_out; k and v go to the pools and, when k_out / v_out are given, also to [rows, Hkv, 128].
 __global__ __launch_bounds__(256) void attn_decode_prologue_kernel(
     const uint16_t* __restrict__ qkv, const uint16_t* __restrict__ qn_w,
     const uint16_t* __restrict__ kn_w, const float* __restrict__ rope_cs, int max_pos,
-    const int32_t* __restrict__ positions, int Hq, int Hkv, int rd, float eps, int use_qk_norm,
-    uint16_t* __restrict__ q_out, uint16_t* __restrict__ k_pool, uint16_t* __restrict__ v_pool,
-    const int32_t* __restrict__ block_tables, int mbps, int block_size, int num_blocks) {
+    const int32_t* __restrict__ positions, const int32_t* __restrict__ bt_rows, int Hq, int Hkv,
+    int rd, float eps, int use_qk_norm, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ k_out, uint16_t* __restrict__ v_out, uint16_t* __restrict__ k_pool,
+    uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_tables, int mbps,
+    int block_size, int num_blocks) {
   const int b = blockIdx.x;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int nwaves = blockDim.x >> 6;
   const int nh = Hq + 2 * Hkv;
   const int pos = positions[b];
+  const int btr = bt_rows ? bt_rows[b] : b;
   int off = 0;
-  const int phys = slot_block(block_tables, b, pos, mbps, block_size, num_blocks, &off);
+  const int phys = slot_block(block_tables, btr, pos, mbps, block_size, num_blocks, &off);
   const bool rope = pos >= 0 && pos < max_pos;
   const RopeLane rl = load_rope_lane(rope ? rope_cs + (size_t)pos * rd : nullptr, rd, lane);
 
@@ -149,12 +155,20 @@ __global__ __launch_bounds__(256) void attn_decode_prologue_kernel(
       uint16_t* dst = q_out + ((size_t)b * Hq + h) * kHeadDim;
       dst[lane] = f32_to_bf16(x0);
       dst[lane + 64] = f32_to_bf16(x1);
-    } else if (phys >= 0) {
+    } else {
       const int g = is_v ? h - Hq - Hkv : h - Hq;
-      uint16_t* pool = is_v ? v_pool : k_pool;
-      uint16_t* dst = pool + (((size_t)phys * Hkv + g) * block_size + off) * kHeadDim;
-      dst[lane] = f32_to_bf16(x0);
-      dst[lane + 64] = f32_to_bf16(x1);
+      uint16_t* kv_out = is_v ? v_out : k_out;
+      if (kv_out) {
+        uint16_t* dst = kv_out + ((size_t)b * Hkv + g) * kHeadDim;
+        dst[lane] = f32_to_bf16(x0);
+        dst[lane + 64] = f32_to_bf16(x1);
+      }
+      if (phys >= 0) {
+        uint16_t* pool = is_v ? v_pool : k_pool;
+        uint16_t* dst = pool + (((size_t)phys * Hkv + g) * block_size + off) * kHeadDim;
+        dst[lane] = f32_to_bf16(x0);
+        dst[lane + 64] = f32_to_bf16(x1);
+      }
     }
   }
 }
@@ -588,9 +602,42 @@ extern "C" int sym_attn_decode_prologue(const void* qkv, const void* q_norm_w,
   (void)hipGetLastError();
   hipLaunchKernelGGL(attn_decode_prologue_kernel, dim3(B), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)qkv, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w,
-                     rope_cs, max_pos, positions, Hq, Hkv, rotary_dim, eps, use_qk_norm,
-                     (uint16_t*)q_out, (uint16_t*)k_pool, (uint16_t*)v_pool, block_tables,
-                     max_blocks_per_seq, block_size, num_blocks);
+                     rope_cs, max_pos, positions, (const int32_t*)nullptr, Hq, Hkv, rotary_dim,
+                     eps, use_qk_norm, (uint16_t*)q_out, (uint16_t*)nullptr, (uint16_t*)nullptr,
+                     (uint16_t*)k_pool, (uint16_t*)v_pool, block_tables, max_blocks_per_seq,
+                     block_size, num_blocks);
+  return sym_host::check_launch("attn_decode_prologue_kernel");
+}
+
+extern "C" int sym_attn_prefill_prologue(const void* qkv, const void* q_norm_w,
+                                         const void* k_norm_w, const float* rope_cs, int max_pos,
+                                         const int32_t* positions, const int32_t* seq_ids, int T,
+                                         int Hq, int Hkv, int head_dim, int rotary_dim, float eps,
+                                         int use_qk_norm, void* q_out, void* k_out, void* v_out,
+                                         void* k_pool, void* v_pool, const int32_t* block_tables,
+                                         int max_blocks_per_seq, int block_size, int num_blocks,
+                                         void* stream) {
+  int rc = check_cache_args("attn_prefill_prologue", T, Hkv, head_dim, block_size,
+                            max_blocks_per_seq, num_blocks);
+  if (rc) return rc;
+  if (T == 0) return SYM_OK;
+  SYM_REQUIRE(qkv && positions && seq_ids && q_out && k_out && v_out && k_pool && v_pool &&
+                  block_tables,
+              SYM_ERR_INVALID, "attn_prefill_prologue: null pointer argument");
+  SYM_REQUIRE(Hq >= Hkv && Hq % Hkv == 0, SYM_ERR_INVALID,
+              "attn_prefill_prologue: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
+  SYM_REQUIRE(rotary_dim >= 0 && rotary_dim <= head_dim && rotary_dim % 2 == 0, SYM_ERR_INVALID,
+              "attn_prefill_prologue: rotary_dim=%d", rotary_dim);
+  SYM_REQUIRE(rotary_dim == 0 || (rope_cs && max_pos > 0), SYM_ERR_INVALID,
+              "attn_prefill_prologue: rope table missing");
+  SYM_REQUIRE(!use_qk_norm || (q_norm_w && k_norm_w), SYM_ERR_INVALID,
+              "attn_prefill_prologue: qk-norm weights missing");
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(attn_decode_prologue_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)qkv, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w,
+                     rope_cs, max_pos, positions, seq_ids, Hq, Hkv, rotary_dim, eps, use_qk_norm,
+                     (uint16_t*)q_out, (uint16_t*)k_out, (uint16_t*)v_out, (uint16_t*)k_pool,
+                     (uint16_t*)v_pool, block_tables, max_blocks_per_seq, block_size, num_blocks);
   return sym_host::check_launch("attn_decode_prologue_kernel");
 }
 

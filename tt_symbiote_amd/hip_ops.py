@@ -141,6 +141,37 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None
     return out
 
 
+def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
+         residual: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
+         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """a [M, K] . w [N, K]^T (+ bias) (+ residual fp32) with the tiled MFMA kernel (prefill-size
+    M)."""
+    _check(a, "a", torch.bfloat16)
+    if a.dim() != 2:
+        raise ValueError(f"a must be [M, K], got {tuple(a.shape)}")
+    M, K = a.shape
+    _check(w, "w", torch.bfloat16, a.device)
+    if w.dim() != 2 or w.shape[1] != K:
+        raise ValueError(f"w must be [N, {K}], got {tuple(w.shape)}")
+    N = w.shape[0]
+    if bias is not None:
+        _check(bias, "bias", torch.bfloat16, a.device)
+        _check_shape(bias, "bias", (N,))
+    if residual is not None:
+        _check(residual, "residual", torch.float32, a.device)
+        _check_shape(residual, "residual", (M, N))
+    if out_dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"out_dtype {out_dtype} (bf16 or fp32)")
+    if out is None:
+        out = torch.empty(M, N, dtype=out_dtype, device=a.device)
+    _check(out, "out", out_dtype, a.device)
+    _check_shape(out, "out", (M, N))
+    _timed("gemm", lambda: _lib.call(
+        "sym_gemm_bf16", _ptr(a), _ptr(w), _ptr(bias), _ptr(residual), M, N, K, _ptr(out),
+        1 if out_dtype == torch.float32 else 0, _stream()))
+    return out
+
+
 def rmsnorm_linear(x: torch.Tensor, gamma: torch.Tensor, eps: float, w: torch.Tensor,
                    bias: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -311,6 +342,73 @@ def attn_decode_step(qkv: torch.Tensor, positions: torch.Tensor, k_pool: torch.T
         1 if use_norm else 0, _ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
         lay.max_blocks_per_seq, lay.block_size, lay.num_blocks, int(max_context), float(scale),
         _ptr(workspace), workspace.numel(), _ptr(out), _stream()))
+    return out
+
+
+def attn_prefill_prologue(qkv: torch.Tensor, positions: torch.Tensor, seq_ids: torch.Tensor,
+                          k_pool: torch.Tensor, v_pool: torch.Tensor, block_tables: torch.Tensor,
+                          *, num_heads: int, num_kv_heads: int, rotary_dim: int,
+                          rope_cs: Optional[torch.Tensor], q_norm_w: Optional[torch.Tensor],
+                          k_norm_w: Optional[torch.Tensor], eps: float):
+    """QK-norm + partial RoPE of T packed tokens (token t at positions[t] of page-table row
+    seq_ids[t]); k/v written into the pools; returns q [T, Hq, D], k, v [T, Hkv, D]."""
+    _check(qkv, "qkv", torch.bfloat16)
+    T = qkv.shape[0]
+    _check_shape(qkv, "qkv", (T, (num_heads + 2 * num_kv_heads) * HEAD_DIM))
+    for t, n in ((positions, "positions"), (seq_ids, "seq_ids")):
+        _check(t, n, torch.int32, qkv.device)
+        _check_shape(t, n, (T,))
+    lay = _check_pools(k_pool, v_pool, block_tables, 1)
+    if lay.num_kv_heads != num_kv_heads:
+        raise ValueError(f"pool has {lay.num_kv_heads} kv heads, module {num_kv_heads}")
+    use_norm = q_norm_w is not None
+    if use_norm:
+        for t, n in ((q_norm_w, "q_norm_w"), (k_norm_w, "k_norm_w")):
+            _check(t, n, torch.bfloat16, qkv.device)
+            _check_shape(t, n, (HEAD_DIM,))
+    max_pos = 0
+    if rotary_dim:
+        _check(rope_cs, "rope_cs", torch.float32, qkv.device)
+        if rope_cs.dim() != 2 or rope_cs.shape[1] != rotary_dim:
+            raise ValueError(f"rope_cs must be [max_pos, {rotary_dim}], got {tuple(rope_cs.shape)}")
+        max_pos = rope_cs.shape[0]
+    bf = dict(dtype=torch.bfloat16, device=qkv.device)
+    q = torch.empty(T, num_heads, HEAD_DIM, **bf)
+    k = torch.empty(T, num_kv_heads, HEAD_DIM, **bf)
+    v = torch.empty(T, num_kv_heads, HEAD_DIM, **bf)
+    _lib.call("sym_attn_prefill_prologue", _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w),
+              _ptr(rope_cs), max_pos, _ptr(positions), _ptr(seq_ids), T, num_heads,
+              num_kv_heads, HEAD_DIM, rotary_dim, float(eps), 1 if use_norm else 0, _ptr(q),
+              _ptr(k), _ptr(v), _ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
+              lay.max_blocks_per_seq, lay.block_size, lay.num_blocks, _stream())
+    return q, k, v
+
+
+def prefill_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                      cu_seqlens: torch.Tensor, max_seqlen: int, scale: float,
+                      out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal GQA attention of packed sequences (rows cu_seqlens[s] .. cu_seqlens[s+1]-1):
+    q [T, Hq, D], k, v [T, Hkv, D] -> [T, Hq, D] (bf16)."""
+    _check(q, "q", torch.bfloat16)
+    if q.dim() != 3 or q.shape[2] != HEAD_DIM:
+        raise ValueError(f"q must be [T, Hq, {HEAD_DIM}], got {tuple(q.shape)}")
+    T, Hq, _ = q.shape
+    _check(k, "k", torch.bfloat16, q.device)
+    _check(v, "v", torch.bfloat16, q.device)
+    if k.dim() != 3 or k.shape[0] != T or k.shape[2] != HEAD_DIM or v.shape != k.shape:
+        raise ValueError(f"k/v must be [{T}, Hkv, {HEAD_DIM}], got {tuple(k.shape)}")
+    Hkv = k.shape[1]
+    _check(cu_seqlens, "cu_seqlens", torch.int32, q.device)
+    if cu_seqlens.dim() != 1 or cu_seqlens.numel() < 1:
+        raise ValueError("cu_seqlens must be [n_seqs + 1]")
+    if out is None:
+        out = torch.empty_like(q)
+    _check(out, "out", torch.bfloat16, q.device)
+    _check_shape(out, "out", tuple(q.shape))
+    _timed("prefill_attention", lambda: _lib.call(
+        "sym_prefill_attention", _ptr(q), _ptr(k), _ptr(v), _ptr(cu_seqlens),
+        cu_seqlens.numel() - 1, int(max_seqlen), Hq, Hkv, HEAD_DIM, float(scale), _ptr(out),
+        _stream()))
     return out
 
 
@@ -501,10 +599,15 @@ def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,
     return res
 
 
+TILED_MIN_TOKENS = 128  # from this many tokens the expert GEMMs use the tiled (MFMA-bound) kernels
+
+
 def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up: torch.Tensor,
                        w_down: torch.Tensor, h: Optional[torch.Tensor] = None,
-                       y: Optional[torch.Tensor] = None):
-    """h = silu(x Wg^T) * (x Wu^T), y = h Wd^T per segment; returns (h [rows, I], y [rows, H])."""
+                       y: Optional[torch.Tensor] = None, kernel: str = "auto"):
+    """h = silu(x Wg^T) * (x Wu^T), y = h Wd^T per segment; returns (h [rows, I], y [rows, H]).
+    ``kernel``: "stream" (weight-streaming kernels for decode-size segments), "tiled" (128 x 128
+    MFMA tiles for prefill-size segments) or "auto" (tiled from TILED_MIN_TOKENS tokens)."""
     _check(x, "x", torch.bfloat16)
     if x.dim() != 2:
         raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
@@ -534,6 +637,19 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up: torch.Ten
     _check(y, "y", torch.float32, dev)
     _check_shape(y, "y", (rows, H))
     stream = _stream()
+    if kernel not in ("auto", "stream", "tiled"):
+        raise ValueError(f"kernel {kernel!r}")
+    tiled = kernel == "tiled" or (kernel == "auto" and T >= TILED_MIN_TOKENS)
+    if tiled:
+        _timed("moe_gate_up", lambda: _lib.call(
+            "sym_moe_gate_up_tiled", _ptr(x), T, H, I, rows, _ptr(route.sorted_tokens),
+            _ptr(route.seg_expert), _ptr(route.seg_offset), _ptr(route.seg_count),
+            _ptr(route.n_segments), max_segments, _ptr(w_gate_up), _ptr(h), stream))
+        _timed("moe_down", lambda: _lib.call(
+            "sym_moe_down_tiled", _ptr(h), T, H, I, rows, _ptr(route.seg_expert),
+            _ptr(route.seg_offset), _ptr(route.seg_count), _ptr(route.n_segments), max_segments,
+            _ptr(w_down), _ptr(y), stream))
+        return h, y
     _timed("moe_gate_up", lambda: _lib.call(
         "sym_moe_gate_up", _ptr(x), T, H, I, _ptr(route.sorted_tokens), _ptr(route.seg_expert),
         _ptr(route.seg_offset), _ptr(route.seg_count), _ptr(route.n_segments), max_segments,
