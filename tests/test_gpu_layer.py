@@ -191,3 +191,59 @@ def test_decode_step_graph_replay_matches_eager(device, ling_layer):
         assert torch.equal(out, eager), f"replay {i} differs"
         _ = (x.float() * 2).sum()          # unrelated eager work between replays
         torch.cuda.synchronize()
+
+
+def test_decoder_layer_prefill_varlen(device, ling_layer):
+    """Packed prefill of three prompts (40, 130 and 7 tokens) through the layer: every token's
+    output against the oracle run on each prompt alone (causal attention over its own tokens,
+    written into its paged cache rows), and the prompts' K/V in the pool."""
+    oracle, layer = ling_layer
+    lens = [40, 130, 7]
+    T, bs = sum(lens), 32
+    nblk = [(L + bs - 1) // bs for L in lens]
+    nb = sum(nblk) + 4
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(7)).int()
+    pt = torch.zeros(len(lens), max(nblk), dtype=torch.int32)
+    o = 0
+    for s, n in enumerate(nblk):
+        pt[s, :n] = perm[o:o + n]
+        o += n
+    cu = torch.tensor([0, 40, 170, 177], dtype=torch.int32)
+    x = torch.randn(T, 2048, generator=torch.Generator().manual_seed(8)).bfloat16()
+    cfg = ts.PagedAttentionConfig(block_size=bs, max_num_blocks=nb, batch_size=1)
+    cache = ts.HIPPagedAttentionKVCache(1, 4, 128, cfg)
+    cache.to_device(device)
+    cache.set_vllm_page_table(pt)
+    out = layer.prefill_varlen(x.to(device), cu.to(device), max(lens), cache)
+    torch.cuda.synchronize()
+    out = out.float().cpu()
+    gpu_idx = layer.mlp.last_route.topk_idx.cpu().long()
+    gate = oracle.mlp.gate
+    kw = dict(n_group=gate.n_group, topk_group=gate.topk_group, top_k=gate.top_k)
+    worst = 0.0
+    for s, L in enumerate(lens):
+        a, b = int(cu[s]), int(cu[s + 1])
+        ref_cache = PagedKVCacheRef([torch.zeros(nb, 4, bs, 128)], [torch.zeros(nb, 4, bs, 128)],
+                                    pt[s:s + 1])
+        gate.route_override = gpu_idx[a:b]
+        try:
+            with torch.no_grad():
+                ref = oracle(x[a:b].float()[None], past_key_value=ref_cache,
+                             cache_position=torch.arange(L)[None])[0][0]
+        finally:
+            gate.route_override = None
+        logits = gate.last_routing[0]
+        own, _ = route_torch(logits, gate.expert_bias, routed_scale=1.0, **kw)
+        same = (gpu_idx[a:b].sort(-1).values == own.sort(-1).values).all(-1)
+        flips = (~same).nonzero().flatten().tolist()
+        if flips:
+            margins = selection_margins(logits, gate.expert_bias, **kw)
+            assert all(float(margins[t]) < FLIP_MARGIN for t in flips), (s, flips)
+        worst = max(worst, (out[a:b] - ref).abs().max().item())
+        kg = cache.key_cache(0).float().cpu()
+        for p in range(L):
+            phys = int(pt[s, p // bs])
+            k_ref = ref_cache.k_pools[0][phys, :, p % bs]
+            assert (kg[phys, :, p % bs] - k_ref).abs().max().item() <= 3e-2
+    print(f"prefill: max|gpu-oracle| = {worst:.3e}")
+    assert worst <= TOL

@@ -369,7 +369,10 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
   const int k_beg = q * quarter + wave * sub + kq * 4;
   const int nk = sub >> 4;                            // 16-wide k chunks of this wave
   const float* wr = w + (size_t)(ntile * 16 + r16) * H + k_beg;
-  for (int mb = 0; mb < T; mb += kLogitRows) {
+  // one pass of kLogitRows tokens per workgroup (grid z), so long prompts spread over many
+  // workgroups
+  {
+    const int mb = blockIdx.z * kLogitRows;
     float rm[2] = {1.f, 1.f};
     // rows past T repeat the last row; their results are dropped
     const int m0 = min(mb + r16, T - 1), m1 = min(mb + 16 + r16, T - 1);
@@ -485,7 +488,6 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
       for (int wv = 0; wv < kLogitWaves; ++wv) v += s_red[wv][t][i][l];
       if (row < T) parts[((size_t)q * T + row) * E + ntile * 16 + (l & 15)] = v;
     }
-    __syncthreads();
   }
 }
 
@@ -515,7 +517,10 @@ extern "C" int sym_moe_router_logits(const void* x, const float* w, int T, int H
   if (rc || T == 0) return rc;
   SYM_REQUIRE(x && w && parts, SYM_ERR_INVALID, "moe_router_logits: null pointer argument");
   (void)hipGetLastError();
-  hipLaunchKernelGGL((moe_router_logits_kernel<false>), dim3(E / 16, kLogitParts),
+  SYM_REQUIRE((T + kLogitRows - 1) / kLogitRows <= 65535, SYM_ERR_UNSUPPORTED,
+              "moe_router_logits: T=%d too large", T);
+  hipLaunchKernelGGL((moe_router_logits_kernel<false>),
+                     dim3(E / 16, kLogitParts, (T + kLogitRows - 1) / kLogitRows),
                      dim3(kLogitWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)x,
                      (const float*)nullptr, (const float*)nullptr, 0, (const uint16_t*)nullptr,
                      0.f, w, T, H, E, parts, (uint16_t*)nullptr);
@@ -532,7 +537,10 @@ extern "C" int sym_moe_router_logits_norm(const float* h, const float* ss_parts,
               "moe_router_logits_norm: null pointer argument");
   SYM_REQUIRE(n_ss >= 1, SYM_ERR_INVALID, "moe_router_logits_norm: n_ss=%d", n_ss);
   (void)hipGetLastError();
-  hipLaunchKernelGGL((moe_router_logits_kernel<true>), dim3(E / 16, kLogitParts),
+  SYM_REQUIRE((T + kLogitRows - 1) / kLogitRows <= 65535, SYM_ERR_UNSUPPORTED,
+              "moe_router_logits_norm: T=%d too large", T);
+  hipLaunchKernelGGL((moe_router_logits_kernel<true>),
+                     dim3(E / 16, kLogitParts, (T + kLogitRows - 1) / kLogitRows),
                      dim3(kLogitWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)nullptr, h,
                      ss_parts, n_ss, (const uint16_t*)gamma, eps, w, T, H, E, parts,
                      (uint16_t*)xn_out);

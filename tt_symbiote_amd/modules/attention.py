@@ -198,6 +198,25 @@ class HIPBailingMoEAttention(StatefulHIPModule):
         d = self._dev
         return hip_ops.linear_residual(o, d["dense_w"], residual, d["dense_b"])
 
+    def prefill_varlen(self, x: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
+                       positions: torch.Tensor, seq_ids: torch.Tensor,
+                       cache: HIPPagedAttentionKVCache) -> torch.Tensor:
+        """Prefill of packed sequences: x [T, H] (bf16, already normalised by the layer), token
+        t of sequence seq_ids[t] at positions[t] (0 .. L-1). Writes the sequences' K/V into the
+        paged cache (page-table row = sequence) and returns the attention output after the
+        dense projection, [T, H] bf16."""
+        d = self._dev
+        qkv = hip_ops.gemm(x, d["qkv_w"], d["qkv_b"])
+        q, k, v = hip_ops.attn_prefill_prologue(
+            qkv, positions, seq_ids, cache.key_cache(self.layer_idx),
+            cache.value_cache(self.layer_idx), cache.page_table_device,
+            num_heads=self.num_heads, num_kv_heads=self.num_kv_heads,
+            rotary_dim=self.rotary_dim, rope_cs=d["rope"], q_norm_w=d["q_norm"],
+            k_norm_w=d["k_norm"], eps=self.norm_eps)
+        o = hip_ops.prefill_attention(q, k, v, cu_seqlens, max_seqlen, self.scaling)
+        return hip_ops.gemm(o.view(-1, self.num_heads * self.head_dim), d["dense_w"],
+                            d["dense_b"])
+
     def forward(self, hidden_states: torch.Tensor, position_embeddings=None,
                 attention_mask=None, past_key_values=None, past_key_value=None,
                 cache_position=None, position_ids=None, **kwargs):

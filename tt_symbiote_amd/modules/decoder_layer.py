@@ -79,6 +79,27 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
         self._host = {}
         return super().move_weights_to_device_impl()
 
+    def prefill_varlen(self, x: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
+                       cache, positions: torch.Tensor = None,
+                       seq_ids: torch.Tensor = None) -> torch.Tensor:
+        """Prefill of packed sequences x [T, H] (bf16), sequence s = rows cu_seqlens[s] ..
+        cu_seqlens[s+1]-1 at positions 0 .. L-1 (page-table row s of the cache). Returns the
+        layer output [T, H] (bf16); the sequences' K/V are written into the paged cache."""
+        x = x.to(torch.bfloat16).contiguous()
+        T, H = x.shape
+        if positions is None or seq_ids is None:
+            cu = cu_seqlens.cpu().long()
+            lens = (cu[1:] - cu[:-1]).tolist()
+            positions = torch.cat([torch.arange(L) for L in lens]).to(torch.int32)
+            seq_ids = torch.cat([torch.full((L,), s) for s, L in enumerate(lens)]).to(torch.int32)
+        positions = positions.to(device=x.device, dtype=torch.int32).contiguous()
+        seq_ids = seq_ids.to(device=x.device, dtype=torch.int32).contiguous()
+        xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
+        attn_out = self.attention.prefill_varlen(xn, cu_seqlens, max_seqlen, positions, seq_ids,
+                                                 cache)
+        xn2, h1 = hip_ops.rmsnorm(attn_out, self._dev["ln2"], self.eps, residual=x)
+        return self.mlp(xn2, residual=h1)
+
     def reset_trace_state(self):
         # The only persistent mutation of a decode step is the KV-slot write of the child
         # attention, which handles its own state; this layer keeps none between calls.
@@ -92,13 +113,23 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
         x = hidden_states
         if x.dtype != torch.bfloat16:
             x = x.to(torch.bfloat16)
+        attn = self.attention
         if x.dim() == 2:
             x = x.unsqueeze(1)
         x = x.contiguous()
         B, S, H = x.shape
         if S != 1:
-            raise NotImplementedError("prefill (seq_len > 1) is not implemented on the HIP path")
-        attn = self.attention
+            # equal-length prompts, positions 0 .. S-1 of sequences 0 .. B-1
+            cu = torch.arange(0, B * S + 1, S, dtype=torch.int32, device=x.device)
+            out = self.prefill_varlen(x.view(B * S, H), cu, S, attn._cache_of(cache, None))
+            outputs = (out.view(B, S, H),)
+            if output_attentions:
+                outputs += (None,)
+            if use_cache:
+                outputs += (cache,)
+            if output_router_logits:
+                outputs += (None,)
+            return outputs
         if self.is_dense_layer:
             xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
             attn_out = attn(
