@@ -44,6 +44,9 @@ def parse_args():
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of replaying a captured HIP graph")
+    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+                    help="decode: the batch-32 decode step (the headline metric); prefill: 8 "
+                         "packed prompts of U[256, 2048] tokens through the same layer")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy kernel (torch.neg, bf16) over 512 MiB three "
                          "times: the reference point that scales the FETCH_SIZE / WRITE_SIZE "
@@ -130,10 +133,117 @@ def cpu_baseline(w_gpu, shape, ctx, x, steps: int) -> dict:
                       f"batch of {B} in fp32 on the host CPU; {med * 1e3:.1f} ms/step"}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_main(args) -> None:
+    """Prefill of 8 packed prompts (lengths U[256, 2048] from the seed, Zipf-skewed expert load)
+    through one layer: tokens/s, and the MFMA roofline of the dominant kernel (the tiled grouped
+    gate/up GEMM)."""
+    import torch
+
+    import tt_symbiote_amd as ts
+    from tt_symbiote_amd import hip_ops
+    from tt_symbiote_amd.workloads import (LING_MINI_2, build_decoder_layer, layer_weights,
+                                           prefill_batch, prefill_layer_config, zipf_expert_bias)
+
+    dev = torch.device("cuda:0")
+    shape = LING_MINI_2
+    wl = prefill_layer_config()
+    w = layer_weights(shape, seed=args.seed, device=dev)
+    w["expert_bias"] = w["expert_bias"] + zipf_expert_bias(
+        shape.num_experts, wl["zipf_s"], seed=args.seed + 3).to(dev)
+    pb = prefill_batch(wl["n_seqs"], wl["len_lo"], wl["len_hi"], shape.hidden_size,
+                       block_size=wl["block_size"], slack=wl["slack"], seed=args.seed + 1,
+                       device=dev)
+    layer = build_decoder_layer(w, shape)
+    ts.set_device(layer, dev)
+    layer.mlp.keep_last_route = True
+    cfg = ts.PagedAttentionConfig(block_size=wl["block_size"], max_num_blocks=pb.num_blocks,
+                                  batch_size=1)
+    cache = ts.HIPPagedAttentionKVCache(1, shape.num_kv_heads, shape.head_dim, cfg)
+    cache.to_device(dev)
+    cache.set_vllm_page_table(pb.page_table)
+    T = pb.tokens
+    cu = pb.cu_seqlens
+    lens_t = torch.tensor(pb.lens)
+    positions = torch.cat([torch.arange(L) for L in pb.lens]).to(torch.int32).to(dev)
+    seq_ids = torch.repeat_interleave(torch.arange(len(pb.lens)), lens_t).to(torch.int32).to(dev)
+
+    def step():
+        return layer.prefill_varlen(pb.x, cu, max(pb.lens), cache, positions, seq_ids)
+
+    _log(f"prefill: {T} tokens in {len(pb.lens)} prompts {pb.lens}")
+    for _ in range(max(1, args.warmup)):
+        step()
+    torch.cuda.synchronize()
+    counts = layer.mlp.last_route.expert_counts.float()
+    steps = max(1, args.steps)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(steps):
+        step()
+    t1.record()
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / steps
+    timer = hip_ops.KernelTimer(["moe_gate_up", "moe_down", "prefill_attention", "gemm"])
+    hip_ops.set_kernel_timer(timer)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    hip_ops.set_kernel_timer(None)
+    K, H, I = shape.top_k, shape.hidden_size, shape.moe_intermediate_size
+    rows = T * K + T * shape.num_shared_experts
+    gu_ms = timer.mean_ms("moe_gate_up")
+    gu_tflops = 2.0 * rows * 2 * I * H / (gu_ms * 1e-3) / 1e12
+    layer_flops = (2.0 * T * H * (shape.num_heads + 2 * shape.num_kv_heads) * shape.head_dim
+                   + 2.0 * T * H * shape.num_heads * shape.head_dim
+                   + sum(2.0 * L * L * shape.num_heads * shape.head_dim for L in pb.lens)
+                   + 2.0 * T * H * shape.num_experts
+                   + 2.0 * rows * 3 * I * H)
+    _log(f"prefill step {ms:.2f} ms | gate_up {gu_ms * 1e3:.0f} us ({gu_tflops:.0f} TFLOP/s) | "
+         f"down {timer.mean_ms('moe_down') * 1e3:.0f} us | attention "
+         f"{timer.mean_ms('prefill_attention') * 1e3:.0f} us | projections "
+         f"{timer.mean_ms('gemm') * 1e3:.0f} us each | expert load max/mean "
+         f"{counts.max().item() / counts.mean().item():.1f}")
+    print(json.dumps({
+        "metric": "prefill tokens/sec, 8 packed prompts U[256,2048], Ling-mini-2.0-shape layer, "
+                  "1 GPU",
+        "value": T / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights (seed 0), Zipf-skewed expert bias (s=1.1)",
+        "config": {"workload": "BailingMoeV2 decoder layer prefill, 8 packed prompts "
+                               "U[256,2048], block size 32", "tokens": T, "lens": pb.lens,
+                   "expert_load_max_over_mean": counts.max().item() / counts.mean().item()},
+        "roofline": {"bound": "mfma", "kernel": "gemm_tile_kernel<GateUp> (grouped gate/up)",
+                     "achieved": gu_tflops, "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": gu_tflops / MFMA_BF16_PEAK_TFLOPS, "traffic": None,
+                     "flops_per_launch": 2.0 * rows * 2 * I * H,
+                     "avg_launch_us": gu_ms * 1e3},
+        "layer_tflops": layer_flops / (ms * 1e-3) / 1e12,
+        "cpu_baseline": None,
+    }), flush=True)
+
+
 def main():
     args = parse_args()
     if args.copy_calibration:
         copy_calibration()
+        return
+    if args.workload == "prefill":
+        if args.gpus != 1:
+            print("bench.py measures one GPU; --gpus must be 1", file=sys.stderr)
+            sys.exit(2)
+        prefill_main(args)
         return
     if args.gpus != 1:
         print(f"bench.py measures the single-GPU decode layer; --gpus {args.gpus} is not "

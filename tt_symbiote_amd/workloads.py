@@ -154,6 +154,56 @@ def decode_layer_config(name: str) -> dict:
     raise KeyError(name)
 
 
+def prefill_layer_config() -> dict:
+    """The prefill workload: 8 prompts of lengths uniform in [256, 2048] packed varlen, block size
+    32, pool 1.25x shuffled; routing skewed so expert load follows a Zipf law (s = 1.1)."""
+    return dict(n_seqs=8, len_lo=256, len_hi=2048, block_size=32, slack=1.25, zipf_s=1.1)
+
+
+def zipf_expert_bias(num_experts: int, s: float, seed: int, strength: float = 0.1) -> torch.Tensor:
+    """Router expert-bias offsets that make expert selection Zipf-skewed: expert of popularity
+    rank r (a seeded permutation) gets strength * log(r^-s); the bias only moves selection, not
+    the routing weights."""
+    g = torch.Generator().manual_seed(seed)
+    rank = torch.empty(num_experts)
+    rank[torch.randperm(num_experts, generator=g)] = torch.arange(1, num_experts + 1).float()
+    return strength * torch.log(rank.pow(-s))
+
+
+@dataclass
+class PrefillBatch:
+    """Packed prompts: x [T, H] bf16, cu_seqlens [n+1] int32, page table [n, blocks] int32 over a
+    zero pool of num_blocks blocks."""
+
+    x: torch.Tensor
+    cu_seqlens: torch.Tensor
+    lens: list
+    page_table: torch.Tensor
+    num_blocks: int
+
+    @property
+    def tokens(self) -> int:
+        return int(sum(self.lens))
+
+
+def prefill_batch(n_seqs: int, len_lo: int, len_hi: int, hidden: int, *, block_size: int = 32,
+                  slack: float = 1.25, seed: int = 0, device="cpu") -> PrefillBatch:
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(len_lo, len_hi + 1, (n_seqs,), generator=g).tolist()
+    nblk = [(L + block_size - 1) // block_size for L in lens]
+    nb = int(math.ceil(slack * sum(nblk)))
+    perm = torch.randperm(nb, generator=g).to(torch.int32)
+    pt = torch.zeros(n_seqs, max(nblk), dtype=torch.int32)
+    o = 0
+    for i, n in enumerate(nblk):
+        pt[i, :n] = perm[o:o + n]
+        o += n
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0).tolist()), dtype=torch.int32)
+    x = torch.randn(sum(lens), hidden, generator=g).to(torch.bfloat16)
+    dev = torch.device(device)
+    return PrefillBatch(x.to(dev), cu.to(dev), lens, pt.to(dev), nb)
+
+
 def build_decoder_layer(w: Dict[str, torch.Tensor], shape: LayerShape = LING_MINI_2,
                         layer_idx: int = 0):
     """HIP decoder layer (attention + MoE) from a :func:`layer_weights` dict (not yet bound
