@@ -44,9 +44,10 @@ def parse_args():
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of replaying a captured HIP graph")
-    ap.add_argument("--workload", choices=["decode", "prefill"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "fp8"], default="decode",
                     help="decode: the batch-32 decode step (the headline metric); prefill: 8 "
-                         "packed prompts of U[256, 2048] tokens through the same layer")
+                         "packed prompts of U[256, 2048] tokens through the same layer; fp8: "
+                         "the batch-128 decode step with fp8 experts and an fp8 KV cache")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy kernel (torch.neg, bf16) over 512 MiB three "
                          "times: the reference point that scales the FETCH_SIZE / WRITE_SIZE "
@@ -234,31 +235,58 @@ def prefill_main(args) -> None:
     }), flush=True)
 
 
+def fp8_workload_config() -> dict:
+    """The quantised decode workload: batch 128, cached lengths uniform in [1024, 8192], block
+    size 32, pool 1.25x shuffled; fp8 e4m3fn experts with 128 x 128 block scales and an fp8 KV
+    cache with per-(block, head) scales."""
+    return dict(batch=128, ctx_lo=1024, ctx_hi=8192, block_size=32, slack=1.25)
+
+
+def fp8_algorithmic_bytes(shape, ctx, n_routed_active: int, B: int) -> dict:
+    """HBM bytes one fp8 decode step must move: e4m3fn expert weights + their fp32 block
+    scales, e4m3fn K/V + one fp32 scale per (block, head) read, bf16 attention weights."""
+    H, I, D, hkv = shape.hidden_size, shape.moe_intermediate_size, shape.head_dim, \
+        shape.num_kv_heads
+    n_exp = n_routed_active + shape.num_shared_experts
+    expert = 3 * I * H + 3 * I * H // (128 * 128) * 4
+    rows = B * shape.top_k + B * shape.num_shared_experts
+    gate_up = n_exp * (2 * I * H + 2 * I * H // (128 * 128) * 4) + B * H * 2 + rows * I * 2
+    tokens = int((ctx.context_lens + 1).sum())
+    blocks = int(((ctx.context_lens + 1 + ctx.block_size - 1) // ctx.block_size).sum())
+    kv_read = tokens * hkv * D * 2 + blocks * hkv * 2 * 4
+    kv_write = B * hkv * D * 2
+    layer = (shape.attention_weight_bytes() + kv_read + kv_write
+             + shape.num_experts * H * 4 + n_exp * expert
+             + 2 * H * 2 + 2 * D * 2 + 4 * B * H * 2)
+    return dict(gate_up=gate_up, layer=layer, kv_read=kv_read, experts=n_exp * expert)
+
+
 def main():
     args = parse_args()
     if args.copy_calibration:
         copy_calibration()
         return
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this build "
+              "(one GPU only).", file=sys.stderr)
+        sys.exit(2)
     if args.workload == "prefill":
-        if args.gpus != 1:
-            print("bench.py measures one GPU; --gpus must be 1", file=sys.stderr)
-            sys.exit(2)
         prefill_main(args)
         return
-    if args.gpus != 1:
-        print(f"bench.py measures the single-GPU decode layer; --gpus {args.gpus} is not "
-              "supported on this build (one GPU only).", file=sys.stderr)
-        sys.exit(2)
+    decode_main(args, fp8=args.workload == "fp8")
+
+
+def decode_main(args, fp8: bool) -> None:
     import torch
 
     import tt_symbiote_amd as ts
     from tt_symbiote_amd import hip_ops
     from tt_symbiote_amd.workloads import (LING_MINI_2, build_decoder_layer, decode_layer_config,
-                                           layer_weights, paged_context)
+                                           fp8_kv_pools, layer_weights, paged_context)
 
     dev = torch.device("cuda:0")
     shape = LING_MINI_2
-    wl = decode_layer_config("batch32")
+    wl = fp8_workload_config() if fp8 else decode_layer_config("batch32")
     B = wl["batch"]
     _log("building weights and paged context on the GPU ...")
     w = layer_weights(shape, seed=args.seed, device=dev)
@@ -268,15 +296,25 @@ def main():
     x = torch.randn(B, 1, shape.hidden_size, generator=torch.Generator().manual_seed(2)) \
         .to(torch.bfloat16).to(dev)
 
-    layer = build_decoder_layer(w, shape)
+    layer = build_decoder_layer(w, shape, weight_format="fp8_e4m3" if fp8 else "bf16")
     ts.set_device(layer, dev)
     layer.mlp.keep_last_route = True
     cfg = ts.PagedAttentionConfig(block_size=wl["block_size"], max_num_blocks=ctx.k_pool.shape[0],
                                   batch_size=1)
-    cache = ts.HIPPagedAttentionKVCache(1, shape.num_kv_heads, shape.head_dim, cfg)
+    cache = ts.HIPPagedAttentionKVCache(1, shape.num_kv_heads, shape.head_dim, cfg,
+                                        dtype=torch.float8_e4m3fn if fp8 else torch.bfloat16)
     cache.to_device(dev)
-    cache.key_cache(0).copy_(ctx.k_pool)
-    cache.value_cache(0).copy_(ctx.v_pool)
+    if fp8:
+        kq, ks = fp8_kv_pools(ctx.k_pool)
+        vq, vs = fp8_kv_pools(ctx.v_pool)
+        cache.key_cache(0).copy_(kq)
+        cache.value_cache(0).copy_(vq)
+        cache.key_scale(0).copy_(ks)
+        cache.value_scale(0).copy_(vs)
+        del kq, vq
+    else:
+        cache.key_cache(0).copy_(ctx.k_pool)
+        cache.value_cache(0).copy_(ctx.v_pool)
     cache.set_vllm_page_table(ctx.page_table)
     pos = ctx.positions.to(dev)
 
@@ -329,7 +367,7 @@ def main():
     attn_ms = timer.mean_ms("paged_gqa_decode")
 
     stream_gbs = hip_ops.hbm_read_bandwidth(device=dev)
-    nbytes = algorithmic_bytes(shape, ctx, n_active, B)
+    nbytes = (fp8_algorithmic_bytes if fp8 else algorithmic_bytes)(shape, ctx, n_active, B)
     achieved = nbytes["gate_up"] / (gate_up_ms * 1e-3) / 1e9
     layer_gbs = nbytes["layer"] / (ms_per_step * 1e-3) / 1e9
     _log(f"step {ms_per_step * 1e3:.1f} us | gate_up {gate_up_ms * 1e3:.1f} us "
@@ -337,8 +375,11 @@ def main():
          f"| active experts {n_active} | layer {layer_gbs:.0f} GB/s | stream read "
          f"{stream_gbs:.0f} GB/s")
 
+    kernel = "moe_gate_up_fp8_kernel" if fp8 else "moe_gate_up_kernel"
     result = {
-        "metric": METRIC,
+        "metric": (METRIC if not fp8 else
+                   "decode tokens/sec @bs128 fp8 (e4m3 block-scaled experts, e4m3 KV) "
+                   "Ling-mini-2.0-shape, 1 GPU; % HBM roofline/layer"),
         "value": B / (ms_per_step * 1e-3),
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -348,12 +389,17 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic: random-init bf16 weights (seed 0), K/V cache ~ N(0,1)",
+        "dtype": "fp8_e4m3 weights and KV, bf16 activations" if fp8 else "bf16",
+        "data": ("synthetic: random-init bf16 weights (seed 0) quantised to fp8 e4m3 with "
+                 "128x128 block scales; K/V ~ N(0,1) quantised per (block, head)" if fp8 else
+                 "synthetic: random-init bf16 weights (seed 0), K/V cache ~ N(0,1)"),
         "config": {
-            "workload": "BailingMoeV2 decoder layer decode step (Ling-mini-2.0 shape: hidden "
-                        "2048, 16q/4kv heads x128, 256 experts top-8 I=512 + 1 shared), batch 32, "
-                        "cached lengths U[128,4096], block size 32, pool 1.25x shuffled",
+            "workload": ("BailingMoeV2 decoder layer decode step (Ling-mini-2.0 shape), fp8 "
+                         "experts + fp8 KV cache, batch 128, cached lengths U[1024,8192], block "
+                         "size 32, pool 1.25x shuffled" if fp8 else
+                         "BailingMoeV2 decoder layer decode step (Ling-mini-2.0 shape: hidden "
+                         "2048, 16q/4kv heads x128, 256 experts top-8 I=512 + 1 shared), batch "
+                         "32, cached lengths U[128,4096], block size 32, pool 1.25x shuffled"),
             "global_batch": B,
             "context_tokens": int(ctx.context_lens.sum()),
             "active_experts": n_active,
@@ -361,12 +407,12 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "moe_gate_up_kernel (grouped gate/up GEMM + SwiGLU)",
+            "kernel": f"{kernel} (grouped gate/up GEMM + SwiGLU)",
             "achieved": achieved,
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": measured_traffic(),
+            "traffic": None if fp8 else measured_traffic(),
             "bytes_per_launch": nbytes["gate_up"],
             "avg_launch_us": gate_up_ms * 1e3,
         },
@@ -385,8 +431,46 @@ def main():
     }
     if not args.no_cpu_baseline:
         _log("cpu baseline ...")
-        result["cpu_baseline"] = cpu_baseline(w, shape, ctx, x, args.cpu_steps)
+        if fp8:
+            result["cpu_baseline"] = cpu_baseline_fp8(layer, w, shape, ctx, cache, x,
+                                                      args.cpu_steps)
+        else:
+            result["cpu_baseline"] = cpu_baseline(w, shape, ctx, x, args.cpu_steps)
     print(json.dumps(result), flush=True)
+
+
+def cpu_baseline_fp8(layer, w_gpu, shape, ctx, cache, x, steps: int) -> dict:
+    """The oracle layer on the dequantised weights and pools (the dequantise-then-bf16
+    reference), fp32 on the host CPU, on a bounded sample: the first 16 sequences."""
+    import types
+
+    import numpy as np
+    import torch
+
+    from oracle.fp8 import decode_e4m3, dequant_blocks
+
+    E = shape.num_experts
+    dq = {}
+    for name in ("gate_up", "down"):
+        bf = layer.mlp._dev[name]
+        dq[name] = torch.from_numpy(dequant_blocks(bf.q.view(torch.uint8).cpu().numpy(),
+                                                   bf.scale.cpu().numpy())).bfloat16()
+    w = dict(w_gpu, gate_up=dq["gate_up"][:E], down=dq["down"][:E],
+             shared_gate_up=dq["gate_up"][E], shared_down=dq["down"][E])
+    n = min(16, x.shape[0])
+
+    def pool(codes, scales):
+        vals = torch.from_numpy(decode_e4m3(codes.view(torch.uint8).cpu().numpy()))
+        return vals * scales.cpu()[..., None, None]
+
+    sub = types.SimpleNamespace(k_pool=pool(cache.key_cache(0), cache.key_scale(0)),
+                                v_pool=pool(cache.value_cache(0), cache.value_scale(0)),
+                                page_table=ctx.page_table[:n], positions=ctx.positions[:n])
+    r = cpu_baseline(w, shape, sub, x[:n], steps)
+    r["sample"] = (f"{steps} decode steps (median, after 2 warm-up) of the same layer on the "
+                   f"dequantised fp8 weights and cache, first {n} of the {x.shape[0]} sequences, "
+                   f"fp32 on the host CPU; " + r["sample"].split("; ")[-1])
+    return r
 
 
 if __name__ == "__main__":

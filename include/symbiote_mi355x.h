@@ -109,7 +109,8 @@ int sym_attn_decode_prologue(const void* qkv, const void* q_norm_w, const void* 
  * several sequences (prefill branch of TTNNBailingMoEAttention, ttnn_attention.py:2153-2230;
  * paged_fill_on_device, 202-233): token t has position positions[t] and page-table row
  * seq_ids[t]; q -> q_out [T, Hq, 128]; k, v -> the pools and k_out / v_out [T, Hkv, 128]
- * (the operands of sym_prefill_attention).
+ * (the operands of sym_prefill_attention). k_pool and v_pool may both be null: then only
+ * k_out / v_out are written (an fp8 cache is filled from them by sym_paged_kv_fill_fp8).
  */
 int sym_attn_prefill_prologue(const void* qkv, const void* q_norm_w, const void* k_norm_w,
                               const float* rope_cs, int max_pos, const int32_t* positions,
@@ -185,6 +186,49 @@ int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const void* k_no
                          int max_blocks_per_seq, int block_size, int num_blocks, int max_context,
                          float scale, void* workspace, size_t workspace_bytes, void* out,
                          void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * fp8 KV cache (the "fp8-KV variant with kv_scales" of the paged decode). Pools
+ * [num_blocks, Hkv, block_size, 128] hold OCP fp8 e4m3fn bytes; k_scale / v_scale
+ * [num_blocks, Hkv] fp32 hold one power-of-two scale per (block, kv head); a stored value is
+ * byte value * scale. Appending tokens to a block: s_new = max(s_old, pow2_ceil(amax / 448))
+ * (s_old = 0 for an empty block); when the scale grows, the block's earlier bytes c become
+ * e4m3(value(c) * s_old / s_new); new tokens are e4m3(x / s_new) with x their bf16 values
+ * (round to nearest even). block_size must divide 256. The reference's cache is bf16
+ * (TTNNPagedAttentionKVCache, ttnn_attention.py:116-137); the layout and page-table semantics
+ * are the same.
+ * sym_paged_kv_fill_fp8: appends tokens cu_seqlens[s] + i (i < L_s) of n_seqs sequences at
+ *   positions start_pos[s] + i (start_pos null: 0) through page-table row s
+ *   (paged_fill_on_device / paged_update_on_device, ttnn_attention.py:202-269). The 128 bf16
+ *   dims of token t, head g start at element t * tok_stride + g * head_stride of k / v
+ *   ([T, Hkv, 128]: Hkv*128, 128; [Hkv, S, 128]: 128, S*128). A sequence whose start is
+ *   negative is skipped. max_seqlen >= every L_s.
+ * sym_paged_gqa_decode_fp8 / sym_attn_decode_step_fp8: sym_paged_gqa_decode /
+ *   sym_attn_decode_step over the fp8 pools (paged_sdpa_decode, ttnn_attention.py:288-329);
+ *   same workspace. The step appends the new token's k and v by the rule above before the
+ *   attention reads the pool.
+ */
+int sym_paged_kv_fill_fp8(const void* k, const void* v, long long tok_stride,
+                          long long head_stride, const int32_t* cu_seqlens,
+                          const int32_t* start_pos, int n_seqs, int max_seqlen, int Hkv,
+                          int head_dim, void* k_pool, void* v_pool, float* k_scale,
+                          float* v_scale, const int32_t* block_tables, int max_blocks_per_seq,
+                          int block_size, int num_blocks, void* stream);
+int sym_paged_gqa_decode_fp8(const void* q, const void* k_pool, const void* v_pool,
+                             const float* k_scale, const float* v_scale,
+                             const int32_t* block_tables, const int32_t* positions, int B,
+                             int Hq, int Hkv, int head_dim, int block_size,
+                             int max_blocks_per_seq, int num_blocks, int max_context,
+                             float scale, void* workspace, size_t workspace_bytes, void* out,
+                             void* stream);
+int sym_attn_decode_step_fp8(const void* qkv, const void* q_norm_w, const void* k_norm_w,
+                             const float* rope_cs, int max_pos, const int32_t* positions, int B,
+                             int Hq, int Hkv, int head_dim, int rotary_dim, float eps,
+                             int use_qk_norm, void* k_pool, void* v_pool, float* k_scale,
+                             float* v_scale, const int32_t* block_tables,
+                             int max_blocks_per_seq, int block_size, int num_blocks,
+                             int max_context, float scale, void* workspace,
+                             size_t workspace_bytes, void* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Router logits in fp32 (fp32 MFMA): replaces the fp32 gate GEMV of TTNNMoE.forward
@@ -270,6 +314,20 @@ int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t* sorted_to
 int sym_moe_down(const void* h, int T, int H, int I, const int32_t* seg_expert,
                  const int32_t* seg_offset, const int32_t* seg_count, const int32_t* n_segments,
                  int max_segments, const void* w_down, float* y, void* stream);
+/* fp8 variants (the "_fp8 variant with w_scales" of the grouped SwiGLU; weight formats of
+ * TTNNExperts.from_torch, ttnn_moe.py:1055-1078, stored as OCP fp8 e4m3fn): w_gate_up
+ * [E+1, 2I, H] and w_down [E+1, H, I] are e4m3fn bytes with one fp32 scale per 128 x 128 block,
+ * s_gate_up [E+1, 2I/128, H/128] and s_down [E+1, H/128, I/128]; weight = byte value * scale.
+ * Dequantized inside the kernel (exact fp8 values on bf16 MFMA, block scale applied in fp32).
+ * Other arguments and results as sym_moe_gate_up / sym_moe_down. H % 512 == 0, I % 128 == 0. */
+int sym_moe_gate_up_fp8(const void* x, int T, int H, int I, const int32_t* sorted_tokens,
+                        const int32_t* seg_expert, const int32_t* seg_offset,
+                        const int32_t* seg_count, const int32_t* n_segments, int max_segments,
+                        const void* w_gate_up, const float* s_gate_up, void* h, void* stream);
+int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expert,
+                     const int32_t* seg_offset, const int32_t* seg_count,
+                     const int32_t* n_segments, int max_segments, const void* w_down,
+                     const float* s_down, float* y, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Tiled GEMMs for prefill-size batches (MFMA-bound; 128 x 128 output tiles).

@@ -110,3 +110,41 @@ def test_linear_and_router_reject_bad_shapes():
     assert _call("sym_moe_router_logits", FAKE, FAKE, 4, 2000, 256, FAKE, None)[0] == 2
     assert _call("sym_moe_router_logits", FAKE, FAKE, 4, 2048, 250, FAKE, None)[0] == 2
     assert _call("sym_moe_router_logits", FAKE, None, 4, 2048, 256, FAKE, None)[0] == 1
+
+
+def _prototype_arg_counts():
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    counts = {}
+    for m in re.finditer(r"\b(sym_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text):
+        args = m.group(2).strip()
+        counts[m.group(1)] = 0 if args in ("", "void") else args.count(",") + 1
+    return counts
+
+
+def test_binding_argument_counts_match_header():
+    counts = _prototype_arg_counts()
+    assert set(counts) == set(_declared())
+    for name, n in counts.items():
+        assert len(_lib._SIGNATURES[name][1]) == n, name
+
+
+def test_fp8_entry_points_reject_bad_shapes():
+    # fp8 GEMMs: H must be a multiple of 512, I of 128
+    args = lambda H, I: (FAKE, 4, H, I, FAKE, FAKE, FAKE, FAKE, FAKE, 65, FAKE, FAKE, FAKE, None)
+    assert _call("sym_moe_gate_up_fp8", *args(256, 512))[0] == 2
+    assert _call("sym_moe_gate_up_fp8", *args(2048, 64))[0] == 2
+    assert _call("sym_moe_gate_up_fp8", *args(2048, 512)[:1], 0, *args(2048, 512)[2:])[0] == 0
+    dargs = lambda H, I: (FAKE, 4, H, I, FAKE, FAKE, FAKE, FAKE, 65, FAKE, FAKE, FAKE, None)
+    assert _call("sym_moe_down_fp8", *dargs(2048, 192))[0] == 2
+    # fp8 cache: the block size must divide 256; strides must be multiples of 8
+    fill = lambda bs, ts, hs: (FAKE, FAKE, ts, hs, FAKE, None, 2, 10, 4, 128, FAKE, FAKE, FAKE,
+                               FAKE, FAKE, 8, bs, 64, None)
+    rc, msg = _call("sym_paged_kv_fill_fp8", *fill(48, 512, 128))
+    assert rc == 2 and "block_size" in msg
+    assert _call("sym_paged_kv_fill_fp8", *fill(32, 500, 128))[0] == 1
+    rc, msg = _call("sym_paged_gqa_decode_fp8", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 4,
+                    128, 48, 8, 64, 300, 1.0, FAKE, 1 << 20, FAKE, None)
+    assert rc == 2 and "block_size" in msg
+    rc, _ = _call("sym_paged_gqa_decode_fp8", FAKE, FAKE, FAKE, None, FAKE, FAKE, FAKE, 2, 16, 4,
+                  128, 32, 8, 64, 256, 1.0, FAKE, 1 << 20, FAKE, None)
+    assert rc == 1   # one scale array missing

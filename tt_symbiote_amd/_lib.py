@@ -19,6 +19,7 @@ from .build import LIB_PATH
 _c_int = ctypes.c_int
 _c_float = ctypes.c_float
 _c_size = ctypes.c_size_t
+_c_ll = ctypes.c_longlong
 _vp = ctypes.c_void_p
 
 # name -> (restype, argtypes)
@@ -50,6 +51,22 @@ _SIGNATURES = {
          _c_int, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _vp, _c_size, _vp,
          _vp],
     ),
+    "sym_paged_kv_fill_fp8": (
+        _c_int,
+        [_vp, _vp, _c_ll, _c_ll, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp,
+         _vp, _c_int, _c_int, _c_int, _vp],
+    ),
+    "sym_paged_gqa_decode_fp8": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_int, _c_int, _c_float, _vp, _c_size, _vp, _vp],
+    ),
+    "sym_attn_decode_step_fp8": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,
+         _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _vp,
+         _c_size, _vp, _vp],
+    ),
     "sym_linear_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]),
     "sym_rmsnorm_linear_bf16": (
         _c_int, [_vp, _vp, _c_float, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]
@@ -76,6 +93,13 @@ _SIGNATURES = {
     ),
     "sym_moe_down": (
         _c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp]
+    ),
+    "sym_moe_gate_up_fp8": (
+        _c_int,
+        [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp],
+    ),
+    "sym_moe_down_fp8": (
+        _c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]
     ),
     "sym_moe_unpermute_combine": (
         _c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]

@@ -36,6 +36,37 @@ __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
   return __builtin_bit_cast(uint16_t, (__bf16)f);
 }
 
+// ---- OCP fp8 e4m3fn (1 sign, 4 exponent bits with bias 7, 3 mantissa bits; no infinities,
+// 0x7f / 0xff are NaN; largest finite 448). gfx950's v_cvt_pk_f32_fp8 / v_cvt_pk_fp8_f32 use
+// this format. Every e4m3fn value is exact in bf16 and fp32.
+constexpr float kFp8Max = 448.0f;
+
+// 4 e4m3fn bytes -> 4 bf16 (two packed words), exact.
+__device__ __forceinline__ uint2 fp8x4_to_bf16x4(uint32_t w) {
+  const floatx2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+  const floatx2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  return make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(lo, bf16x2)),
+                    __builtin_bit_cast(uint32_t, __builtin_convertvector(hi, bf16x2)));
+}
+
+// 8 e4m3fn bytes (two words) -> the 8 bf16 of one MFMA operand, exact.
+__device__ __forceinline__ uint4 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+  const uint2 a = fp8x4_to_bf16x4(w0), b = fp8x4_to_bf16x4(w1);
+  return make_uint4(a.x, a.y, b.x, b.y);
+}
+
+// 4 floats -> 4 e4m3fn bytes, round to nearest even. Callers clamp to [-448, 448] first, so
+// the result is always finite.
+__device__ __forceinline__ uint32_t f32x4_to_fp8x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
+}
+
+__device__ __forceinline__ float clamp_fp8(float x) {
+  return fminf(fmaxf(x, -kFp8Max), kFp8Max);
+}
+
 // 8 bf16 packed in a uint4 -> 8 floats.
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x);

@@ -40,7 +40,11 @@ __device__ __forceinline__ void gate_up_pass(const uint16_t* __restrict__ x, int
                                              int r16, int kq, floatx4& accg, floatx4& accu) {
   accg = floatx4{0.f, 0.f, 0.f, 0.f};
   accu = floatx4{0.f, 0.f, 0.f, 0.f};
-  const uint16_t* xr = nullptr;
+  // the lane's token (rows past the pass read its last row, in bounds; their outputs are
+  // dropped), loaded before the weights: waiting for it does not wait for them
+  const int tok = tok_rows[min(r16, rows - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  const uint16_t* xr = x + kq * 16;
   for (int st = s_beg; st < s_end; st += U) {
     uint4 bg[U][2], bu[U][2], a[U][2];
 #pragma unroll
@@ -52,16 +56,7 @@ __device__ __forceinline__ void gate_up_pass(const uint16_t* __restrict__ x, int
       bu[s][1] = ld16(wu + k + 8);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if (st == s_beg) {
-      // rows past the pass read its last row (in bounds); their outputs are dropped
-      int tok = tok_rows[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) {
-        const int ti = tok_rows[min(i, rows - 1)];
-        tok = r16 == i ? ti : tok;
-      }
-      xr = x + (size_t)tok * H + kq * 16;
-    }
+    if (st == s_beg) xr += (size_t)tok * H;
 #pragma unroll
     for (int s = 0; s < U; ++s) {
       const int k = (st + s) << 6;
@@ -137,7 +132,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
   if (seg >= nseg) return;
   const int tile = blockIdx.x - seg * tiles_per_seg;
   const int col0 = tile * 16;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
@@ -253,6 +248,187 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
     const int rows = min(16, cnt - mb);
     floatx4 acc0[1], acc1[1];
     down_pass<1, U>(hbuf + (size_t)(row0 + mb) * I, I, rows, wd0, wd1, r16, kq, acc0, acc1);
+    down_store<1>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// fp8 e4m3fn expert weights with one fp32 scale per 128 x 128 block (w = q * scale): the same
+// grouped GEMMs, dequantized in-kernel. A K-step is 128 wide, one scale block: lane l streams
+// 32 contiguous weight bytes of row l % 16 (4 lanes cover the 128 bytes of a row in the block),
+// converts them exactly to bf16 and runs four v_mfma_f32_16x16x32_bf16 with the activations at
+// the same k (MFMA j takes the lane's elements 8j .. 8j+7). The 16 rows of a wave lie in one
+// 128-row block, so the block scale is wave-uniform: each step's MFMA sum is scaled once in
+// fp32 and added to the accumulator. Weights in HBM are half the bf16 bytes; the products are
+// exact fp8 x bf16 values, so the result equals the bf16 GEMM over dequantized weights up to
+// fp32 summation order (the weights are never rounded to bf16 after scaling).
+__device__ __forceinline__ floatx4 mfma_fp8_step(const uint4 (&a)[4], const uint4 (&w)[2],
+                                                 floatx4 acc, float scale) {
+  floatx4 t = {0.f, 0.f, 0.f, 0.f};
+  t = mfma16x16x32(a[0], fp8x8_to_bf16x8(w[0].x, w[0].y), t);
+  t = mfma16x16x32(a[1], fp8x8_to_bf16x8(w[0].z, w[0].w), t);
+  t = mfma16x16x32(a[2], fp8x8_to_bf16x8(w[1].x, w[1].y), t);
+  t = mfma16x16x32(a[3], fp8x8_to_bf16x8(w[1].z, w[1].w), t);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = fmaf(scale, t[i], acc[i]);
+  return acc;
+}
+
+__device__ __forceinline__ uint4 ld16b(const uint8_t* p) {
+  return *reinterpret_cast<const uint4*>(p);
+}
+
+// gate/up over 16 rows of a segment, K-steps [s_beg, s_end) of 128 (a multiple of U); sg / su
+// point at the scales of this wave's gate / up row block, one per K-step.
+template <int U>
+__device__ __forceinline__ void gate_up_pass_fp8(const uint16_t* __restrict__ x, int H,
+                                                 const int32_t* __restrict__ tok_rows, int rows,
+                                                 const uint8_t* __restrict__ wg,
+                                                 const uint8_t* __restrict__ wu,
+                                                 const float* __restrict__ sg,
+                                                 const float* __restrict__ su, int s_beg,
+                                                 int s_end, int r16, int kq, floatx4& accg,
+                                                 floatx4& accu) {
+  accg = floatx4{0.f, 0.f, 0.f, 0.f};
+  accu = floatx4{0.f, 0.f, 0.f, 0.f};
+  // the lane's token, loaded before the weights (see gate_up_pass)
+  const int tok = tok_rows[min(r16, rows - 1)];
+  __builtin_amdgcn_sched_barrier(0);
+  const uint16_t* xr = x + kq * 32;
+  for (int st = s_beg; st < s_end; st += U) {
+    uint4 bg[U][2], bu[U][2], a[U][4];
+    float cg[U], cu[U];
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      cg[s] = sg[st + s];
+      cu[s] = su[st + s];
+    }
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      const int k = (st + s) << 7;
+      bg[s][0] = ld16b(wg + k);
+      bg[s][1] = ld16b(wg + k + 16);
+      bu[s][0] = ld16b(wu + k);
+      bu[s][1] = ld16b(wu + k + 16);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if (st == s_beg) xr += (size_t)tok * H;
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      const int k = (st + s) << 7;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) a[s][j] = ld16(xr + k + 8 * j);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < U; ++s) {
+      accg = mfma_fp8_step(a[s], bg[s], accg, cg[s]);
+      accu = mfma_fp8_step(a[s], bu[s], accu, cu[s]);
+    }
+  }
+}
+
+// gate/up + SwiGLU with fp8 weights: w_gu [E+1, 2I, H] e4m3fn bytes, s_gu [E+1, 2I/128, H/128].
+// Workgroup = (segment, 16 columns of h) as in moe_gate_up_kernel.
+template <int U>
+__global__ __launch_bounds__(kGemmThreads) void moe_gate_up_fp8_kernel(
+    const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
+    const int32_t* __restrict__ seg_expert, const int32_t* __restrict__ seg_offset,
+    const int32_t* __restrict__ seg_count, const int32_t* __restrict__ n_segments,
+    const uint8_t* __restrict__ w_gu, const float* __restrict__ s_gu, uint16_t* __restrict__ h,
+    int tiles_per_seg) {
+  __shared__ float s_red[4][1][2][4][64];
+  const int seg = blockIdx.x / tiles_per_seg;
+  const int nseg = n_segments[0];
+  const int e = seg_expert[seg];
+  const int row0 = seg_offset[seg];
+  const int cnt = seg_count[seg];
+  asm volatile("" ::"s"(nseg), "s"(e), "s"(row0), "s"(cnt), "s"(x), "s"(sorted_tokens),
+               "s"(w_gu), "s"(s_gu), "s"(h));
+  if (seg >= nseg) return;
+  const int tile = blockIdx.x - seg * tiles_per_seg;
+  const int col0 = tile * 16;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int nsteps = H >> 7;
+  const int s_beg = (wave * nsteps) >> 2;
+  const int s_end = ((wave + 1) * nsteps) >> 2;
+  const uint8_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * 32;
+  const uint8_t* wu = wg + (size_t)I * H;
+  const int rb = (2 * I) >> 7;  // row blocks per expert
+  const float* sg = s_gu + ((size_t)e * rb + (col0 >> 7)) * nsteps;
+  const float* su = s_gu + ((size_t)e * rb + ((I + col0) >> 7)) * nsteps;
+
+  for (int mb = 0; mb < cnt; mb += 16) {
+    const int rows = min(16, cnt - mb);
+    floatx4 accg[1], accu[1];
+    gate_up_pass_fp8<U>(x, H, sorted_tokens + row0 + mb, rows, wg, wu, sg, su, s_beg, s_end, r16,
+                        kq, accg[0], accu[0]);
+    gate_up_epilogue<1>(s_red, accg, accu, wave, lane, rows, (size_t)row0 + mb, I, col0, h);
+  }
+}
+
+// down projection with fp8 weights: w_d [E+1, H, I] e4m3fn bytes, s_d [E+1, H/128, I/128]. One
+// wave per (segment, 32 output columns), all of I in batches of U K-steps of 128.
+template <int U>
+__global__ __launch_bounds__(kGemmThreads) void moe_down_fp8_kernel(
+    const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
+    const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
+    const int32_t* __restrict__ n_segments, const uint8_t* __restrict__ w_d,
+    const float* __restrict__ s_d, float* __restrict__ y, int tiles_per_seg) {
+  const int seg = blockIdx.x / tiles_per_seg;
+  const int nseg = n_segments[0];
+  const int e = seg_expert[seg];
+  const int row0 = seg_offset[seg];
+  const int cnt = seg_count[seg];
+  asm volatile("" ::"s"(nseg), "s"(e), "s"(row0), "s"(cnt), "s"(hbuf), "s"(w_d), "s"(s_d),
+               "s"(y), "s"(H), "s"(I));
+  if (seg >= nseg) return;
+  const int tile = blockIdx.x - seg * tiles_per_seg;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int col0 = (tile * 4 + wave) * 32;
+  if (col0 >= H) return;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int nsteps = I >> 7;
+  const uint8_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 32;
+  const uint8_t* wd1 = wd0 + (size_t)16 * I;
+  const float* sd = s_d + ((size_t)e * (H >> 7) + (col0 >> 7)) * nsteps;
+
+  for (int mb = 0; mb < cnt; mb += 16) {
+    const int rows = min(16, cnt - mb);
+    const uint16_t* hr = hbuf + (size_t)(row0 + mb + min(r16, rows - 1)) * I + kq * 32;
+    floatx4 acc0[1] = {{0.f, 0.f, 0.f, 0.f}}, acc1[1] = {{0.f, 0.f, 0.f, 0.f}};
+    for (int st = 0; st < nsteps; st += U) {
+      uint4 b0[U][2], b1[U][2], a[U][4];
+      float c[U];
+#pragma unroll
+      for (int s = 0; s < U; ++s) c[s] = sd[st + s];
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        const int k = (st + s) << 7;
+        b0[s][0] = ld16b(wd0 + k);
+        b0[s][1] = ld16b(wd0 + k + 16);
+        b1[s][0] = ld16b(wd1 + k);
+        b1[s][1] = ld16b(wd1 + k + 16);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        const int k = (st + s) << 7;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) a[s][j] = ld16(hr + k + 8 * j);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        acc0[0] = mfma_fp8_step(a[s], b0[s], acc0[0], c[s]);
+        acc1[0] = mfma_fp8_step(a[s], b1[s], acc1[0], c[s]);
+      }
+    }
     down_store<1>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
   }
 }
@@ -388,4 +564,66 @@ extern "C" int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm
   hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, y, inv_perm,
                      topk_w, top_k, H, shared_row0, residual, (uint16_t*)out);
   return sym_host::check_launch("moe_combine_kernel");
+}
+
+static int check_fp8_gemm_args(const char* what, int T, int H, int I, int max_segments) {
+  SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "%s: T=%d < 0", what, T);
+  SYM_REQUIRE(H > 0 && H % 512 == 0, SYM_ERR_UNSUPPORTED,
+              "%s: H=%d must be a positive multiple of 512", what, H);
+  SYM_REQUIRE(I > 0 && I % 128 == 0, SYM_ERR_UNSUPPORTED,
+              "%s: I=%d must be a positive multiple of 128", what, I);
+  SYM_REQUIRE(max_segments >= 1 && max_segments <= 4096, SYM_ERR_INVALID,
+              "%s: max_segments=%d out of range", what, max_segments);
+  return SYM_OK;
+}
+
+extern "C" int sym_moe_gate_up_fp8(const void* x, int T, int H, int I,
+                                   const int32_t* sorted_tokens, const int32_t* seg_expert,
+                                   const int32_t* seg_offset, const int32_t* seg_count,
+                                   const int32_t* n_segments, int max_segments,
+                                   const void* w_gate_up, const float* s_gate_up, void* h,
+                                   void* stream) {
+  int rc = check_fp8_gemm_args("moe_gate_up_fp8", T, H, I, max_segments);
+  if (rc) return rc;
+  if (T == 0) return SYM_OK;
+  SYM_REQUIRE(x && sorted_tokens && seg_expert && seg_offset && seg_count && n_segments &&
+                  w_gate_up && s_gate_up && h,
+              SYM_ERR_INVALID, "moe_gate_up_fp8: null pointer argument");
+  (void)hipGetLastError();
+  const int tiles = I / 16;
+  const int wave_steps = H / 512;  // K-steps of 128 per wave (4 waves split H)
+  const dim3 grid(max_segments * tiles), block(kGemmThreads);
+#define SYM_LAUNCH_GATE_UP_FP8(UU)                                                              \
+  hipLaunchKernelGGL((moe_gate_up_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,          \
+                     (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
+                     n_segments, (const uint8_t*)w_gate_up, s_gate_up, (uint16_t*)h, tiles)
+  if (wave_steps % 4 == 0) SYM_LAUNCH_GATE_UP_FP8(4);
+  else if (wave_steps % 2 == 0) SYM_LAUNCH_GATE_UP_FP8(2);
+  else SYM_LAUNCH_GATE_UP_FP8(1);
+#undef SYM_LAUNCH_GATE_UP_FP8
+  return sym_host::check_launch("moe_gate_up_fp8_kernel");
+}
+
+extern "C" int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expert,
+                                const int32_t* seg_offset, const int32_t* seg_count,
+                                const int32_t* n_segments, int max_segments, const void* w_down,
+                                const float* s_down, float* y, void* stream) {
+  int rc = check_fp8_gemm_args("moe_down_fp8", T, H, I, max_segments);
+  if (rc) return rc;
+  if (T == 0) return SYM_OK;
+  SYM_REQUIRE(h && seg_expert && seg_offset && seg_count && n_segments && w_down && s_down && y,
+              SYM_ERR_INVALID, "moe_down_fp8: null pointer argument");
+  (void)hipGetLastError();
+  const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
+  const int steps = I / 128;  // K-steps of 128 per wave (one wave covers all of I)
+  const dim3 grid(max_segments * tiles), block(kGemmThreads);
+#define SYM_LAUNCH_DOWN_FP8(UU)                                                                 \
+  hipLaunchKernelGGL((moe_down_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,             \
+                     (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
+                     (const uint8_t*)w_down, s_down, y, tiles)
+  if (steps % 4 == 0) SYM_LAUNCH_DOWN_FP8(4);
+  else if (steps % 2 == 0) SYM_LAUNCH_DOWN_FP8(2);
+  else SYM_LAUNCH_DOWN_FP8(1);
+#undef SYM_LAUNCH_DOWN_FP8
+  return sym_host::check_launch("moe_down_fp8_kernel");
 }

@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void attn_decode_prologue_kernel(
         dst[lane] = f32_to_bf16(x0);
         dst[lane + 64] = f32_to_bf16(x1);
       }
-      if (phys >= 0) {
+      if (phys >= 0 && k_pool) {
         uint16_t* pool = is_v ? v_pool : k_pool;
         uint16_t* dst = pool + (((size_t)phys * Hkv + g) * block_size + off) * kHeadDim;
         dst[lane] = f32_to_bf16(x0);
@@ -561,6 +561,424 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
       L > 0.f ? pack_bf16x2(ox / L, oy / L) : 0u;
 }
 
+// ---------------------------------------------------------------------------------------------
+// fp8 e4m3fn KV cache: pools [num_blocks, Hkv, block_size, 128] of e4m3fn bytes and one fp32
+// scale per (block, kv head), scales [num_blocks, Hkv]; a stored value is byte value * scale.
+// Scales are powers of two. Appending tokens to a block (prefill fill or the decode write):
+//   s_new = max(s_old, pow2_ceil(amax(new tokens) / 448))     (s_old = 0 for an empty block)
+//   if the block already holds tokens and s_new > s_old, each of their bytes c becomes
+//   e4m3(value(c) * (s_old / s_new)) (an exact exponent shift except where a value turns
+//   subnormal); the new tokens are e4m3(x / s_new) with x their bf16 values.
+// So no value is ever clamped, and the scale of a block is fixed once the block is full.
+
+__device__ __forceinline__ float pow2_ceil_f32(float y) {
+  if (y == 0.f) return 0.f;
+  if (y < 1.17549435e-38f) return 1.17549435e-38f;  // 2^-126
+  const uint32_t b = __float_as_uint(y);
+  if ((b & 0x7fffffu) == 0) return y;
+  return __uint_as_float((b & 0x7f800000u) + 0x00800000u);
+}
+
+// value(c) * r for the 4 bytes of w, re-encoded (r <= 1: no clamp needed).
+__device__ __forceinline__ uint32_t fp8x4_rescale(uint32_t w, float r) {
+  const floatx2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+  const floatx2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+  return f32x4_to_fp8x4(lo.x * r, lo.y * r, hi.x * r, hi.y * r);
+}
+
+// 8 e4m3fn bytes (lo word: dims 0-3, hi word: dims 4-7) -> 8 floats.
+__device__ __forceinline__ void fp8x8_to_f32(uint2 w, float* f) {
+  const floatx2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false);
+  const floatx2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
+  const floatx2 c = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, false);
+  const floatx2 d = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, true);
+  f[0] = a.x; f[1] = a.y; f[2] = b.x; f[3] = b.y;
+  f[4] = c.x; f[5] = c.y; f[6] = d.x; f[7] = d.y;
+}
+
+// Fill: grid (ceil(max_seqlen / block_size) + 1, Hkv, n_seqs), 256 threads; workgroup = the
+// j-th block touched by sequence s for kv head g. Sequence s holds tokens cu[s] + i, i < L, at
+// positions start[s] + i (start null: from 0), in page-table row s; the 128 bf16 dims of token
+// t, head g start at element t * tok_stride + g * head_stride of k / v. Each (block, head) is
+// owned by one workgroup.
+__global__ __launch_bounds__(256) void paged_kv_fill_fp8_kernel(
+    const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, long long tok_stride,
+    long long head_stride, const int32_t* __restrict__ cu_seqlens,
+    const int32_t* __restrict__ start_pos, int Hkv, uint8_t* __restrict__ k_pool,
+    uint8_t* __restrict__ v_pool, float* __restrict__ k_scale, float* __restrict__ v_scale,
+    const int32_t* __restrict__ block_tables, int mbps, int block_size, int num_blocks) {
+  __shared__ float s_amax[2][4];
+  const int j = blockIdx.x, g = blockIdx.y, sq = blockIdx.z;
+  const int c0 = cu_seqlens[sq];
+  const int L = cu_seqlens[sq + 1] - c0;
+  const int start = start_pos ? start_pos[sq] : 0;
+  if (L <= 0 || start < 0) return;
+  const int blk = start / block_size + j;
+  const int p0 = max(start, blk * block_size);
+  const int p1 = min(start + L, (blk + 1) * block_size);
+  if (p0 >= p1 || blk >= mbps) return;
+  const int phys = block_tables[(size_t)sq * mbps + blk];
+  if (phys < 0 || phys >= num_blocks) return;
+  const int n_old = p0 - blk * block_size;
+  const int n_new = p1 - p0;
+  const int tid = threadIdx.x;
+  const int nchunk = n_new * (kHeadDim / 8);  // 8 dims per chunk
+  const size_t tok0 = (size_t)c0 + (p0 - start);
+  auto src_off = [&](int c) -> size_t {
+    return (tok0 + c / 16) * (size_t)tok_stride + (size_t)g * head_stride + (c % 16) * 8;
+  };
+  float ak = 0.f, av = 0.f;
+  for (int c = tid; c < nchunk; c += 256) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(k + src_off(c)), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) ak = fmaxf(ak, fabsf(f[i]));
+    unpack8(*reinterpret_cast<const uint4*>(v + src_off(c)), f);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) av = fmaxf(av, fabsf(f[i]));
+  }
+  ak = wave_max(ak);
+  av = wave_max(av);
+  if ((tid & 63) == 0) {
+    s_amax[0][tid >> 6] = ak;
+    s_amax[1][tid >> 6] = av;
+  }
+  const size_t sidx = (size_t)phys * Hkv + g;
+  const float sk_old = n_old > 0 ? k_scale[sidx] : 0.f;
+  const float sv_old = n_old > 0 ? v_scale[sidx] : 0.f;
+  __syncthreads();
+  ak = fmaxf(fmaxf(s_amax[0][0], s_amax[0][1]), fmaxf(s_amax[0][2], s_amax[0][3]));
+  av = fmaxf(fmaxf(s_amax[1][0], s_amax[1][1]), fmaxf(s_amax[1][2], s_amax[1][3]));
+  const float sk = fmaxf(sk_old, pow2_ceil_f32(ak / kFp8Max));
+  const float sv = fmaxf(sv_old, pow2_ceil_f32(av / kFp8Max));
+  uint8_t* kb = k_pool + sidx * block_size * kHeadDim;
+  uint8_t* vb = v_pool + sidx * block_size * kHeadDim;
+  // requantise the block's earlier tokens where the scale grew
+  const int nw_old = n_old * (kHeadDim / 4);
+  if (sk > sk_old && n_old > 0) {
+    const float r = sk_old / sk;
+    uint32_t* w = reinterpret_cast<uint32_t*>(kb);
+    for (int i = tid; i < nw_old; i += 256) w[i] = fp8x4_rescale(w[i], r);
+  }
+  if (sv > sv_old && n_old > 0) {
+    const float r = sv_old / sv;
+    uint32_t* w = reinterpret_cast<uint32_t*>(vb);
+    for (int i = tid; i < nw_old; i += 256) w[i] = fp8x4_rescale(w[i], r);
+  }
+  // the new tokens
+  for (int c = tid; c < nchunk; c += 256) {
+    const size_t dst = (size_t)(n_old + c / 16) * kHeadDim + (c % 16) * 8;
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(k + src_off(c)), f);
+    uint2 q = make_uint2(0u, 0u);
+    if (sk > 0.f) {
+      q.x = f32x4_to_fp8x4(clamp_fp8(f[0] / sk), clamp_fp8(f[1] / sk), clamp_fp8(f[2] / sk),
+                           clamp_fp8(f[3] / sk));
+      q.y = f32x4_to_fp8x4(clamp_fp8(f[4] / sk), clamp_fp8(f[5] / sk), clamp_fp8(f[6] / sk),
+                           clamp_fp8(f[7] / sk));
+    }
+    *reinterpret_cast<uint2*>(kb + dst) = q;
+    unpack8(*reinterpret_cast<const uint4*>(v + src_off(c)), f);
+    q = make_uint2(0u, 0u);
+    if (sv > 0.f) {
+      q.x = f32x4_to_fp8x4(clamp_fp8(f[0] / sv), clamp_fp8(f[1] / sv), clamp_fp8(f[2] / sv),
+                           clamp_fp8(f[3] / sv));
+      q.y = f32x4_to_fp8x4(clamp_fp8(f[4] / sv), clamp_fp8(f[5] / sv), clamp_fp8(f[6] / sv),
+                           clamp_fp8(f[7] / sv));
+    }
+    *reinterpret_cast<uint2*>(vb + dst) = q;
+  }
+  if (tid == 0) {
+    k_scale[sidx] = sk;
+    v_scale[sidx] = sv;
+  }
+}
+
+// The decode write of one head of the new token by one wave: x0 / x1 are dims lane / lane+64
+// (bf16 values as floats); appended to (block phys, head g) at slot off by the rule above.
+__device__ __forceinline__ void fp8_append_token(uint8_t* __restrict__ pool,
+                                                 float* __restrict__ scales, int phys, int g,
+                                                 int Hkv, int block_size, int off, float x0,
+                                                 float x1, int lane) {
+  const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
+  const size_t sidx = (size_t)phys * Hkv + g;
+  const float s_old = off > 0 ? scales[sidx] : 0.f;
+  const float s_new = fmaxf(s_old, pow2_ceil_f32(amax / kFp8Max));
+  uint8_t* blk = pool + sidx * block_size * kHeadDim;
+  if (off > 0 && s_new > s_old) {
+    const float r = s_old / s_new;
+    uint32_t* w = reinterpret_cast<uint32_t*>(blk);
+    for (int i = lane; i < off * (kHeadDim / 4); i += 64) w[i] = fp8x4_rescale(w[i], r);
+  }
+  uint32_t q = 0;
+  if (s_new > 0.f)
+    q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp_fp8(x0 / s_new), clamp_fp8(x1 / s_new),
+                                                  0, false);
+  blk[(size_t)off * kHeadDim + lane] = (uint8_t)(q & 0xffu);
+  blk[(size_t)off * kHeadDim + lane + 64] = (uint8_t)((q >> 8) & 0xffu);
+  if (lane == 0) scales[sidx] = s_new;
+}
+
+// Split-K decode over the fp8 cache, same workgroup shape and outputs as paged_decode_kernel.
+//   K in the MFMA B layout: lane l holds bytes [32*(l/16), +32) of token l%16 of a 16-token tile
+//   (two 16-byte loads); MFMA j takes its bytes 8j .. 8j+7, converted exactly to bf16, against
+//   the query dims 32*(l/16) + 8j .. +7 from LDS. V for P.V: 8 bytes (dims r16*8 .. +7) of one
+//   token per step. A token's K scale multiplies its score and its V scale its probability in
+//   P.V (the softmax sum uses the unscaled probability), so the dequantised values are never
+//   formed. In the fused step the workgroup of the sequence's last split first appends the new
+//   token's k and v to the pool (with any requantisation of its block), then reads the split
+//   from the pool like every other workgroup; a block never straddles two splits
+//   (256 % block_size == 0), so no other workgroup reads the block being rewritten.
+template <int G, bool FUSED>
+__global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
+    const uint16_t* __restrict__ q, FusedQKV fq, uint8_t* __restrict__ k_pool,
+    uint8_t* __restrict__ v_pool, float* __restrict__ k_scale, float* __restrict__ v_scale,
+    const int32_t* __restrict__ block_tables, const int32_t* __restrict__ positions, int Hkv,
+    int block_size, int mbps, int num_blocks, int max_context, float scale_log2,
+    float* __restrict__ ws_o, float* __restrict__ ws_ml, int max_splits,
+    uint16_t* __restrict__ out) {
+  constexpr int D = kHeadDim;
+  constexpr int TPW = kTPW;
+  constexpr int SPLIT = kSplit;
+  constexpr int KT = TPW / 16;
+  constexpr int VS = TPW / 4;
+  __shared__ __align__(16) uint16_t s_q[G][D];
+  __shared__ float s_p[G][SPLIT];
+  __shared__ float s_red[4][G][D];
+  __shared__ float s_stat[G][4];
+  __shared__ float s_fin[2][G];
+  __shared__ unsigned s_row[SPLIT];
+
+  const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  const int Hq = Hkv * G;
+  const int tid = threadIdx.x;
+  const int pos = positions[b];
+  const int ctx = min(pos + 1, max_context);
+  if (ctx <= 0) {
+    if (split == 0)
+      for (int i = tid; i < G * D; i += kAttnThreads)
+        out[((size_t)b * Hq + g * G) * D + i] = 0;
+    return;
+  }
+  const int t0 = split * SPLIT;
+  if (t0 >= ctx) return;
+  const int t1 = min(ctx, t0 + SPLIT);
+  const int nsplit = (ctx + SPLIT - 1) / SPLIT;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int r16 = lane & 15;
+  const int kg = lane >> 4;
+
+  constexpr int JPW = FUSED ? (G + 2 + 3) / 4 : 1;
+  const bool writer = FUSED && split == (ctx - 1) / SPLIT;
+  const int n_jobs = writer ? G + 2 : G;
+  float hx[JPW][2];
+  float wq[2] = {1.f, 1.f}, wk[2] = {1.f, 1.f};
+  RopeLane rl{1.f, 0.f, 1.f, 0.f};
+  const bool rope = FUSED && pos < fq.max_pos;
+  if constexpr (FUSED) {
+    const int nh = Hq + 2 * Hkv;
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) {
+      const int job = min(wave + 4 * jj, n_jobs - 1);
+      const int h = job < G ? g * G + job : (job == G ? Hq + g : Hq + Hkv + g);
+      const uint16_t* src = fq.qkv + ((size_t)b * nh + h) * D;
+      hx[jj][0] = bf16_to_f32(src[lane]);
+      hx[jj][1] = bf16_to_f32(src[lane + 64]);
+    }
+    const uint16_t* qw = fq.qn_w ? fq.qn_w : kOnesBf16;
+    const uint16_t* kw = fq.qn_w ? fq.kn_w : kOnesBf16;
+    wq[0] = bf16_to_f32(qw[lane]);
+    wq[1] = bf16_to_f32(qw[lane + 64]);
+    wk[0] = bf16_to_f32(kw[lane]);
+    wk[1] = bf16_to_f32(kw[lane + 64]);
+    rl = load_rope_lane_nobranch(rope ? fq.rope_cs + (size_t)pos * fq.rd : kZeroRope, fq.rd,
+                                 lane);
+  } else {
+    if (tid < G * 16) {
+      const int h = tid >> 4, c = tid & 15;
+      *reinterpret_cast<uint4*>(&s_q[h][c * 8]) = *reinterpret_cast<const uint4*>(
+          q + ((size_t)b * Hq + g * G + h) * D + c * 8);
+    }
+  }
+  // token t0 + tid: its pool row (always in bounds), validity and scale index
+  bool my_ok;
+  size_t my_sidx;
+  {
+    const int t = t0 + tid;
+    const int tc = min(t, t1 - 1);
+    const int blk = tc / block_size;
+    int pb = blk < mbps ? block_tables[(size_t)b * mbps + blk] : -1;
+    my_ok = t < t1 && pb >= 0 && pb < num_blocks;
+    if (pb < 0 || pb >= num_blocks) pb = 0;
+    s_row[tid] = (unsigned)(((size_t)pb * Hkv + g) * block_size + (tc - blk * block_size));
+    my_sidx = (size_t)pb * Hkv + g;
+  }
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) asm volatile("" ::"v"(hx[jj][0]), "v"(hx[jj][1]));
+    asm volatile("" ::"v"(wq[0]), "v"(wq[1]), "v"(wk[0]), "v"(wk[1]), "v"(rl.c0), "v"(rl.s0),
+                 "v"(rl.c1), "v"(rl.s1));
+  }
+  __syncthreads();
+
+  const int wt0 = wave * TPW;
+  uint4 kb[KT][2];
+  uint2 vreg[VS];
+  float ks_own = 0.f, vs_own = 0.f;
+  auto issue_loads = [&]() {
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+      const uint8_t* kr = k_pool + (size_t)s_row[wt0 + tt * 16 + r16] * D + 32 * kg;
+      kb[tt][0] = *reinterpret_cast<const uint4*>(kr);
+      kb[tt][1] = *reinterpret_cast<const uint4*>(kr + 16);
+    }
+#pragma unroll
+    for (int it = 0; it < VS; ++it)
+      vreg[it] = *reinterpret_cast<const uint2*>(v_pool + (size_t)s_row[wt0 + it * 4 + kg] * D +
+                                                 r16 * 8);
+    ks_own = k_scale[my_sidx];
+    vs_own = v_scale[my_sidx];
+  };
+  if (!writer) issue_loads();
+  if constexpr (FUSED) {
+#pragma unroll
+    for (int jj = 0; jj < JPW; ++jj) {
+      const int job = wave + 4 * jj;
+      if (job < n_jobs) {
+        float x0 = hx[jj][0], x1 = hx[jj][1];
+        if (job <= G)
+          qk_norm_rope(x0, x1, fq.qn_w != nullptr, job < G ? wq[0] : wk[0],
+                       job < G ? wq[1] : wk[1], fq.eps, rope, rl, fq.rd, lane);
+        const uint16_t y0 = f32_to_bf16(x0), y1 = f32_to_bf16(x1);
+        if (job < G) {
+          s_q[job][lane] = y0;
+          s_q[job][lane + 64] = y1;
+        } else {
+          int off = 0;
+          const int phys = slot_block(block_tables, b, pos, mbps, block_size, num_blocks, &off);
+          if (phys >= 0)
+            fp8_append_token(job == G ? k_pool : v_pool, job == G ? k_scale : v_scale, phys, g,
+                             Hkv, block_size, off, bf16_to_f32(y0), bf16_to_f32(y1), lane);
+        }
+      }
+    }
+    // the appended token (and any requantised rows) are visible to the whole workgroup after
+    // the barrier
+    __syncthreads();
+    if (writer) issue_loads();
+  }
+  uint4 qa[4];
+  {
+    const uint16_t* qr = &s_q[min(r16, G - 1)][32 * kg];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint4 v = *reinterpret_cast<const uint4*>(qr + 8 * j);
+      qa[j] = r16 < G ? v : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  // ---- raw scores (before the K scale) on MFMA ----
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt) {
+    floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
+    sacc = mfma16x16x32(qa[0], fp8x8_to_bf16x8(kb[tt][0].x, kb[tt][0].y), sacc);
+    sacc = mfma16x16x32(qa[1], fp8x8_to_bf16x8(kb[tt][0].z, kb[tt][0].w), sacc);
+    sacc = mfma16x16x32(qa[2], fp8x8_to_bf16x8(kb[tt][1].x, kb[tt][1].y), sacc);
+    sacc = mfma16x16x32(qa[3], fp8x8_to_bf16x8(kb[tt][1].z, kb[tt][1].w), sacc);
+    const int tl = wt0 + tt * 16 + r16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kg + i;
+      if (h < G) s_p[h][tl] = sacc[i];
+    }
+  }
+  __syncthreads();
+
+  // ---- softmax statistics (log2 domain); thread tid owns token t0 + tid ----
+  const float kscale = ks_own * scale_log2;
+  float mx[G];
+  float sc[G];
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    sc[h] = my_ok ? s_p[h][tid] * kscale : -INFINITY;
+    const float m = wave_max(sc[h]);
+    if (lane == 0) s_stat[h][wave] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+    mx[h] = fmaxf(fmaxf(s_stat[h][0], s_stat[h][1]), fmaxf(s_stat[h][2], s_stat[h][3]));
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < G; ++h) {
+    const float pr = (mx[h] == -INFINITY || sc[h] == -INFINITY) ? 0.f : exp2f(sc[h] - mx[h]);
+    s_p[h][tid] = pr * vs_own;
+    const float l = wave_sum(pr);
+    if (lane == 0) s_stat[h][wave] = l;
+  }
+  __syncthreads();
+
+  // ---- P.V ----
+  float acc[G][8];
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
+#pragma unroll
+  for (int it = 0; it < VS; ++it) {
+    const int tl = wt0 + it * 4 + kg;
+    float vf[8];
+    fp8x8_to_f32(vreg[it], vf);
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      const float pr = s_p[h][tl];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(pr, vf[i], acc[h][i]);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < G; ++h)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float v = acc[h][i];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[h][i] = v;
+    }
+  if (kg == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s_red[wave][h][r16 * 8 + i] = acc[h][i];
+  }
+  if (tid < G) {
+    s_fin[0][tid] = mx[tid];
+    s_fin[1][tid] = (s_stat[tid][0] + s_stat[tid][1]) + (s_stat[tid][2] + s_stat[tid][3]);
+  }
+  __syncthreads();
+
+  if (nsplit == 1) {
+    for (int i = tid; i < G * D; i += kAttnThreads) {
+      const int h = i / D, d = i - h * D;
+      const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
+      const float L = s_fin[1][h];
+      out[((size_t)b * Hq + g * G + h) * D + d] = f32_to_bf16(L > 0.f ? o / L : 0.f);
+    }
+    return;
+  }
+  for (int i = tid; i < G * D; i += kAttnThreads) {
+    const int h = i / D, d = i - h * D;
+    const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
+    ws_o[(((size_t)b * Hq + g * G + h) * max_splits + split) * D + d] = o;
+  }
+  if (tid < G) {
+    float* ml = ws_ml + (((size_t)b * Hq + g * G + tid) * max_splits + split) * 2;
+    ml[0] = s_fin[0][tid];
+    ml[1] = s_fin[1][tid];
+  }
+}
+
 }  // namespace sym
 
 using namespace sym;
@@ -621,9 +1039,10 @@ extern "C" int sym_attn_prefill_prologue(const void* qkv, const void* q_norm_w,
                             max_blocks_per_seq, num_blocks);
   if (rc) return rc;
   if (T == 0) return SYM_OK;
-  SYM_REQUIRE(qkv && positions && seq_ids && q_out && k_out && v_out && k_pool && v_pool &&
-                  block_tables,
+  SYM_REQUIRE(qkv && positions && seq_ids && q_out && k_out && v_out && block_tables,
               SYM_ERR_INVALID, "attn_prefill_prologue: null pointer argument");
+  SYM_REQUIRE((k_pool == nullptr) == (v_pool == nullptr), SYM_ERR_INVALID,
+              "attn_prefill_prologue: k_pool and v_pool must both be given or both be null");
   SYM_REQUIRE(Hq >= Hkv && Hq % Hkv == 0, SYM_ERR_INVALID,
               "attn_prefill_prologue: Hq=%d not a multiple of Hkv=%d", Hq, Hkv);
   SYM_REQUIRE(rotary_dim >= 0 && rotary_dim <= head_dim && rotary_dim % 2 == 0, SYM_ERR_INVALID,
@@ -694,16 +1113,22 @@ extern "C" size_t sym_paged_gqa_decode_workspace_bytes(int B, int Hq, int head_d
 
 // Argument checks and launch of the split kernel (plain or fused with the prologue) and the
 // merge kernel.
+// k_scale / v_scale non-null: the pools are fp8 e4m3fn with per-(block, head) scales.
 static int launch_decode(const char* what, const void* q, const FusedQKV* fq, void* k_pool,
-                         void* v_pool, const int32_t* block_tables, const int32_t* positions,
-                         int B, int Hq, int Hkv, int head_dim, int block_size,
-                         int max_blocks_per_seq, int num_blocks, int max_context, float scale,
-                         void* workspace, size_t workspace_bytes, void* out, void* stream) {
+                         void* v_pool, float* k_scale, float* v_scale,
+                         const int32_t* block_tables, const int32_t* positions, int B, int Hq,
+                         int Hkv, int head_dim, int block_size, int max_blocks_per_seq,
+                         int num_blocks, int max_context, float scale, void* workspace,
+                         size_t workspace_bytes, void* out, void* stream) {
   int rc = check_cache_args(what, B, Hkv, head_dim, block_size, max_blocks_per_seq, num_blocks);
   if (rc) return rc;
   if (B == 0) return SYM_OK;
   SYM_REQUIRE((q || fq) && k_pool && v_pool && block_tables && positions && workspace && out,
               SYM_ERR_INVALID, "%s: null pointer argument", what);
+  const bool fp8 = k_scale != nullptr;
+  SYM_REQUIRE(fp8 == (v_scale != nullptr), SYM_ERR_INVALID, "%s: k_scale and v_scale", what);
+  SYM_REQUIRE(!fp8 || kSplit % block_size == 0, SYM_ERR_UNSUPPORTED,
+              "%s: fp8 cache needs block_size dividing %d (got %d)", what, kSplit, block_size);
   SYM_REQUIRE(Hq >= Hkv && Hq % Hkv == 0, SYM_ERR_INVALID, "%s: Hq=%d not a multiple of Hkv=%d",
               what, Hq, Hkv);
   const int G = Hq / Hkv;
@@ -727,10 +1152,19 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
   uint16_t* kp = (uint16_t*)k_pool;
   uint16_t* vp = (uint16_t*)v_pool;
   const FusedQKV f = fq ? *fq : FusedQKV{};
+  uint8_t* kp8 = (uint8_t*)k_pool;
+  uint8_t* vp8 = (uint8_t*)v_pool;
 #define SYM_LAUNCH_DECODE(GG, FF)                                                               \
-  hipLaunchKernelGGL((paged_decode_kernel<GG, kTPW, FF>), grid, block, 0, s, qq, f, kp, vp,     \
-                     block_tables, positions, Hkv, block_size, max_blocks_per_seq, num_blocks,  \
-                     max_context, scale_log2, ws_o, ws_ml, max_splits, (uint16_t*)out)
+  if (fp8)                                                                                      \
+    hipLaunchKernelGGL((paged_decode_fp8_kernel<GG, FF>), grid, block, 0, s, qq, f, kp8, vp8,   \
+                       k_scale, v_scale, block_tables, positions, Hkv, block_size,              \
+                       max_blocks_per_seq, num_blocks, max_context, scale_log2, ws_o, ws_ml,    \
+                       max_splits, (uint16_t*)out);                                             \
+  else                                                                                          \
+    hipLaunchKernelGGL((paged_decode_kernel<GG, kTPW, FF>), grid, block, 0, s, qq, f, kp, vp,   \
+                       block_tables, positions, Hkv, block_size, max_blocks_per_seq,            \
+                       num_blocks, max_context, scale_log2, ws_o, ws_ml, max_splits,            \
+                       (uint16_t*)out)
 #define SYM_LAUNCH_DECODE_G(FF)               \
   switch (G) {                                \
     case 1: SYM_LAUNCH_DECODE(1, FF); break;  \
@@ -745,7 +1179,7 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
   }
 #undef SYM_LAUNCH_DECODE_G
 #undef SYM_LAUNCH_DECODE
-  rc = sym_host::check_launch("paged_decode_kernel");
+  rc = sym_host::check_launch(fp8 ? "paged_decode_fp8_kernel" : "paged_decode_kernel");
   if (rc || max_splits == 1) return rc;
   hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((B * Hq + 3) / 4), dim3(256), 0, s, ws_o,
                      ws_ml, positions, B, Hq, max_context, max_splits, (uint16_t*)out);
@@ -761,7 +1195,8 @@ extern "C" int sym_paged_gqa_decode(const void* q, const void* k_pool, const voi
   SYM_REQUIRE(B <= 0 || q, SYM_ERR_INVALID, "paged_gqa_decode: null pointer argument");
   // the plain kernel only reads the pools
   return launch_decode("paged_gqa_decode", q, nullptr, const_cast<void*>(k_pool),
-                       const_cast<void*>(v_pool), block_tables, positions, B, Hq, Hkv, head_dim,
+                       const_cast<void*>(v_pool), nullptr, nullptr, block_tables, positions, B,
+                       Hq, Hkv, head_dim,
                        block_size, max_blocks_per_seq, num_blocks, max_context, scale, workspace,
                        workspace_bytes, out, stream);
 }
@@ -788,7 +1223,85 @@ extern "C" int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const
                     rotary_dim ? max_pos : 0,
                     rotary_dim,
                     eps};
-  return launch_decode("attn_decode_step", nullptr, &fq, k_pool, v_pool, block_tables, positions,
-                       B, Hq, Hkv, head_dim, block_size, max_blocks_per_seq, num_blocks,
-                       max_context, scale, workspace, workspace_bytes, out, stream);
+  return launch_decode("attn_decode_step", nullptr, &fq, k_pool, v_pool, nullptr, nullptr,
+                       block_tables, positions, B, Hq, Hkv, head_dim, block_size,
+                       max_blocks_per_seq, num_blocks, max_context, scale, workspace,
+                       workspace_bytes, out, stream);
+}
+
+extern "C" int sym_paged_gqa_decode_fp8(const void* q, const void* k_pool, const void* v_pool,
+                                        const float* k_scale, const float* v_scale,
+                                        const int32_t* block_tables, const int32_t* positions,
+                                        int B, int Hq, int Hkv, int head_dim, int block_size,
+                                        int max_blocks_per_seq, int num_blocks, int max_context,
+                                        float scale, void* workspace, size_t workspace_bytes,
+                                        void* out, void* stream) {
+  SYM_REQUIRE(B <= 0 || (q && k_scale && v_scale), SYM_ERR_INVALID,
+              "paged_gqa_decode_fp8: null pointer argument");
+  // the plain kernel only reads the pools and scales
+  return launch_decode("paged_gqa_decode_fp8", q, nullptr, const_cast<void*>(k_pool),
+                       const_cast<void*>(v_pool), const_cast<float*>(k_scale),
+                       const_cast<float*>(v_scale), block_tables, positions, B, Hq, Hkv,
+                       head_dim, block_size, max_blocks_per_seq, num_blocks, max_context, scale,
+                       workspace, workspace_bytes, out, stream);
+}
+
+extern "C" int sym_attn_decode_step_fp8(const void* qkv, const void* q_norm_w,
+                                        const void* k_norm_w, const float* rope_cs, int max_pos,
+                                        const int32_t* positions, int B, int Hq, int Hkv,
+                                        int head_dim, int rotary_dim, float eps, int use_qk_norm,
+                                        void* k_pool, void* v_pool, float* k_scale,
+                                        float* v_scale, const int32_t* block_tables,
+                                        int max_blocks_per_seq, int block_size, int num_blocks,
+                                        int max_context, float scale, void* workspace,
+                                        size_t workspace_bytes, void* out, void* stream) {
+  SYM_REQUIRE(B <= 0 || (qkv && k_scale && v_scale), SYM_ERR_INVALID,
+              "attn_decode_step_fp8: null pointer argument");
+  SYM_REQUIRE(rotary_dim >= 0 && rotary_dim <= head_dim && rotary_dim % 2 == 0, SYM_ERR_INVALID,
+              "attn_decode_step_fp8: rotary_dim=%d", rotary_dim);
+  SYM_REQUIRE(rotary_dim == 0 || (rope_cs && max_pos > 0), SYM_ERR_INVALID,
+              "attn_decode_step_fp8: rope table missing");
+  SYM_REQUIRE(!use_qk_norm || (q_norm_w && k_norm_w), SYM_ERR_INVALID,
+              "attn_decode_step_fp8: QK-norm weights missing");
+  const FusedQKV fq{(const uint16_t*)qkv,
+                    use_qk_norm ? (const uint16_t*)q_norm_w : nullptr,
+                    use_qk_norm ? (const uint16_t*)k_norm_w : nullptr,
+                    rotary_dim ? rope_cs : nullptr,
+                    rotary_dim ? max_pos : 0,
+                    rotary_dim,
+                    eps};
+  return launch_decode("attn_decode_step_fp8", nullptr, &fq, k_pool, v_pool, k_scale, v_scale,
+                       block_tables, positions, B, Hq, Hkv, head_dim, block_size,
+                       max_blocks_per_seq, num_blocks, max_context, scale, workspace,
+                       workspace_bytes, out, stream);
+}
+
+extern "C" int sym_paged_kv_fill_fp8(const void* k, const void* v, long long tok_stride,
+                                     long long head_stride, const int32_t* cu_seqlens,
+                                     const int32_t* start_pos, int n_seqs, int max_seqlen,
+                                     int Hkv, int head_dim, void* k_pool, void* v_pool,
+                                     float* k_scale, float* v_scale, const int32_t* block_tables,
+                                     int max_blocks_per_seq, int block_size, int num_blocks,
+                                     void* stream) {
+  int rc = check_cache_args("paged_kv_fill_fp8", n_seqs, Hkv, head_dim, block_size,
+                            max_blocks_per_seq, num_blocks);
+  if (rc) return rc;
+  SYM_REQUIRE(max_seqlen >= 0, SYM_ERR_INVALID, "paged_kv_fill_fp8: max_seqlen=%d", max_seqlen);
+  if (n_seqs == 0 || max_seqlen == 0) return SYM_OK;
+  SYM_REQUIRE(k && v && cu_seqlens && k_pool && v_pool && k_scale && v_scale && block_tables,
+              SYM_ERR_INVALID, "paged_kv_fill_fp8: null pointer argument");
+  SYM_REQUIRE(kSplit % block_size == 0, SYM_ERR_UNSUPPORTED,
+              "paged_kv_fill_fp8: block_size=%d must divide %d", block_size, kSplit);
+  SYM_REQUIRE(n_seqs <= 65535 && Hkv <= 65535, SYM_ERR_INVALID, "paged_kv_fill_fp8: grid");
+  SYM_REQUIRE(tok_stride > 0 && head_stride > 0 && tok_stride % 8 == 0 && head_stride % 8 == 0,
+              SYM_ERR_INVALID, "paged_kv_fill_fp8: strides %lld, %lld must be positive multiples"
+              " of 8", tok_stride, head_stride);
+  const int gx = (max_seqlen + block_size - 1) / block_size + 1;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(paged_kv_fill_fp8_kernel, dim3(gx, Hkv, n_seqs), dim3(256), 0,
+                     (hipStream_t)stream, (const uint16_t*)k, (const uint16_t*)v, tok_stride,
+                     head_stride, cu_seqlens, start_pos, Hkv, (uint8_t*)k_pool, (uint8_t*)v_pool,
+                     k_scale, v_scale,
+                     block_tables, max_blocks_per_seq, block_size, num_blocks);
+  return sym_host::check_launch("paged_kv_fill_fp8_kernel");
 }

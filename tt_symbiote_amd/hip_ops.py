@@ -240,9 +240,23 @@ class PagedLayout:
     max_blocks_per_seq: int
 
 
-def _check_pools(k_pool, v_pool, block_tables, batch: int) -> PagedLayout:
-    _check(k_pool, "k_pool", torch.bfloat16)
-    _check(v_pool, "v_pool", torch.bfloat16, k_pool.device)
+def _check_pools(k_pool, v_pool, block_tables, batch: int, k_scale=None,
+                 v_scale=None) -> PagedLayout:
+    """bf16 pools, or fp8 e4m3fn pools with their [num_blocks, Hkv] fp32 scales."""
+    fp8 = k_pool.dtype == torch.float8_e4m3fn if isinstance(k_pool, torch.Tensor) else False
+    dt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    _check(k_pool, "k_pool", dt)
+    _check(v_pool, "v_pool", dt, k_pool.device)
+    if fp8:
+        if k_scale is None or v_scale is None:
+            raise ValueError("an fp8 KV cache needs k_scale and v_scale [num_blocks, Hkv]")
+        for t, n in ((k_scale, "k_scale"), (v_scale, "v_scale")):
+            _check(t, n, torch.float32, k_pool.device)
+            _check_shape(t, n, tuple(k_pool.shape[:2]))
+        if 256 % k_pool.shape[2]:
+            raise ValueError(f"fp8 KV cache: block_size {k_pool.shape[2]} must divide 256")
+    elif k_scale is not None or v_scale is not None:
+        raise ValueError("k_scale / v_scale given for a bf16 KV cache")
     if k_pool.dim() != 4 or k_pool.shape != v_pool.shape:
         raise ValueError(f"k_pool/v_pool must be [num_blocks, Hkv, block_size, D] and equal, got "
                          f"{tuple(k_pool.shape)} / {tuple(v_pool.shape)}")
@@ -300,16 +314,17 @@ def attn_decode_step(qkv: torch.Tensor, positions: torch.Tensor, k_pool: torch.T
                      rope_cs: Optional[torch.Tensor], q_norm_w: Optional[torch.Tensor],
                      k_norm_w: Optional[torch.Tensor], eps: float,
                      max_context: Optional[int] = None, workspace: Optional[torch.Tensor] = None,
-                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     out: Optional[torch.Tensor] = None, k_scale: Optional[torch.Tensor] = None,
+                     v_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The fused decode step: :func:`attn_decode_prologue` (QK-norm, RoPE, k/v written into the
     pools at ``positions``) and :func:`paged_gqa_decode` in one pass; returns the attention
-    output [B, Hq, D]."""
+    output [B, Hq, D]. fp8 pools take their per-(block, head) scales."""
     _check(qkv, "qkv", torch.bfloat16)
     B = qkv.shape[0]
     _check_shape(qkv, "qkv", (B, (num_heads + 2 * num_kv_heads) * HEAD_DIM))
     _check(positions, "positions", torch.int32, qkv.device)
     _check_shape(positions, "positions", (B,))
-    lay = _check_pools(k_pool, v_pool, block_tables, B)
+    lay = _check_pools(k_pool, v_pool, block_tables, B, k_scale, v_scale)
     if lay.num_kv_heads != num_kv_heads:
         raise ValueError(f"pool has {lay.num_kv_heads} kv heads, module {num_kv_heads}")
     use_norm = q_norm_w is not None
@@ -336,6 +351,15 @@ def attn_decode_step(qkv: torch.Tensor, positions: torch.Tensor, k_pool: torch.T
         out = torch.empty(B, num_heads, HEAD_DIM, dtype=torch.bfloat16, device=qkv.device)
     _check(out, "out", torch.bfloat16, qkv.device)
     _check_shape(out, "out", (B, num_heads, HEAD_DIM))
+    if k_scale is not None:
+        _timed("paged_gqa_decode", lambda: _lib.call(
+            "sym_attn_decode_step_fp8", _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w),
+            _ptr(rope_cs), max_pos, _ptr(positions), B, num_heads, num_kv_heads, HEAD_DIM,
+            rotary_dim, float(eps), 1 if use_norm else 0, _ptr(k_pool), _ptr(v_pool),
+            _ptr(k_scale), _ptr(v_scale), _ptr(block_tables), lay.max_blocks_per_seq,
+            lay.block_size, lay.num_blocks, int(max_context), float(scale), _ptr(workspace),
+            workspace.numel(), _ptr(out), _stream()))
+        return out
     _timed("paged_gqa_decode", lambda: _lib.call(
         "sym_attn_decode_step", _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w), _ptr(rope_cs),
         max_pos, _ptr(positions), B, num_heads, num_kv_heads, HEAD_DIM, rotary_dim, float(eps),
@@ -351,14 +375,23 @@ def attn_prefill_prologue(qkv: torch.Tensor, positions: torch.Tensor, seq_ids: t
                           rope_cs: Optional[torch.Tensor], q_norm_w: Optional[torch.Tensor],
                           k_norm_w: Optional[torch.Tensor], eps: float):
     """QK-norm + partial RoPE of T packed tokens (token t at positions[t] of page-table row
-    seq_ids[t]); k/v written into the pools; returns q [T, Hq, D], k, v [T, Hkv, D]."""
+    seq_ids[t]); k/v written into bf16 pools (not when the pools are fp8: those are filled from
+    the returned k, v by :func:`paged_kv_fill_fp8`); returns q [T, Hq, D], k, v [T, Hkv, D]."""
     _check(qkv, "qkv", torch.bfloat16)
     T = qkv.shape[0]
     _check_shape(qkv, "qkv", (T, (num_heads + 2 * num_kv_heads) * HEAD_DIM))
     for t, n in ((positions, "positions"), (seq_ids, "seq_ids")):
         _check(t, n, torch.int32, qkv.device)
         _check_shape(t, n, (T,))
-    lay = _check_pools(k_pool, v_pool, block_tables, 1)
+    write_pools = k_pool.dtype == torch.bfloat16
+    if write_pools:
+        lay = _check_pools(k_pool, v_pool, block_tables, 1)
+    else:
+        if k_pool.dtype != torch.float8_e4m3fn or v_pool.dtype != torch.float8_e4m3fn:
+            raise TypeError(f"pools must be bf16 or float8_e4m3fn, got {k_pool.dtype}")
+        _check(block_tables, "block_tables", torch.int32, qkv.device)
+        nb, hkv, bs, _ = k_pool.shape
+        lay = PagedLayout(nb, hkv, bs, HEAD_DIM, block_tables.shape[1])
     if lay.num_kv_heads != num_kv_heads:
         raise ValueError(f"pool has {lay.num_kv_heads} kv heads, module {num_kv_heads}")
     use_norm = q_norm_w is not None
@@ -379,7 +412,8 @@ def attn_prefill_prologue(qkv: torch.Tensor, positions: torch.Tensor, seq_ids: t
     _lib.call("sym_attn_prefill_prologue", _ptr(qkv), _ptr(q_norm_w), _ptr(k_norm_w),
               _ptr(rope_cs), max_pos, _ptr(positions), _ptr(seq_ids), T, num_heads,
               num_kv_heads, HEAD_DIM, rotary_dim, float(eps), 1 if use_norm else 0, _ptr(q),
-              _ptr(k), _ptr(v), _ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
+              _ptr(k), _ptr(v), _ptr(k_pool) if write_pools else None,
+              _ptr(v_pool) if write_pools else None, _ptr(block_tables),
               lay.max_blocks_per_seq, lay.block_size, lay.num_blocks, _stream())
     return q, k, v
 
@@ -452,13 +486,15 @@ def paged_decode_workspace_bytes(batch: int, num_heads: int, max_context: int) -
 def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                      block_tables: torch.Tensor, positions: torch.Tensor, scale: float,
                      max_context: Optional[int] = None, workspace: Optional[torch.Tensor] = None,
-                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Decode attention of q [B, Hq, D] over slots 0..positions[b] of each sequence."""
+                     out: Optional[torch.Tensor] = None, k_scale: Optional[torch.Tensor] = None,
+                     v_scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Decode attention of q [B, Hq, D] over slots 0..positions[b] of each sequence (bf16
+    pools, or fp8 pools with their scales)."""
     _check(q, "q", torch.bfloat16)
     if q.dim() != 3 or q.shape[2] != HEAD_DIM:
         raise ValueError(f"q must be [B, Hq, {HEAD_DIM}], got {tuple(q.shape)}")
     B, Hq, _ = q.shape
-    lay = _check_pools(k_pool, v_pool, block_tables, B)
+    lay = _check_pools(k_pool, v_pool, block_tables, B, k_scale, v_scale)
     _check(positions, "positions", torch.int32, q.device)
     _check_shape(positions, "positions", (B,))
     cap = lay.max_blocks_per_seq * lay.block_size
@@ -474,12 +510,58 @@ def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
         out = torch.empty_like(q)
     _check(out, "out", torch.bfloat16, q.device)
     _check_shape(out, "out", tuple(q.shape))
+    if k_scale is not None:
+        _timed("paged_gqa_decode", lambda: _lib.call(
+            "sym_paged_gqa_decode_fp8", _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(k_scale),
+            _ptr(v_scale), _ptr(block_tables), _ptr(positions), B, Hq, lay.num_kv_heads,
+            HEAD_DIM, lay.block_size, lay.max_blocks_per_seq, lay.num_blocks, int(max_context),
+            float(scale), _ptr(workspace), workspace.numel(), _ptr(out), _stream()))
+        return out
     _timed("paged_gqa_decode", lambda: _lib.call(
         "sym_paged_gqa_decode", _ptr(q), _ptr(k_pool), _ptr(v_pool), _ptr(block_tables),
         _ptr(positions), B, Hq, lay.num_kv_heads, HEAD_DIM, lay.block_size,
         lay.max_blocks_per_seq, lay.num_blocks, int(max_context), float(scale),
         _ptr(workspace), workspace.numel(), _ptr(out), _stream()))
     return out
+
+
+def paged_kv_fill_fp8(k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
+                      max_seqlen: int, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                      k_scale: torch.Tensor, v_scale: torch.Tensor, block_tables: torch.Tensor,
+                      start_pos: Optional[torch.Tensor] = None, layout: str = "thd") -> None:
+    """Append tokens to an fp8 KV cache (per-(block, head) power-of-two scales, requantising a
+    block's earlier tokens when its scale grows). Sequence s = tokens cu_seqlens[s] ..
+    cu_seqlens[s+1]-1 at positions start_pos[s] + i (0 when start_pos is None) in page-table row
+    s. ``layout``: "thd" for k, v [T, Hkv, D]; "htd" for k, v [Hkv, T, D]."""
+    _check(k, "k", torch.bfloat16)
+    _check(v, "v", torch.bfloat16, k.device)
+    _check_shape(v, "v", tuple(k.shape))
+    _check(cu_seqlens, "cu_seqlens", torch.int32, k.device)
+    n = cu_seqlens.numel() - 1
+    if n < 0 or cu_seqlens.dim() != 1:
+        raise ValueError("cu_seqlens must be [n_seqs + 1]")
+    lay = _check_pools(k_pool, v_pool, block_tables, n, k_scale, v_scale)
+    if k_pool.dtype != torch.float8_e4m3fn:
+        raise TypeError("paged_kv_fill_fp8 needs float8_e4m3fn pools")
+    if k.dim() != 3 or k.shape[2] != HEAD_DIM:
+        raise ValueError(f"k must be 3-D with head_dim {HEAD_DIM}, got {tuple(k.shape)}")
+    if layout == "thd":
+        T, hkv, _ = k.shape
+        strides = (hkv * HEAD_DIM, HEAD_DIM)
+    elif layout == "htd":
+        hkv, T, _ = k.shape
+        strides = (HEAD_DIM, T * HEAD_DIM)
+    else:
+        raise ValueError(f"layout {layout!r}")
+    if hkv != lay.num_kv_heads:
+        raise ValueError(f"k has {hkv} kv heads, the pool {lay.num_kv_heads}")
+    if start_pos is not None:
+        _check(start_pos, "start_pos", torch.int32, k.device)
+        _check_shape(start_pos, "start_pos", (n,))
+    _lib.call("sym_paged_kv_fill_fp8", _ptr(k), _ptr(v), strides[0], strides[1],
+              _ptr(cu_seqlens), _ptr(start_pos), n, int(max_seqlen), lay.num_kv_heads, HEAD_DIM,
+              _ptr(k_pool), _ptr(v_pool), _ptr(k_scale), _ptr(v_scale), _ptr(block_tables),
+              lay.max_blocks_per_seq, lay.block_size, lay.num_blocks, _stream())
 
 
 # -------------------------------------------------------------------------------------------
@@ -602,19 +684,71 @@ def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,
 TILED_MIN_TOKENS = 128  # from this many tokens the expert GEMMs use the tiled (MFMA-bound) kernels
 
 
-def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up: torch.Tensor,
-                       w_down: torch.Tensor, h: Optional[torch.Tensor] = None,
+FP8_BLOCK = 128
+
+
+@dataclass
+class BlockFp8:
+    """A weight stored as OCP fp8 e4m3fn with one fp32 scale per 128 x 128 block of its last two
+    dims: w[..., n, k] = float(q[..., n, k]) * scale[..., n // 128, k // 128]."""
+    q: torch.Tensor      # [..., N, K] torch.float8_e4m3fn
+    scale: torch.Tensor  # [..., N / 128, K / 128] float32
+
+    @property
+    def shape(self):
+        return self.q.shape
+
+    def check(self, name: str, device=None):
+        _check(self.q, name + ".q", torch.float8_e4m3fn, device)
+        _check(self.scale, name + ".scale", torch.float32, device)
+        *lead, n, k = self.q.shape
+        if n % FP8_BLOCK or k % FP8_BLOCK:
+            raise ValueError(f"{name}: dims {n} x {k} must be multiples of {FP8_BLOCK}")
+        _check_shape(self.scale, name + ".scale", (*lead, n // FP8_BLOCK, k // FP8_BLOCK))
+
+    def numel_bytes(self) -> int:
+        return self.q.numel() + 4 * self.scale.numel()
+
+
+def quantize_block_fp8(w: torch.Tensor) -> BlockFp8:
+    """Weight intake for the fp8 format: per 128 x 128 block, scale = amax / 448 (1 for an
+    all-zero block) and q = e4m3fn(w / scale) (round to nearest even, clamped to +-448). Runs
+    once when weights are prepared, on whatever device w is on."""
+    *lead, n, k = w.shape
+    if n % FP8_BLOCK or k % FP8_BLOCK:
+        raise ValueError(f"dims {n} x {k} must be multiples of {FP8_BLOCK}")
+    wb = w.float().reshape(*lead, n // FP8_BLOCK, FP8_BLOCK, k // FP8_BLOCK, FP8_BLOCK)
+    amax = wb.abs().amax(dim=(-3, -1))
+    scale = torch.where(amax > 0, amax / 448.0, torch.ones_like(amax))
+    q = (wb / scale[..., :, None, :, None]).clamp(-448.0, 448.0)
+    q = q.reshape(*lead, n, k).to(torch.float8_e4m3fn)
+    return BlockFp8(q.contiguous(), scale.contiguous())
+
+
+def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
+                       w_down, h: Optional[torch.Tensor] = None,
                        y: Optional[torch.Tensor] = None, kernel: str = "auto"):
     """h = silu(x Wg^T) * (x Wu^T), y = h Wd^T per segment; returns (h [rows, I], y [rows, H]).
-    ``kernel``: "stream" (weight-streaming kernels for decode-size segments), "tiled" (128 x 128
-    MFMA tiles for prefill-size segments) or "auto" (tiled from TILED_MIN_TOKENS tokens)."""
+    The weights are bf16 tensors, or BlockFp8 (fp8 e4m3fn + 128 x 128 block scales, dequantized
+    in the kernel). ``kernel``: "stream" (weight-streaming kernels for decode-size segments),
+    "tiled" (128 x 128 MFMA tiles for prefill-size segments, bf16 only) or "auto" (tiled from
+    TILED_MIN_TOKENS tokens with bf16 weights)."""
     _check(x, "x", torch.bfloat16)
     if x.dim() != 2:
         raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
     T, H = x.shape
     dev = x.device
-    _check(w_gate_up, "w_gate_up", torch.bfloat16, dev)
-    _check(w_down, "w_down", torch.bfloat16, dev)
+    fp8 = isinstance(w_gate_up, BlockFp8)
+    if fp8 != isinstance(w_down, BlockFp8):
+        raise ValueError("w_gate_up and w_down must both be bf16 or both BlockFp8")
+    if fp8:
+        w_gate_up.check("w_gate_up", dev)
+        w_down.check("w_down", dev)
+        s_gate_up, s_down = w_gate_up.scale, w_down.scale
+        w_gate_up, w_down = w_gate_up.q, w_down.q
+    else:
+        _check(w_gate_up, "w_gate_up", torch.bfloat16, dev)
+        _check(w_down, "w_down", torch.bfloat16, dev)
     if w_gate_up.dim() != 3 or w_gate_up.shape[2] != H or w_gate_up.shape[1] % 2:
         raise ValueError(f"w_gate_up must be [S, 2I, {H}], got {tuple(w_gate_up.shape)}")
     S, I2, _ = w_gate_up.shape
@@ -639,6 +773,19 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up: torch.Ten
     stream = _stream()
     if kernel not in ("auto", "stream", "tiled"):
         raise ValueError(f"kernel {kernel!r}")
+    if fp8:
+        if kernel == "tiled":
+            raise NotImplementedError("fp8 expert weights: only the streaming kernels")
+        _timed("moe_gate_up", lambda: _lib.call(
+            "sym_moe_gate_up_fp8", _ptr(x), T, H, I, _ptr(route.sorted_tokens),
+            _ptr(route.seg_expert), _ptr(route.seg_offset), _ptr(route.seg_count),
+            _ptr(route.n_segments), max_segments, _ptr(w_gate_up), _ptr(s_gate_up), _ptr(h),
+            stream))
+        _timed("moe_down", lambda: _lib.call(
+            "sym_moe_down_fp8", _ptr(h), T, H, I, _ptr(route.seg_expert), _ptr(route.seg_offset),
+            _ptr(route.seg_count), _ptr(route.n_segments), max_segments, _ptr(w_down),
+            _ptr(s_down), _ptr(y), stream))
+        return h, y
     tiled = kernel == "tiled" or (kernel == "auto" and T >= TILED_MIN_TOKENS)
     if tiled:
         _timed("moe_gate_up", lambda: _lib.call(

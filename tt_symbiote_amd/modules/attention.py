@@ -189,7 +189,8 @@ class HIPBailingMoEAttention(StatefulHIPModule):
             cache.page_table_device, self.scaling, num_heads=self.num_heads,
             num_kv_heads=self.num_kv_heads, rotary_dim=self.rotary_dim, rope_cs=d["rope"],
             q_norm_w=d["q_norm"], k_norm_w=d["k_norm"], eps=self.norm_eps,
-            max_context=cache.max_context, workspace=cache.decode_workspace(B, self.num_heads))
+            max_context=cache.max_context, workspace=cache.decode_workspace(B, self.num_heads),
+            k_scale=cache.key_scale(self.layer_idx), v_scale=cache.value_scale(self.layer_idx))
         return o.view(B, self.num_heads * self.head_dim)
 
     def dense_residual(self, o: torch.Tensor, residual: torch.Tensor):
@@ -204,7 +205,8 @@ class HIPBailingMoEAttention(StatefulHIPModule):
         """Prefill of packed sequences: x [T, H] (bf16, already normalised by the layer), token
         t of sequence seq_ids[t] at positions[t] (0 .. L-1). Writes the sequences' K/V into the
         paged cache (page-table row = sequence) and returns the attention output after the
-        dense projection, [T, H] bf16."""
+        dense projection, [T, H] bf16. With an fp8 cache the sequences start at position 0 and
+        sequence s uses page-table row s (the K/V are appended per block after the prologue)."""
         d = self._dev
         qkv = hip_ops.gemm(x, d["qkv_w"], d["qkv_b"])
         q, k, v = hip_ops.attn_prefill_prologue(
@@ -213,6 +215,11 @@ class HIPBailingMoEAttention(StatefulHIPModule):
             num_heads=self.num_heads, num_kv_heads=self.num_kv_heads,
             rotary_dim=self.rotary_dim, rope_cs=d["rope"], q_norm_w=d["q_norm"],
             k_norm_w=d["k_norm"], eps=self.norm_eps)
+        if cache.is_fp8:
+            hip_ops.paged_kv_fill_fp8(
+                k, v, cu_seqlens, max_seqlen, cache.key_cache(self.layer_idx),
+                cache.value_cache(self.layer_idx), cache.key_scale(self.layer_idx),
+                cache.value_scale(self.layer_idx), cache.page_table_device)
         o = hip_ops.prefill_attention(q, k, v, cu_seqlens, max_seqlen, self.scaling)
         return hip_ops.gemm(o.view(-1, self.num_heads * self.head_dim), d["dense_w"],
                             d["dense_b"])

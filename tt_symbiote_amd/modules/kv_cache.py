@@ -9,6 +9,11 @@ table ``[batch, blocks_per_sequence]`` int32 mapping logical to physical blocks 
 ``paged_sdpa_decode``, ``update_seq_length``, ``get_seq_length``, ``get_max_cache_shape``,
 ``update`` and ``reset``, with the same host-side counter semantics.
 
+An fp8 variant (``dtype=torch.float8_e4m3fn``) keeps the same pools in OCP e4m3fn bytes with
+one power-of-two fp32 scale per (block, kv head) per layer (``key_scale`` / ``value_scale``,
+``[max_num_blocks, num_kv_heads]``); appends requantise a block's earlier tokens when its scale
+grows. The reference's cache is bf16 only; the format and its rule are this build's.
+
 Differences: pools are torch tensors in HBM (one allocation per pool); the page table is
 validated on the host when installed (every entry must name a block of the pool) and copied in
 place when its shape is unchanged, so captured HIP graphs that read it stay valid; positions are
@@ -52,8 +57,10 @@ class HIPPagedAttentionKVCache(_CacheBase):
                 super().__init__(layers=[])
             except Exception:
                 super().__init__()
-        if dtype != torch.bfloat16:
-            raise NotImplementedError(f"KV cache dtype {dtype} (bf16 only)")
+        if dtype not in (torch.bfloat16, torch.float8_e4m3fn):
+            raise NotImplementedError(f"KV cache dtype {dtype} (bf16 or float8_e4m3fn)")
+        if dtype == torch.float8_e4m3fn and 256 % config.block_size:
+            raise ValueError(f"fp8 KV cache: block_size {config.block_size} must divide 256")
         if head_dim != hip_ops.HEAD_DIM:
             raise NotImplementedError(f"head_dim {head_dim} (kernels implement {hip_ops.HEAD_DIM})")
         if config.blocks_per_sequence < 1:
@@ -71,6 +78,9 @@ class HIPPagedAttentionKVCache(_CacheBase):
         self.page_table = table.reshape(config.batch_size, config.blocks_per_sequence)
         self._key_cache: List[Optional[torch.Tensor]] = [None] * num_layers
         self._value_cache: List[Optional[torch.Tensor]] = [None] * num_layers
+        self._key_scale: List[Optional[torch.Tensor]] = [None] * num_layers
+        self._value_scale: List[Optional[torch.Tensor]] = [None] * num_layers
+        self._arange: Optional[torch.Tensor] = None
         self._page_table_dev: Optional[torch.Tensor] = None
         self._is_on_device = False
         self._decode_ws: Optional[torch.Tensor] = None
@@ -87,6 +97,9 @@ class HIPPagedAttentionKVCache(_CacheBase):
         for i in range(self.num_layers):
             self._key_cache[i] = torch.zeros(shape, dtype=self.dtype, device=device)
             self._value_cache[i] = torch.zeros(shape, dtype=self.dtype, device=device)
+            if self.is_fp8:
+                self._key_scale[i] = torch.zeros(shape[:2], dtype=torch.float32, device=device)
+                self._value_scale[i] = torch.zeros(shape[:2], dtype=torch.float32, device=device)
         self._page_table_dev = self.page_table.to(device)
         self._device = device
         self._is_on_device = True
@@ -99,6 +112,25 @@ class HIPPagedAttentionKVCache(_CacheBase):
     @property
     def device(self):
         return self._device
+
+    @property
+    def is_fp8(self) -> bool:
+        return self.dtype == torch.float8_e4m3fn
+
+    def key_scale(self, layer_idx: int) -> Optional[torch.Tensor]:
+        """Per-(block, kv head) scales of layer ``layer_idx``'s K pool (None for bf16)."""
+        self._require_device()
+        return self._key_scale[layer_idx]
+
+    def value_scale(self, layer_idx: int) -> Optional[torch.Tensor]:
+        self._require_device()
+        return self._value_scale[layer_idx]
+
+    def _cu_arange(self, n: int) -> torch.Tensor:
+        """[0, 1, .., n] int32 on the device (one token per sequence), kept for reuse."""
+        if self._arange is None or self._arange.numel() < n + 1:
+            self._arange = torch.arange(max(n + 1, 2), dtype=torch.int32, device=self._device)
+        return self._arange[:n + 1]
 
     def key_cache(self, layer_idx: int) -> torch.Tensor:
         self._require_device()
@@ -187,6 +219,17 @@ class HIPPagedAttentionKVCache(_CacheBase):
         max_len = self.max_context
         if k.shape[1] > max_len:
             k, v = k[:, :max_len], v[:, :max_len]
+        if self.is_fp8:
+            k = k.to(torch.bfloat16).contiguous()
+            v = v.to(torch.bfloat16).contiguous()
+            S = k.shape[1]
+            cu = torch.tensor([0, S], dtype=torch.int32, device=self._device)
+            hip_ops.paged_kv_fill_fp8(
+                k, v, cu, S, self._key_cache[layer_idx], self._value_cache[layer_idx],
+                self._key_scale[layer_idx], self._value_scale[layer_idx],
+                self._page_table_dev[batch_idx:batch_idx + 1], layout="htd")
+            self._advance(layer_idx, S)
+            return
         k = k.to(self.dtype).contiguous()
         v = v.to(self.dtype).contiguous()
         hip_ops.paged_kv_fill(k, v, self._key_cache[layer_idx], self._value_cache[layer_idx],
@@ -201,6 +244,14 @@ class HIPPagedAttentionKVCache(_CacheBase):
         v = value_states[0] if value_states.dim() == 4 else value_states
         B = k.shape[0]
         pos = self._positions(current_pos, B)
+        if self.is_fp8:
+            hip_ops.paged_kv_fill_fp8(
+                k.to(torch.bfloat16).contiguous(), v.to(torch.bfloat16).contiguous(),
+                self._cu_arange(B), 1, self._key_cache[layer_idx], self._value_cache[layer_idx],
+                self._key_scale[layer_idx], self._value_scale[layer_idx], self._page_table_dev,
+                start_pos=pos)
+            self._advance(layer_idx, 1)
+            return
         hip_ops.paged_kv_write(k.to(self.dtype).contiguous(), v.to(self.dtype).contiguous(),
                                self._key_cache[layer_idx], self._value_cache[layer_idx],
                                self._page_table_dev, pos)
@@ -224,8 +275,11 @@ class HIPPagedAttentionKVCache(_CacheBase):
         q = query[0] if squeeze else query
         B, Hq, _ = q.shape
         pos = self._positions(current_pos, B)
-        out = hip_ops.paged_gqa_decode(q.to(self.dtype).contiguous(), self._key_cache[layer_idx],
+        out = hip_ops.paged_gqa_decode(q.to(torch.bfloat16).contiguous(),
+                                       self._key_cache[layer_idx],
                                        self._value_cache[layer_idx], self._page_table_dev, pos,
                                        scale, max_context=self.max_context,
-                                       workspace=self.decode_workspace(B, Hq))
+                                       workspace=self.decode_workspace(B, Hq),
+                                       k_scale=self._key_scale[layer_idx],
+                                       v_scale=self._value_scale[layer_idx])
         return out.unsqueeze(0) if squeeze else out

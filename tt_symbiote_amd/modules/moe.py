@@ -9,6 +9,10 @@ Replaces ``TTNNBailingMoE`` (ttnn_moe.py:1494-1647) / ``TTNNMoE.forward`` (1413-
 forces ``norm_topk_prob`` True (ttnn_moe.py:1532). The shared expert (intermediate
 ``I * num_shared_experts``) is stored as stack slot ``E`` when its width equals ``I``.
 
+``weight_format="fp8_e4m3"`` stores the routed and shared expert weights as OCP fp8 e4m3fn with
+one fp32 scale per 128 x 128 block (quantised once when the weights are prepared); the grouped
+kernels dequantise inside the GEMM.
+
 Forward (decode or prefill token counts alike, no host synchronisation):
   logits = x_fp32 W_gate_fp32^T                   fp32 MFMA kernel (four partial sums)
   route  = fused router + top-k + permute kernel  (bit-exact indices)
@@ -36,13 +40,16 @@ class HIPBailingMoE(StatelessHIPModule):
         self.routed_scaling_factor = 1.0
         self.intermediate_size = None
         self.has_shared = False
+        self.weight_format = "bf16"
         self.keep_last_route = False  # keep the last RouteResult (inspection / tests)
         self.last_route = None
         self._host: Dict[str, torch.Tensor] = {}
         self._dev: Dict[str, torch.Tensor] = {}
 
+    WEIGHT_FORMATS = ("bf16", "fp8_e4m3")
+
     @classmethod
-    def from_torch(cls, torch_moe):
+    def from_torch(cls, torch_moe, weight_format: str = "bf16"):
         cfg = torch_moe.config
         experts = list(torch_moe.experts)
         gate = torch_moe.gate
@@ -61,16 +68,19 @@ class HIPBailingMoE(StatelessHIPModule):
             gate_weight=gate.weight, expert_bias=bias, experts=experts,
             shared_gate_up=shared_gate_up, shared_down=shared_down,
             top_k=cfg.num_experts_per_tok, n_group=cfg.n_group, topk_group=cfg.topk_group,
-            routed_scaling_factor=cfg.routed_scaling_factor)
+            routed_scaling_factor=cfg.routed_scaling_factor, weight_format=weight_format)
         new._fallback_torch_layer = torch_moe
         return new
 
     @classmethod
     def from_weights(cls, *, gate_weight, expert_bias, top_k, n_group, topk_group,
                      routed_scaling_factor, w_gate_up=None, w_down=None, experts=None,
-                     shared_gate_up=None, shared_down=None):
+                     shared_gate_up=None, shared_down=None, weight_format: str = "bf16"):
         """Build from stacked ``w_gate_up [E, 2I, H]`` / ``w_down [E, H, I]``, or from a list of
-        HF expert MLPs (stacked lazily in ``preprocess_weights`` to bound host memory)."""
+        HF expert MLPs (stacked lazily in ``preprocess_weights`` to bound host memory).
+        ``weight_format``: "bf16", or "fp8_e4m3" (128 x 128 block-scaled e4m3fn experts)."""
+        if weight_format not in cls.WEIGHT_FORMATS:
+            raise ValueError(f"weight_format {weight_format!r} not in {cls.WEIGHT_FORMATS}")
         if experts is not None:
             E = len(experts)
             I, H = experts[0].gate_proj.weight.shape
@@ -93,6 +103,7 @@ class HIPBailingMoE(StatelessHIPModule):
         new.routed_scaling_factor = float(routed_scaling_factor)
         new.intermediate_size = I
         new.has_shared = shared_gate_up is not None
+        new.weight_format = weight_format
         new._host = dict(gate_w=gate_weight, bias=expert_bias, gate_up=w_gate_up, down=w_down,
                          experts=experts, shared_gate_up=shared_gate_up, shared_down=shared_down)
         return new
@@ -117,6 +128,9 @@ class HIPBailingMoE(StatelessHIPModule):
         if self.has_shared:
             gate_up[E] = h["shared_gate_up"].detach().to(torch.bfloat16)
             down[E] = h["shared_down"].detach().to(torch.bfloat16)
+        if self.weight_format == "fp8_e4m3":
+            gate_up = hip_ops.quantize_block_fp8(gate_up)
+            down = hip_ops.quantize_block_fp8(down)
         self._host = dict(
             gate_w=h["gate_w"].detach().float().contiguous(),
             bias=h["bias"].detach().float().contiguous(),
@@ -124,7 +138,11 @@ class HIPBailingMoE(StatelessHIPModule):
         return super().preprocess_weights_impl()
 
     def move_weights_to_device_impl(self):
-        self._dev = {k: v.to(self.device) for k, v in self._host.items()}
+        def move(v):
+            if isinstance(v, hip_ops.BlockFp8):
+                return hip_ops.BlockFp8(v.q.to(self.device), v.scale.to(self.device))
+            return v.to(self.device)
+        self._dev = {k: move(v) for k, v in self._host.items()}
         self._host = {}
         return super().move_weights_to_device_impl()
 

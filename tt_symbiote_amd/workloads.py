@@ -143,6 +143,18 @@ def paged_context(batch: int, ctx_lo: int, ctx_hi: int, *, block_size: int = 32,
                         positions=ctx.to(torch.int32).to(dev), context_lens=ctx)
 
 
+def fp8_kv_pools(pool: torch.Tensor):
+    """Synthetic contents of an fp8 KV cache from a bf16 pool [nb, Hkv, bs, D]: per (block,
+    head) the power-of-two scale at or above amax / 448 and the e4m3fn bytes of pool / scale
+    (what appending the block's tokens to an empty block produces). Setup only."""
+    amax = pool.float().abs().amax(dim=(2, 3))
+    scale = torch.where(amax > 0, torch.exp2(torch.ceil(torch.log2(amax / 448.0))),
+                        torch.zeros_like(amax))
+    safe = torch.where(scale > 0, scale, torch.ones_like(scale))
+    q = (pool.float() / safe[..., None, None]).clamp(-448.0, 448.0).to(torch.float8_e4m3fn)
+    return q, scale.contiguous()
+
+
 def decode_layer_config(name: str) -> dict:
     """The decode workloads of the Ling-mini-2.0 layer: 'single' (one sequence of 512 cached
     tokens, 16+1 blocks of 32 placed by a random permutation of a 64-block pool) and 'batch32'
@@ -205,9 +217,9 @@ def prefill_batch(n_seqs: int, len_lo: int, len_hi: int, hidden: int, *, block_s
 
 
 def build_decoder_layer(w: Dict[str, torch.Tensor], shape: LayerShape = LING_MINI_2,
-                        layer_idx: int = 0):
+                        layer_idx: int = 0, weight_format: str = "bf16"):
     """HIP decoder layer (attention + MoE) from a :func:`layer_weights` dict (not yet bound
-    to a device)."""
+    to a device); ``weight_format`` "fp8_e4m3" stores the experts block-scaled in fp8."""
     from .modules.attention import HIPBailingMoEAttention
     from .modules.decoder_layer import HIPBailingMoEDecoderLayer
     from .modules.moe import HIPBailingMoE
@@ -224,6 +236,7 @@ def build_decoder_layer(w: Dict[str, torch.Tensor], shape: LayerShape = LING_MIN
         gate_weight=w["gate_w"], expert_bias=w["expert_bias"], w_gate_up=w["gate_up"],
         w_down=w["down"], shared_gate_up=w.get("shared_gate_up"),
         shared_down=w.get("shared_down"), top_k=shape.top_k, n_group=shape.n_group,
-        topk_group=shape.topk_group, routed_scaling_factor=shape.routed_scaling_factor)
+        topk_group=shape.topk_group, routed_scaling_factor=shape.routed_scaling_factor,
+        weight_format=weight_format)
     return HIPBailingMoEDecoderLayer.from_modules(attn, moe, w["ln1"], w["ln2"],
                                                   eps=shape.rms_norm_eps)
