@@ -259,7 +259,7 @@ def test_decoder_layer_fp8(device):
     <= 2e-2 on the output; the new token's K lands in its slot within fp8 rounding."""
     from oracle.bailing_moe_v2 import decoder_layer_from_weights
     from tt_symbiote_amd.workloads import (LING_MINI_2, build_decoder_layer, decode_layer_config,
-                                           layer_weights)
+                                           fp8_kv_pools, layer_weights)
     from test_gpu_layer import TOL, _oracle_with_gpu_routing
 
     w = layer_weights(LING_MINI_2, seed=0)
@@ -277,7 +277,11 @@ def test_decoder_layer_fp8(device):
     ctx = paged_context(cfg["batch"], cfg["ctx_lo"], cfg["ctx_hi"], block_size=cfg["block_size"],
                         num_kv_heads=4, seed=1, slack=cfg["slack"])
     nb = ctx.k_pool.shape[0]
-    kp, vp, ks, vs, codes, scales = _random_fp8_cache(nb, 4, cfg["block_size"], 3, device)
+    # K/V ~ N(0, 1) quantised per (block, head), as appending them to empty blocks would
+    kp, ks = fp8_kv_pools(ctx.k_pool.to(device))
+    vp, vs = fp8_kv_pools(ctx.v_pool.to(device))
+    codes = torch.stack([kp.view(torch.uint8).cpu(), vp.view(torch.uint8).cpu()])
+    scales = torch.stack([ks.cpu(), vs.cpu()])
     pcfg = ts.PagedAttentionConfig(block_size=cfg["block_size"], max_num_blocks=nb, batch_size=1)
     cache = ts.HIPPagedAttentionKVCache(1, 4, 128, pcfg, dtype=torch.float8_e4m3fn)
     cache.to_device(device)
