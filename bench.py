@@ -44,10 +44,12 @@ def parse_args():
     ap.add_argument("--cpu-steps", type=int, default=5)
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of replaying a captured HIP graph")
-    ap.add_argument("--workload", choices=["decode", "prefill", "fp8"], default="decode",
+    ap.add_argument("--workload", choices=["decode", "prefill", "fp8", "generate"],
+                    default="decode",
                     help="decode: the batch-32 decode step (the headline metric); prefill: 8 "
                          "packed prompts of U[256, 2048] tokens through the same layer; fp8: "
-                         "the batch-128 decode step with fp8 experts and an fp8 KV cache")
+                         "the batch-128 decode step with fp8 experts and an fp8 KV cache; "
+                         "generate: greedy generation with the whole 20-layer model")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy kernel (torch.neg, bf16) over 512 MiB three "
                          "times: the reference point that scales the FETCH_SIZE / WRITE_SIZE "
@@ -261,6 +263,135 @@ def fp8_algorithmic_bytes(shape, ctx, n_routed_active: int, B: int) -> dict:
     return dict(gate_up=gate_up, layer=layer, kv_read=kv_read, experts=n_exp * expert)
 
 
+def generate_main(args) -> None:
+    """Greedy generation with the whole Ling-mini-2.0-shaped model: 20 layers (layer 0 dense,
+    intermediate 5120; 19 MoE layers), vocab 157184, batch 64 prompts of 2048 random ids, 128
+    new tokens, paged KV (block 32, 8192 blocks). value = decode tokens/s (64 x 127 / the time
+    of the 127 captured decode steps after the first token)."""
+    import torch
+
+    from tt_symbiote_amd import hip_ops
+    from tt_symbiote_amd.generate import greedy_generate
+    from tt_symbiote_amd.modules.kv_cache import HIPPagedAttentionKVCache, PagedAttentionConfig
+    from tt_symbiote_amd.modules.model import HIPBailingMoeV2Model, HIPLMHead
+    from tt_symbiote_amd.utils.device_management import set_device
+    from tt_symbiote_amd.workloads import (LING_MINI_2, build_decoder_layer,
+                                           build_dense_decoder_layer, layer_weights,
+                                           model_config)
+
+    dev = torch.device("cuda:0")
+    shape = LING_MINI_2
+    mc = model_config()
+    B, L, n_new = mc["batch"], mc["prompt_len"], mc["new_tokens"]
+    V, H = mc["vocab_size"], shape.hidden_size
+    _log(f"building {mc['num_layers']} layers on the GPU ...")
+    layers = []
+    for i in range(mc["num_layers"]):
+        if i < mc["first_k_dense_replace"]:
+            layers.append(build_dense_decoder_layer(
+                shape, mc["dense_intermediate_size"], seed=args.seed + i, device=dev,
+                layer_idx=i))
+        else:
+            w = layer_weights(shape, seed=args.seed + i, device=dev)
+            layers.append(build_decoder_layer(w, shape, layer_idx=i))
+            del w
+        set_device(layers[-1], dev)
+        if not layers[-1].is_dense_layer:
+            layers[-1].mlp.keep_last_route = True
+    g = torch.Generator(device=dev).manual_seed(args.seed + 100)
+    embed = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    head_w = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+    norm_w = (1.0 + 0.02 * torch.randn(H, generator=g, device=dev)).to(torch.bfloat16)
+    trunk = HIPBailingMoeV2Model.from_modules(embed, layers, norm_w, shape.rms_norm_eps)
+    head = HIPLMHead.from_weight(head_w)
+    set_device(trunk, dev)
+    set_device(head, dev)
+    del embed, head_w
+    cfg = PagedAttentionConfig(block_size=mc["block_size"], max_num_blocks=mc["max_num_blocks"],
+                               batch_size=B)
+    cache = HIPPagedAttentionKVCache(mc["num_layers"], shape.num_kv_heads, shape.head_dim, cfg,
+                                     device=dev)
+    prompts = torch.randint(0, V, (B, L), generator=torch.Generator().manual_seed(args.seed + 7))
+    # warm-up: a short generation (fills the workspaces, loads the code objects)
+    _log("warm-up generation ...")
+    greedy_generate(trunk, head, prompts[:, :64], cache, 4)
+    cache.reset()
+    _log(f"greedy generation: batch {B}, prompts of {L}, {n_new} new tokens ...")
+    r = greedy_generate(trunk, head, prompts, cache, n_new)
+    decode_tps = B * r.decode_steps / r.decode_s
+    ms_step = r.decode_s / r.decode_steps * 1e3
+    # bytes of the last decode step (routing of every MoE layer's last step)
+    kv_tok = shape.num_kv_heads * shape.head_dim * 2 * 2
+    ctx_read = B * (L + n_new - 1)                      # slots read in the last step
+    step_bytes = V * H * 2 + B * H * 2                  # lm head + embedding rows
+    exp_bytes = 3 * shape.moe_intermediate_size * H * 2
+    n_active = []
+    for layer in layers:
+        step_bytes += shape.attention_weight_bytes() + ctx_read * kv_tok
+        if layer.is_dense_layer:
+            step_bytes += 3 * mc["dense_intermediate_size"] * H * 2
+        else:
+            na = int(layer.mlp.last_route.n_segments.item())
+            n_active.append(na - shape.num_shared_experts)
+            step_bytes += na * exp_bytes + shape.num_experts * H * 4
+    gbs = step_bytes / (ms_step * 1e-3) / 1e9
+    # the LM head kernel alone (HIP events on its stream), on the last step's hidden rows
+    timer = hip_ops.KernelTimer(["lm_head"])
+    hip_ops.set_kernel_timer(timer)
+    xh = torch.randn(B, H, device=dev).to(torch.bfloat16)
+    for _ in range(20):
+        head.greedy(xh)
+    torch.cuda.synchronize()
+    hip_ops.set_kernel_timer(None)
+    lm_ms = timer.mean_ms("lm_head")
+    lm_gbs = V * H * 2 / (lm_ms * 1e-3) / 1e9
+    _log(f"prefill {r.prefill_s * 1e3:.0f} ms ({B * L / r.prefill_s:.0f} tok/s) | decode "
+         f"{ms_step:.2f} ms/step, {decode_tps:.0f} tok/s, {gbs:.0f} GB/s | lm head "
+         f"{lm_ms * 1e3:.0f} us ({lm_gbs:.0f} GB/s) | active experts per MoE layer "
+         f"{min(n_active)}..{max(n_active)}")
+    result = {
+        "metric": "greedy generate decode tokens/sec @bs64 Ling-mini-2.0-shape full model "
+                  "(20 layers, vocab 157184), 1 GPU",
+        "value": decode_tps,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": r.decode_steps,
+        "warmup": 1,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: random-init bf16 weights (per-layer seeds), random prompt ids",
+        "config": {
+            "workload": f"greedy generation, {mc['num_layers']} layers (layer 0 dense I=5120, "
+                        f"19 MoE), vocab {V}, batch {B} prompts of {L} random ids, {n_new} new "
+                        "tokens, paged KV block 32 / 8192 blocks, decode step captured as one "
+                        "HIP graph",
+            "global_batch": B,
+            "prefill_ms": r.prefill_s * 1e3,
+            "prefill_tokens_per_s": B * L / r.prefill_s,
+            "end_to_end_tokens_per_s": B * n_new / (r.prefill_s + r.decode_s),
+            "active_experts_last_step": n_active,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "lm_head_partial_kernel (LM head GEMV + argmax)",
+            "achieved": lm_gbs,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": lm_gbs / HBM_PEAK_GBS,
+            "traffic": None,
+            "bytes_per_launch": V * H * 2,
+            "avg_launch_us": lm_ms * 1e3,
+        },
+        "step_roofline": {"bytes_per_step": step_bytes, "achieved": gbs, "peak": HBM_PEAK_GBS,
+                          "unit": "GB/s", "frac": gbs / HBM_PEAK_GBS},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(result), flush=True)
+
+
 def main():
     args = parse_args()
     if args.copy_calibration:
@@ -272,6 +403,9 @@ def main():
         sys.exit(2)
     if args.workload == "prefill":
         prefill_main(args)
+        return
+    if args.workload == "generate":
+        generate_main(args)
         return
     decode_main(args, fp8=args.workload == "fp8")
 

@@ -352,6 +352,28 @@ int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows, const int32
                        void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Model ends of greedy generation (the embedding and final-norm swap of TTNNBailingMoeV2Model,
+ * modeling_bailing_moe_v2.py:56-95 / 97-334; the lm_head linear; HF generate's greedy argmax,
+ * taken on the device instead of the host).
+ * sym_embedding_bf16: out[t] = table[ids[t]] ([T, H] rows of a [V, H] bf16 table); an id outside
+ *   [0, V) gives a zero row. Also gathers rows of any [V, H] bf16 matrix (e.g. the last hidden
+ *   row of each packed prompt). H % 8 == 0.
+ * sym_lm_head_greedy: ids[b] = argmax_v x[b] . w[v] (x [B, H] bf16, already normalised; w [V, H]
+ *   bf16; fp32 logits, never written; ties -> the lowest v). Workspace: the bytes
+ *   sym_lm_head_greedy_workspace_bytes(B, V) returns. H % 256 == 0.
+ * sym_greedy_advance: positions[b] += 1, then (history non-null) history[b][positions[b] -
+ *   hist_base[b]] = ids[b] when that column lies in [0, hist_cols) -- the per-step bookkeeping of
+ *   a captured decode step (positions and generated tokens stay on the device).
+ */
+int sym_embedding_bf16(const int32_t* ids, const void* table, int T, int H, int V, void* out,
+                       void* stream);
+size_t sym_lm_head_greedy_workspace_bytes(int B, int V);
+int sym_lm_head_greedy(const void* x, const void* w, int B, int H, int V, void* workspace,
+                       size_t workspace_bytes, int32_t* ids, void* stream);
+int sym_greedy_advance(const int32_t* ids, int B, int32_t* positions, int32_t* history,
+                       const int32_t* hist_base, int hist_cols, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Unpermute + weighted combine (+ shared expert, + residual).
  * Replaces all_to_all_combine + mul + sum(dim=0) (ttnn_moe.py:1307-1335), the shared-expert
  * add (ttnn_moe.py:1487-1490) and the decoder layer's residual add

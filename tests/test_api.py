@@ -40,6 +40,7 @@ def test_build_module_dict_is_flat_class_map():
     assert mapping[BailingMoeV2DecoderLayer] is ts.HIPBailingMoEDecoderLayer
     assert mapping[BailingMoeV2Attention] is ts.HIPBailingMoEAttention
     assert mapping[BailingMoeV2SparseMoeBlock] is ts.HIPBailingMoE
+    assert mapping[type(model.model)] is ts.HIPBailingMoeV2Model
     for k, v in mapping.items():
         assert isinstance(k, type) and isinstance(v, type)
 
@@ -47,7 +48,12 @@ def test_build_module_dict_is_flat_class_map():
 def test_apply_recipe_swaps_layers_and_keeps_fallback():
     model = _tiny_model(layers=2)
     swapped = ts.apply_recipe(model, kv_cache_kwargs={"block_size": 32, "max_num_blocks": 8})
-    assert set(swapped) == {"model.layers.0", "model.layers.1"}
+    # the trunk is swapped as a whole (its from_torch converts the layers); the lm_head by
+    # post_register
+    assert set(swapped) == {"model"}
+    assert isinstance(model.model, ts.HIPBailingMoeV2Model)
+    assert isinstance(model.lm_head, ts.HIPLMHead) and model.lm_head.vocab_size == 100
+    assert type(model.model.torch_layer).__name__ == "BailingMoeV2Model"
     l0, l1 = model.model.layers[0], model.model.layers[1]
     assert isinstance(l0, ts.HIPBailingMoEDecoderLayer) and l0.is_dense_layer
     assert isinstance(l1.mlp, ts.HIPBailingMoE) and not l1.is_dense_layer

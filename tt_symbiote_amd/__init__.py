@@ -2,7 +2,7 @@
 module-replacement API.
 
     import tt_symbiote_amd as ts
-    ts.apply_recipe(model)              # swap the HF decoder layers / attention / MoE blocks
+    ts.apply_recipe(model)              # swap the HF trunk, decoder layers, attention, MoE, lm_head
     ts.set_device(model, "cuda:0")      # bind to the GPU, move weights, allocate the paged cache
     cache = model._tt_kv_cache          # pass back as past_key_values
 
@@ -14,7 +14,8 @@ from . import recipe_bailing_moe_v2  # noqa: F401  -- registers the recipe
 from .core.module import (HIPModule, StatefulHIPModule, StatefulTTNNModule, StatelessHIPModule,
                           StatelessTTNNModule, TTNNModule)
 from .modules import (HIPBailingMoE, HIPBailingMoEAttention, HIPBailingMoEDecoderLayer,
-                      HIPBailingMoeV2MLP, HIPPagedAttentionKVCache, PagedAttentionConfig)
+                      HIPBailingMoeV2MLP, HIPBailingMoeV2Model, HIPLMHead,
+                      HIPPagedAttentionKVCache, PagedAttentionConfig)
 from .registry import TT_MODEL_REGISTRY, register_recipe
 from .utils import compatibility
 from .utils.device_management import set_device
@@ -39,4 +40,5 @@ __all__ = ["apply_recipe", "set_device", "register_modules", "register_recipe",
            "TT_MODEL_REGISTRY", "compatibility", "HIPModule", "StatelessHIPModule",
            "StatefulHIPModule", "TTNNModule", "StatelessTTNNModule", "StatefulTTNNModule",
            "HIPBailingMoE", "HIPBailingMoEAttention", "HIPBailingMoEDecoderLayer",
-           "HIPBailingMoeV2MLP", "HIPPagedAttentionKVCache", "PagedAttentionConfig"]
+           "HIPBailingMoeV2MLP", "HIPBailingMoeV2Model", "HIPLMHead",
+           "HIPPagedAttentionKVCache", "PagedAttentionConfig"]

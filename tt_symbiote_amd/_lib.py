@@ -67,6 +67,12 @@ _SIGNATURES = {
          _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_float, _vp,
          _c_size, _vp, _vp],
     ),
+    "sym_embedding_bf16": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "sym_lm_head_greedy_workspace_bytes": (_c_size, [_c_int, _c_int]),
+    "sym_lm_head_greedy": (
+        _c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _c_size, _vp, _vp]
+    ),
+    "sym_greedy_advance": (_c_int, [_vp, _c_int, _vp, _vp, _vp, _c_int, _vp]),
     "sym_linear_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]),
     "sym_rmsnorm_linear_bf16": (
         _c_int, [_vp, _vp, _c_float, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]

@@ -160,9 +160,10 @@ class HIPModule:
                     if isinstance(v, (torch.nn.Module, HIPModule)):
                         yield f"{name}[{k}]", v
             elif isinstance(child, (list, tuple)):
+                # list members are named like nn.ModuleList children: "layers.0", "layers.1", ...
                 for i, v in enumerate(child):
                     if isinstance(v, (torch.nn.Module, HIPModule)):
-                        yield f"{name}[{i}]", v
+                        yield f"{name}.{i}", v
 
     def children(self):
         for _, c in self.named_children():

@@ -565,6 +565,72 @@ def paged_kv_fill_fp8(k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor
 
 
 # -------------------------------------------------------------------------------------------
+def embedding(ids: torch.Tensor, table: torch.Tensor,
+              out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """out[t] = table[ids[t]] for ids [T] int32 and a [V, H] bf16 table (ids outside [0, V)
+    give zero rows)."""
+    _check(table, "table", torch.bfloat16)
+    if table.dim() != 2:
+        raise ValueError(f"table must be [V, H], got {tuple(table.shape)}")
+    V, H = table.shape
+    _check(ids, "ids", torch.int32, table.device)
+    T = ids.numel()
+    if out is None:
+        out = torch.empty(T, H, dtype=torch.bfloat16, device=table.device)
+    _check(out, "out", torch.bfloat16, table.device)
+    _check_shape(out, "out", (T, H))
+    _lib.call("sym_embedding_bf16", _ptr(ids), _ptr(table), T, H, V, _ptr(out), _stream())
+    return out
+
+
+def lm_head_greedy(x: torch.Tensor, w: torch.Tensor, ids: Optional[torch.Tensor] = None,
+                   workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """ids[b] = argmax_v x[b] . w[v] (x [B, H] bf16, w [V, H] bf16, fp32 logits; ties go to the
+    lowest index) -> [B] int32."""
+    _check(x, "x", torch.bfloat16)
+    _check(w, "w", torch.bfloat16, x.device)
+    B, H = x.shape
+    V = w.shape[0]
+    _check_shape(w, "w", (V, H))
+    if ids is None:
+        ids = torch.empty(B, dtype=torch.int32, device=x.device)
+    _check(ids, "ids", torch.int32, x.device)
+    _check_shape(ids, "ids", (B,))
+    need = _lib.query("sym_lm_head_greedy_workspace_bytes", B, V)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+    _check(workspace, "workspace", torch.uint8, x.device)
+    _timed("lm_head", lambda: _lib.call(
+        "sym_lm_head_greedy", _ptr(x), _ptr(w), B, H, V, _ptr(workspace), workspace.numel(),
+        _ptr(ids), _stream()))
+    return ids
+
+
+def lm_head_greedy_workspace_bytes(batch: int, vocab: int) -> int:
+    return _lib.query("sym_lm_head_greedy_workspace_bytes", batch, vocab)
+
+
+def greedy_advance(ids: torch.Tensor, positions: torch.Tensor,
+                   history: Optional[torch.Tensor] = None,
+                   hist_base: Optional[torch.Tensor] = None) -> None:
+    """positions += 1; history[b, positions[b] - hist_base[b]] = ids[b] (inside the row)."""
+    _check(ids, "ids", torch.int32)
+    B = ids.numel()
+    _check(positions, "positions", torch.int32, ids.device)
+    _check_shape(positions, "positions", (B,))
+    cols = 0
+    if history is not None:
+        _check(history, "history", torch.int32, ids.device)
+        if history.dim() != 2 or history.shape[0] != B:
+            raise ValueError(f"history must be [{B}, n], got {tuple(history.shape)}")
+        cols = history.shape[1]
+        _check(hist_base, "hist_base", torch.int32, ids.device)
+        _check_shape(hist_base, "hist_base", (B,))
+    _lib.call("sym_greedy_advance", _ptr(ids), B, _ptr(positions), _ptr(history),
+              _ptr(hist_base), cols, _stream())
+
+
+# -------------------------------------------------------------------------------------------
 @dataclass
 class RouteResult:
     """Outputs of :func:`moe_route_permute` (all on the device)."""

@@ -207,10 +207,16 @@ class HIPBailingMoeV2MLP(StatelessHIPModule):
 
     @classmethod
     def from_torch(cls, torch_mlp):
-        new = cls()
-        new._host = dict(gate=torch_mlp.gate_proj.weight, up=torch_mlp.up_proj.weight,
-                         down=torch_mlp.down_proj.weight)
+        new = cls.from_weights(torch_mlp.gate_proj.weight, torch_mlp.up_proj.weight,
+                               torch_mlp.down_proj.weight)
         new._fallback_torch_layer = torch_mlp
+        return new
+
+    @classmethod
+    def from_weights(cls, gate_weight, up_weight, down_weight):
+        """gate / up [I, H], down [H, I] (HF nn.Linear layouts)."""
+        new = cls()
+        new._host = dict(gate=gate_weight, up=up_weight, down=down_weight)
         return new
 
     def preprocess_weights_impl(self):

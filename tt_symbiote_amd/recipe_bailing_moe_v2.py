@@ -8,12 +8,19 @@ without the layer wrapper -- the attention and sparse-MoE classes themselves. Th
 are remote code, so they are matched by class name on the model instance.
 ``make_kv_cache(model, device, batch_size=1, **kwargs)`` allocates the paged cache
 (``block_size`` default 64, ``max_num_blocks`` default 32, as the reference).
+
+As the reference's ``{type(model.model): TTNNBailingMoeV2Model, ...}`` (modeling_bailing_moe_v2.py
+:715-719), the HF trunk (``BailingMoeV2Model``) is swapped for :class:`HIPBailingMoeV2Model`
+(embedding, decoder layers, final norm), and ``post_register`` swaps ``model.lm_head`` for
+:class:`HIPLMHead` (the reference maps ``nn.Linear`` to a TTNN linear), so
+:func:`tt_symbiote_amd.generate.greedy_generate` runs the whole model on the device.
 """
 from __future__ import annotations
 
 from .modules.attention import HIPBailingMoEAttention
 from .modules.decoder_layer import HIPBailingMoEDecoderLayer
 from .modules.kv_cache import HIPPagedAttentionKVCache, PagedAttentionConfig
+from .modules.model import HIPBailingMoeV2Model, HIPLMHead
 from .modules.moe import HIPBailingMoE
 from .registry import register_recipe
 
@@ -21,16 +28,18 @@ _LAYER_CLASSES = {"BailingMoeV2DecoderLayer"}
 _ATTENTION_CLASSES = {"BailingMoeV2Attention", "BailingMoeV2SdpaAttention",
                       "BailingMoeV2FlashAttention2"}
 _MOE_CLASSES = {"BailingMoeV2SparseMoeBlock"}
+_MODEL_CLASSES = {"BailingMoeV2Model"}
 
 
 @register_recipe(hf_class_name="BailingMoeV2ForCausalLM")
 class BailingMoEV2Recipe:
     # design-time coverage lists (modeling_bailing_moe_v2.py:656-705), for this hot path
-    tt_implemented = ["BailingMoeV2DecoderLayer", "BailingMoeV2SdpaAttention",
-                      "BailingMoeV2Attention", "BailingMoeV2SparseMoeBlock",
-                      "BailingMoeV2Gate", "BailingMoeV2MLP", "BailingMoeV2RMSNorm"]
+    tt_implemented = ["BailingMoeV2Model", "BailingMoeV2DecoderLayer",
+                      "BailingMoeV2SdpaAttention", "BailingMoeV2Attention",
+                      "BailingMoeV2SparseMoeBlock", "BailingMoeV2Gate", "BailingMoeV2MLP",
+                      "BailingMoeV2RMSNorm", "Linear"]
     cpu_fallback: list = []
-    host_glue = ["BailingMoeV2PreTrainedModel", "BailingMoeV2ForCausalLM", "BailingMoeV2Model",
+    host_glue = ["BailingMoeV2PreTrainedModel", "BailingMoeV2ForCausalLM",
                  "BailingMoeV2RotaryEmbedding"]
     out_of_scope = ["BailingMoeV2FlashAttention2", "BailingMoeV2MTPLayer"]
 
@@ -39,7 +48,9 @@ class BailingMoEV2Recipe:
         modules = model.modules() if hasattr(model, "modules") else []
         for m in modules:
             name = type(m).__name__
-            if name in _LAYER_CLASSES:
+            if name in _MODEL_CLASSES:
+                mapping[type(m)] = HIPBailingMoeV2Model
+            elif name in _LAYER_CLASSES:
                 mapping[type(m)] = HIPBailingMoEDecoderLayer
             elif name in _ATTENTION_CLASSES:
                 mapping[type(m)] = HIPBailingMoEAttention
@@ -48,6 +59,12 @@ class BailingMoEV2Recipe:
         return mapping
 
     def post_register(self, model):
+        children = getattr(model, "_modules", {})
+        head = children.get("lm_head")
+        if head is not None and type(head).__name__ == "Linear":
+            new = HIPLMHead.from_torch(head)
+            new._unique_name = "lm_head"
+            children["lm_head"] = new      # spliced in as register_modules does
         return None
 
     def make_kv_cache(self, model, device, batch_size: int = 1, **kwargs):

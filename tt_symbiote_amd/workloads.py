@@ -14,6 +14,7 @@ Both the benchmark and the tests draw their inputs here, so the same seed gives 
 """
 from __future__ import annotations
 
+import dataclasses
 import math
 from dataclasses import dataclass
 from typing import Dict, Optional
@@ -240,3 +241,45 @@ def build_decoder_layer(w: Dict[str, torch.Tensor], shape: LayerShape = LING_MIN
         weight_format=weight_format)
     return HIPBailingMoEDecoderLayer.from_modules(attn, moe, w["ln1"], w["ln2"],
                                                   eps=shape.rms_norm_eps)
+
+
+def build_dense_decoder_layer(shape: LayerShape = LING_MINI_2, intermediate_size: int = 5120,
+                              seed: int = 0, device="cpu", layer_idx: int = 0,
+                              std: float = 0.02):
+    """HIP decoder layer with the dense SwiGLU MLP (the layers before first_k_dense_replace),
+    random-init like :func:`layer_weights`."""
+    from .modules.attention import HIPBailingMoEAttention
+    from .modules.decoder_layer import HIPBailingMoEDecoderLayer
+    from .modules.moe import HIPBailingMoeV2MLP
+
+    w = layer_weights(dataclasses.replace(shape, num_experts=8, moe_intermediate_size=128,
+                                          num_shared_experts=0), seed=seed, device=device,
+                      std=std)
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed + 1000)
+    H = shape.hidden_size
+    gate = _randn(g, (intermediate_size, H), dev, std).to(torch.bfloat16)
+    up = _randn(g, (intermediate_size, H), dev, std).to(torch.bfloat16)
+    down = _randn(g, (H, intermediate_size), dev, std).to(torch.bfloat16)
+    attn = HIPBailingMoEAttention.from_weights(
+        num_heads=shape.num_heads, num_kv_heads=shape.num_kv_heads, head_dim=shape.head_dim,
+        hidden_size=H, qkv_weight=w["qkv_w"], dense_weight=w["dense_w"],
+        q_norm_weight=w["q_norm"] if shape.use_qk_norm else None,
+        k_norm_weight=w["k_norm"] if shape.use_qk_norm else None,
+        partial_rotary_factor=shape.partial_rotary_factor, rope_theta=shape.rope_theta,
+        max_position_embeddings=shape.max_position_embeddings, norm_eps=shape.rms_norm_eps,
+        layer_idx=layer_idx)
+    mlp = HIPBailingMoeV2MLP.from_weights(gate, up, down)
+    return HIPBailingMoEDecoderLayer.from_modules(attn, mlp, w["ln1"], w["ln2"],
+                                                  eps=shape.rms_norm_eps)
+
+
+def model_config(num_layers: int = 20, vocab_size: int = 157184,
+                 first_k_dense_replace: int = 1, dense_intermediate_size: int = 5120) -> dict:
+    """The whole-model greedy workload: Ling-mini-2.0 shape (20 layers, layer 0 dense with
+    intermediate 5120, 19 MoE layers), vocab 157184, batch 64 prompts of 2048 random ids, 128
+    greedy tokens, paged KV with block size 32 and 8192 blocks."""
+    return dict(num_layers=num_layers, vocab_size=vocab_size,
+                first_k_dense_replace=first_k_dense_replace,
+                dense_intermediate_size=dense_intermediate_size, batch=64, prompt_len=2048,
+                new_tokens=128, block_size=32, max_num_blocks=8192)
