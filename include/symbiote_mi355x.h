@@ -360,7 +360,7 @@ int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows, const int32
  *   row of each packed prompt). H % 8 == 0.
  * sym_lm_head_greedy: ids[b] = argmax_v x[b] . w[v] (x [B, H] bf16, already normalised; w [V, H]
  *   bf16; fp32 logits, never written; ties -> the lowest v). Workspace: the bytes
- *   sym_lm_head_greedy_workspace_bytes(B, V) returns. H % 256 == 0.
+ *   sym_lm_head_greedy_workspace_bytes(B, V) returns. H % 256 == 0 (token rows are staged 256 columns at a time).
  * sym_greedy_advance: positions[b] += 1, then (history non-null) history[b][positions[b] -
  *   hist_base[b]] = ids[b] when that column lies in [0, hist_cols) -- the per-step bookkeeping of
  *   a captured decode step (positions and generated tokens stay on the device).

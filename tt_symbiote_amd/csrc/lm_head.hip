@@ -7,19 +7,24 @@
 // (greedy). Here the argmax runs on the device and only token ids leave it.
 //
 // LM head design (gfx950): at decode the head is a skinny GEMM that streams the [V, H] weight
-// once (157184 x 2048 bf16 = 644 MB for Ling-mini-2.0). A workgroup of 4 waves owns 64 vocab
+// once (157184 x 2048 bf16 = 644 MB for Ling-mini-2.0). A workgroup of 8 waves owns 128 vocab
 // rows; each wave streams 16 rows over all of H (lane l: 32 contiguous bytes of row l % 16 per
-// 64-wide K step, the B operand of v_mfma_f32_16x16x32_bf16) against up to 64 token rows (four
-// 16-row A tiles read from L2), so the logits never go to memory: the wave reduces its 16
-// columns to (max, lowest index) per token row with lane shuffles, the workgroup reduces its 4
-// waves through LDS and writes one partial per (workgroup, row); a second kernel reduces the
-// partials of a row. Ties resolve to the lowest vocab index (torch.argmax's rule).
+// 64-wide K step, the B operand of v_mfma_f32_16x16x32_bf16). The token rows (up to 64 per
+// pass, the A operand) are staged in LDS 256 columns at a time, once per workgroup, while the
+// chunk's weight loads are in flight, so the 8 waves share one read of them. The logits never
+// go to memory: the wave reduces its 16 columns to (max, lowest index) per token row with lane
+// shuffles, the workgroup reduces its 8 waves through LDS and writes one partial per
+// (workgroup, row); a second kernel reduces the partials of a row. Ties resolve to the lowest
+// vocab index (torch.argmax's rule).
 #include "common.h"
 
 namespace sym {
 
-constexpr int kLmWaves = 4;
-constexpr int kLmRowsPerWG = kLmWaves * 16;
+constexpr int kLmWaves = 8;
+constexpr int kLmThreads = kLmWaves * 64;
+constexpr int kLmRowsPerWG = kLmWaves * 16;  // vocab rows per workgroup
+constexpr int kLmKC = 256;                   // K chunk of the token rows staged in LDS
+constexpr int kLmXStride = kLmKC + 8;        // LDS row stride (528 B: conflict-free b128 reads)
 
 __global__ __launch_bounds__(256) void embedding_gather_kernel(
     const int32_t* __restrict__ ids, const uint16_t* __restrict__ table, int H, int V,
@@ -40,52 +45,58 @@ __device__ __forceinline__ void arg_better(float& v, int& i, float v2, int i2) {
   }
 }
 
-template <int MT, int U>
-__global__ __launch_bounds__(256) void lm_head_partial_kernel(
+template <int MT>
+__global__ __launch_bounds__(kLmThreads) void lm_head_partial_kernel(
     const uint16_t* __restrict__ x, int B, int H, const uint16_t* __restrict__ w, int V,
     float* __restrict__ part_val, int* __restrict__ part_idx) {
+  __shared__ __align__(16) uint16_t s_x[2 * 16 * MT * kLmXStride];
   __shared__ float s_val[kLmWaves][16 * MT];
   __shared__ int s_idx[kLmWaves][16 * MT];
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
-  const int v0 = blockIdx.x * kLmRowsPerWG + wave * 16;
-  const int vcol = v0 + r16;                 // this lane's vocab column
+  const int vcol = blockIdx.x * kLmRowsPerWG + wave * 16 + r16;   // this lane's vocab column
   const uint16_t* wr = w + (size_t)min(vcol, V - 1) * H + kq * 16;
-  const int nsteps = H >> 6;
+  constexpr int kXLoads = 16 * MT * (kLmKC / 8) / kLmThreads;      // 16-byte pieces per thread
   for (int mb = 0; mb < B; mb += 16 * MT) {
-    const uint16_t* xr[MT];
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      xr[mt] = x + (size_t)min(mb + mt * 16 + r16, B - 1) * H + kq * 16;
     floatx4 acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int st = 0; st < nsteps; st += U) {
-      uint4 b[U][2], a[MT][U][2];
+    for (int kc = 0; kc < H; kc += kLmKC) {
+      // this chunk's weights first (in flight while the token rows are staged)
+      uint4 b[kLmKC / 64][2];
 #pragma unroll
-      for (int s = 0; s < U; ++s) {
-        const int k = (st + s) << 6;
-        b[s][0] = *reinterpret_cast<const uint4*>(wr + k);
-        b[s][1] = *reinterpret_cast<const uint4*>(wr + k + 8);
+      for (int s = 0; s < kLmKC / 64; ++s) {
+        b[s][0] = *reinterpret_cast<const uint4*>(wr + kc + s * 64);
+        b[s][1] = *reinterpret_cast<const uint4*>(wr + kc + s * 64 + 8);
       }
-      __builtin_amdgcn_sched_barrier(0);
+      // stage the chunk of token rows into the LDS buffer of this chunk's parity (last read
+      // two chunks ago, before the previous chunk's barrier)
+      uint16_t* sx = s_x + ((kc / kLmKC) & 1) * (16 * MT * kLmXStride);
+      const int c8 = (tid % (kLmKC / 8)) * 8;
+      uint4 xv[kXLoads];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int j = 0; j < kXLoads; ++j) {
+        const int row = tid / (kLmKC / 8) + j * (kLmThreads / (kLmKC / 8));
+        xv[j] = *reinterpret_cast<const uint4*>(x + (size_t)min(mb + row, B - 1) * H + kc + c8);
+      }
 #pragma unroll
-        for (int s = 0; s < U; ++s) {
-          const int k = (st + s) << 6;
-          a[mt][s][0] = *reinterpret_cast<const uint4*>(xr[mt] + k);
-          a[mt][s][1] = *reinterpret_cast<const uint4*>(xr[mt] + k + 8);
-        }
-      __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < kXLoads; ++j) {
+        const int row = tid / (kLmKC / 8) + j * (kLmThreads / (kLmKC / 8));
+        *reinterpret_cast<uint4*>(&sx[row * kLmXStride + c8]) = xv[j];
+      }
+      __syncthreads();
 #pragma unroll
-      for (int s = 0; s < U; ++s)
+      for (int s = 0; s < kLmKC / 64; ++s)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          acc[mt] = mfma16x16x32(a[mt][s][0], b[s][0], acc[mt]);
-          acc[mt] = mfma16x16x32(a[mt][s][1], b[s][1], acc[mt]);
+          const uint16_t* ar = &sx[(mt * 16 + r16) * kLmXStride + s * 64 + kq * 16];
+          const uint4 a0 = *reinterpret_cast<const uint4*>(ar);
+          const uint4 a1 = *reinterpret_cast<const uint4*>(ar + 8);
+          acc[mt] = mfma16x16x32(a0, b[s][0], acc[mt]);
+          acc[mt] = mfma16x16x32(a1, b[s][1], acc[mt]);
         }
     }
     // lane holds logits of token rows 4*kq + i (tile mt), vocab column vcol: reduce the
@@ -108,19 +119,17 @@ __global__ __launch_bounds__(256) void lm_head_partial_kernel(
         }
       }
     __syncthreads();
-    if (threadIdx.x < 16 * MT) {
-      const int row = mb + threadIdx.x;
-      float bv = s_val[0][threadIdx.x];
-      int bi = s_idx[0][threadIdx.x];
+    if (tid < 16 * MT) {
+      const int row = mb + tid;
+      float bv = s_val[0][tid];
+      int bi = s_idx[0][tid];
 #pragma unroll
-      for (int wv = 1; wv < kLmWaves; ++wv)
-        arg_better(bv, bi, s_val[wv][threadIdx.x], s_idx[wv][threadIdx.x]);
+      for (int wv = 1; wv < kLmWaves; ++wv) arg_better(bv, bi, s_val[wv][tid], s_idx[wv][tid]);
       if (row < B) {
         part_val[(size_t)blockIdx.x * B + row] = bv;
         part_idx[(size_t)blockIdx.x * B + row] = bi;
       }
     }
-    __syncthreads();
   }
 }
 
@@ -199,8 +208,8 @@ extern "C" int sym_lm_head_greedy(const void* x, const void* w, int B, int H, in
               V);
   if (B == 0) return SYM_OK;
   SYM_REQUIRE(x && w && workspace && ids, SYM_ERR_INVALID, "lm_head_greedy: null pointer");
-  SYM_REQUIRE(H % 256 == 0, SYM_ERR_UNSUPPORTED,
-              "lm_head_greedy: H=%d must be a multiple of 256", H);
+  SYM_REQUIRE(H % kLmKC == 0, SYM_ERR_UNSUPPORTED,
+              "lm_head_greedy: H=%d must be a multiple of %d", H, kLmKC);
   const size_t need = sym_lm_head_greedy_workspace_bytes(B, V);
   SYM_REQUIRE(workspace_bytes >= need, SYM_ERR_WORKSPACE,
               "lm_head_greedy: workspace %zu < required %zu", workspace_bytes, need);
@@ -209,15 +218,14 @@ extern "C" int sym_lm_head_greedy(const void* x, const void* w, int B, int H, in
   int* pi = (int*)(pv + (size_t)parts * B);
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
-  const int nsteps = H / 64;
-  if (B <= 16 && nsteps % 8 == 0)
-    hipLaunchKernelGGL((lm_head_partial_kernel<1, 8>), dim3(parts), dim3(256), 0, s,
+  if (B <= 16)
+    hipLaunchKernelGGL((lm_head_partial_kernel<1>), dim3(parts), dim3(kLmThreads), 0, s,
                        (const uint16_t*)x, B, H, (const uint16_t*)w, V, pv, pi);
-  else if (B <= 32 && nsteps % 4 == 0)
-    hipLaunchKernelGGL((lm_head_partial_kernel<2, 4>), dim3(parts), dim3(256), 0, s,
+  else if (B <= 32)
+    hipLaunchKernelGGL((lm_head_partial_kernel<2>), dim3(parts), dim3(kLmThreads), 0, s,
                        (const uint16_t*)x, B, H, (const uint16_t*)w, V, pv, pi);
   else
-    hipLaunchKernelGGL((lm_head_partial_kernel<4, 4>), dim3(parts), dim3(256), 0, s,
+    hipLaunchKernelGGL((lm_head_partial_kernel<4>), dim3(parts), dim3(kLmThreads), 0, s,
                        (const uint16_t*)x, B, H, (const uint16_t*)w, V, pv, pi);
   int rc = sym_host::check_launch("lm_head_partial_kernel");
   if (rc) return rc;
