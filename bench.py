@@ -27,6 +27,7 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "decode tokens/sec @bs32 Ling-mini-2.0-shape, 1 GPU; % HBM roofline/layer"
+STEPS_PER_GRAPH = 10
 HBM_PEAK_GBS = 8000.0
 
 
@@ -50,6 +51,10 @@ def parse_args():
                          "packed prompts of U[256, 2048] tokens through the same layer; fp8: "
                          "the batch-128 decode step with fp8 experts and an fp8 KV cache; "
                          "generate: greedy generation with the whole 20-layer model")
+    ap.add_argument("--replays-only", action="store_true",
+                    help="decode workloads: stop after the timed graph replays (no per-kernel "
+                         "eager pass, no bandwidth probe, no JSON), so a kernel trace ends with "
+                         "the replayed steps")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain copy kernel (torch.neg, bf16) over 512 MiB three "
                          "times: the reference point that scales the FETCH_SIZE / WRITE_SIZE "
@@ -463,12 +468,17 @@ def decode_main(args, fp8: bool) -> None:
 
     run = step
     graph = None
+    per_run = 1
     if not args.eager:
-        # capture one decode step (all of its launches, host logic included) as a HIP graph;
-        # positions, page table and workspaces are device buffers, so a replay is a full step
+        # capture decode steps (all of their launches, host logic included) as one HIP graph;
+        # positions, page table and workspaces are device buffers, so a replay is full steps.
+        # Several steps per graph, as the whole model puts its 20 layer steps in one graph:
+        # the graph launch gap (about 8 us) is then not charged to every layer step.
+        per_run = STEPS_PER_GRAPH if args.steps % STEPS_PER_GRAPH == 0 else 1
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            step()
+            for _ in range(per_run):
+                step()
         torch.cuda.synchronize()
         run = graph.replay
         for _ in range(3):
@@ -476,16 +486,20 @@ def decode_main(args, fp8: bool) -> None:
         torch.cuda.synchronize()
 
     # timed region: K steps
-    _log(f"timing {args.steps} steps ({'eager' if args.eager else 'graph replay'}) ...")
+    _log(f"timing {args.steps} steps ({'eager' if args.eager else 'graph replay'}, "
+         f"{per_run} per launch) ...")
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record()
-    for _ in range(args.steps):
+    for _ in range(args.steps // per_run):
         run()
     t_end.record()
     torch.cuda.synchronize()
     ms_per_step = t_start.elapsed_time(t_end) / args.steps
+    if args.replays_only:
+        _log(f"{ms_per_step * 1e3:.1f} us per step")
+        return
 
     # per-kernel pass: the same steps launched eagerly with HIP events around the dominant
     # kernels (on the stream they are launched on)
@@ -537,7 +551,7 @@ def decode_main(args, fp8: bool) -> None:
             "global_batch": B,
             "context_tokens": int(ctx.context_lens.sum()),
             "active_experts": n_active,
-            "launch": "eager" if args.eager else "hip_graph",
+            "launch": "eager" if args.eager else f"hip_graph ({per_run} steps per graph)",
         },
         "roofline": {
             "bound": "hbm",

@@ -208,6 +208,29 @@ def test_paged_decode_fp8(device, B, Hq, Hkv, bs, lo, hi):
     _close(out, ref, atol=1e-2, rtol=1e-2)
 
 
+def test_paged_decode_fp8_split_boundaries(device):
+    """Contexts on either side of the 512-token split of the fp8 kernel (and of its 16-token
+    tiles and 128-token waves)."""
+    lens = [0, 1, 15, 16, 127, 128, 255, 256, 511, 512, 513, 1023, 1024, 1535]
+    B, Hq, Hkv, bs = len(lens), 8, 2, 32
+    nblk = [(L + 1 + bs - 1) // bs for L in lens]
+    nb = sum(nblk) + 7
+    perm = torch.randperm(nb, generator=torch.Generator().manual_seed(9))
+    table = torch.zeros(B, max(nblk), dtype=torch.int32)
+    o = 0
+    for i, n in enumerate(nblk):
+        table[i, :n] = perm[o:o + n].to(torch.int32)
+        o += n
+    pos = torch.tensor(lens, dtype=torch.int32)
+    kp, vp, ks, vs, codes, scales = _random_fp8_cache(nb, Hkv, bs, 21, device)
+    q = torch.randn(B, Hq, 128, generator=torch.Generator().manual_seed(3)).bfloat16()
+    out = hip_ops.paged_gqa_decode(q.to(device), kp, vp, table.to(device), pos.to(device), 0.1,
+                                   k_scale=ks, v_scale=vs)
+    ref = paged_decode_ref(q.float(), _deq_pool(codes[0], scales[0]),
+                           _deq_pool(codes[1], scales[1]), table, pos, 0.1)
+    _close(out, ref, atol=1e-2, rtol=1e-2)
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,rd,use_norm,lo,hi,bs,cap", [
     (8, 16, 4, 64, True, 5, 3000, 32, None),
     (5, 16, 2, 128, False, 0, 300, 16, None),

@@ -167,6 +167,8 @@ def test_router_logits(device, T, H, E):
     (32, 2048, 2048, True, torch.bfloat16),
     (1, 256, 512, False, torch.float32),
     (70, 128, 192, True, torch.float32),
+    (64, 2048, 2048, False, torch.float32),      # one 64-row pass
+    (100, 512, 1024, True, torch.bfloat16),
 ])
 def test_linear(device, M, N, K, bias, out_dtype):
     g = torch.Generator().manual_seed(M + N + K)
@@ -189,7 +191,8 @@ def _rmsnorm_bf16(x, gamma, eps):
     return (xf * r * gamma.float()).bfloat16()
 
 
-@pytest.mark.parametrize("M,N,K,bias", [(32, 3072, 2048, False), (1, 256, 2048, True),
+@pytest.mark.parametrize("M,N,K,bias", [(32, 3072, 2048, False), (64, 3072, 2048, False),
+                                        (48, 512, 1024, True), (1, 256, 2048, True),
                                         (70, 128, 192, True)])
 def test_rmsnorm_linear(device, M, N, K, bias):
     g = torch.Generator().manual_seed(M * 3 + N + K)
@@ -209,7 +212,8 @@ def test_rmsnorm_linear(device, M, N, K, bias):
     _close(out_bf, ref, atol=3e-3, rtol=8e-3)
 
 
-@pytest.mark.parametrize("M,N,K", [(32, 2048, 2048), (5, 256, 512), (40, 128, 192)])
+@pytest.mark.parametrize("M,N,K", [(32, 2048, 2048), (64, 2048, 2048), (5, 256, 512),
+                                   (40, 128, 192)])
 def test_linear_residual(device, M, N, K):
     g = torch.Generator().manual_seed(M + 7 * N + K)
     x = torch.randn(M, K, generator=g).bfloat16()

@@ -152,7 +152,10 @@ _lib = None
 
 
 def library_path() -> str:
-    return LIB_PATH
+    """The library this process loads: ``$SYMBIOTE_MI355X_LIB`` when set (e.g. a build with
+    other tuning parameters, see ``python -m tt_symbiote_amd.build --help``), else the in-tree
+    build."""
+    return os.environ.get("SYMBIOTE_MI355X_LIB") or LIB_PATH
 
 
 def load() -> ctypes.CDLL:
@@ -162,12 +165,13 @@ def load() -> ctypes.CDLL:
         return _lib
     with _lock:
         if _lib is None:
-            if not os.path.exists(LIB_PATH):
+            path = library_path()
+            if not os.path.exists(path):
                 raise HipExtensionMissing(
-                    f"{LIB_PATH} is missing: build it with `python -m tt_symbiote_amd.build` "
+                    f"{path} is missing: build it with `python -m tt_symbiote_amd.build` "
                     "(or __graft_entry__.build()) before running the HIP path"
                 )
-            lib = ctypes.CDLL(LIB_PATH)
+            lib = ctypes.CDLL(path)
             for name, (restype, argtypes) in _SIGNATURES.items():
                 fn = getattr(lib, name)
                 fn.restype = restype

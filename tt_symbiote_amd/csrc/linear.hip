@@ -250,11 +250,13 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) s_red[wave][mt][i][lane] = acc[mt][i];
     __syncthreads();
-    if (threadIdx.x < 256 * MT) {
+    // 256 fragment elements per tile; a 512-thread workgroup covers two tiles per round (the
+    // round count is uniform, so the shuffles below see whole waves)
+    for (int e = threadIdx.x; e < 256 * MT; e += kLinThreads) {
       // thread -> element i of lane l's fragment of tile mt: row 4*(l/16)+i, column l%16
-      const int mt = threadIdx.x >> 8;
-      const int l = threadIdx.x & 63;
-      const int i = (threadIdx.x >> 6) & 3;
+      const int mt = e >> 8;
+      const int l = e & 63;
+      const int i = (e >> 6) & 3;
       const int row = mb + mt * 16 + 4 * (l >> 4) + i;
       const int col = col0 + (l & 15);
       float v = 0.f;
@@ -301,10 +303,19 @@ template <bool NORM, bool RES>
 static void launch_proj(const void* x, const void* w, const void* bias, int M, int N, int K,
                         const void* gamma, float eps, const void* residual, float* sumsq_parts,
                         void* out_bf16, float* out_f32, hipStream_t s) {
-  hipLaunchKernelGGL((proj_kernel<2, 4, NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
-                     (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
-                     (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
-                     (uint16_t*)out_bf16, out_f32);
+  // rows in passes of 16 * MT, each pass streaming the weights: one pass up to 64 rows (with
+  // the norm fused, batches of 2 K-steps keep the 64-row pass within the register budget)
+  if (M > 32)
+    hipLaunchKernelGGL((proj_kernel<4, NORM ? 2 : 4, NORM, RES>), dim3(N / 16),
+                       dim3(kLinThreads), 0, s,
+                       (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
+                       (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
+                       (uint16_t*)out_bf16, out_f32);
+  else
+    hipLaunchKernelGGL((proj_kernel<2, 4, NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
+                       (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
+                       (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
+                       (uint16_t*)out_bf16, out_f32);
 }
 
 extern "C" int sym_linear_bf16(const void* x, const void* w, const void* bias, int M, int N,

@@ -27,6 +27,15 @@ __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// Lane -> k mapping inside a 64-wide K step (the same for both MFMA operands, so any mapping
+// is exact): lane group kq = l / 16 takes k = kKLane * kq + 0..7 for the first MFMA and the same
+// + kKHalf for the second.
+#ifdef SYM_KMAP_CONTIG
+constexpr int kKLane = 8, kKHalf = 32;   // one load instruction covers 64 contiguous bytes/row
+#else
+constexpr int kKLane = 16, kKHalf = 8;   // a lane's two loads are 32 contiguous bytes
+#endif
+
 // One pass of gate/up over 16 rows of a segment, for this wave's K-step range [s_beg, s_end)
 // (a multiple of U steps). Per batch of U K-steps: the weight loads, then the activation loads,
 // then the MFMAs, kept in that order by scheduling barriers. The 16 token indices of the pass
@@ -44,16 +53,16 @@ __device__ __forceinline__ void gate_up_pass(const uint16_t* __restrict__ x, int
   // dropped), loaded before the weights: waiting for it does not wait for them
   const int tok = tok_rows[min(r16, rows - 1)];
   __builtin_amdgcn_sched_barrier(0);
-  const uint16_t* xr = x + kq * 16;
+  const uint16_t* xr = x + kq * kKLane;
   for (int st = s_beg; st < s_end; st += U) {
     uint4 bg[U][2], bu[U][2], a[U][2];
 #pragma unroll
     for (int s = 0; s < U; ++s) {
       const int k = (st + s) << 6;
       bg[s][0] = ld16(wg + k);
-      bg[s][1] = ld16(wg + k + 8);
+      bg[s][1] = ld16(wg + k + kKHalf);
       bu[s][0] = ld16(wu + k);
-      bu[s][1] = ld16(wu + k + 8);
+      bu[s][1] = ld16(wu + k + kKHalf);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (st == s_beg) xr += (size_t)tok * H;
@@ -61,7 +70,7 @@ __device__ __forceinline__ void gate_up_pass(const uint16_t* __restrict__ x, int
     for (int s = 0; s < U; ++s) {
       const int k = (st + s) << 6;
       a[s][0] = ld16(xr + k);
-      a[s][1] = ld16(xr + k + 8);
+      a[s][1] = ld16(xr + k + kKHalf);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -139,7 +148,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
   const int nsteps = H >> 6;
   const int s_beg = (wave * nsteps) >> 2;
   const int s_end = ((wave + 1) * nsteps) >> 2;
-  const uint16_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * 16;
+  const uint16_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * kKLane;
   const uint16_t* wu = wg + (size_t)I * H;
 
   for (int mb = 0; mb < cnt; mb += 16) {
@@ -171,19 +180,19 @@ __device__ __forceinline__ void down_pass(const uint16_t* __restrict__ hrow, int
     for (int s = 0; s < U; ++s) {
       const int k = (st + s) << 6;
       b0[s][0] = ld16(wd0 + k);
-      b0[s][1] = ld16(wd0 + k + 8);
+      b0[s][1] = ld16(wd0 + k + kKHalf);
       b1[s][0] = ld16(wd1 + k);
-      b1[s][1] = ld16(wd1 + k + 8);
+      b1[s][1] = ld16(wd1 + k + kKHalf);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      const uint16_t* hr = hrow + (size_t)min(mt * 16 + r16, rows - 1) * I + kq * 16;
+      const uint16_t* hr = hrow + (size_t)min(mt * 16 + r16, rows - 1) * I + kq * kKLane;
 #pragma unroll
       for (int s = 0; s < U; ++s) {
         const int k = (st + s) << 6;
         a[mt][s][0] = ld16(hr + k);
-        a[mt][s][1] = ld16(hr + k + 8);
+        a[mt][s][1] = ld16(hr + k + kKHalf);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -241,7 +250,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
   if (col0 >= H) return;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
-  const uint16_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 16;
+  const uint16_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * kKLane;
   const uint16_t* wd1 = wd0 + (size_t)16 * I;
 
   for (int mb = 0; mb < cnt; mb += 16) {
@@ -504,6 +513,10 @@ extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t
   hipLaunchKernelGGL((moe_gate_up_kernel<UU>), grid, block, 0, (hipStream_t)stream,              \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
                      n_segments, (const uint16_t*)w_gate_up, (uint16_t*)h, tiles)
+#ifdef SYM_GATE_UP_U
+  if (wave_steps % SYM_GATE_UP_U == 0) SYM_LAUNCH_GATE_UP(SYM_GATE_UP_U);
+  else
+#endif
   if (wave_steps % 4 == 0) SYM_LAUNCH_GATE_UP(4);
   else if (wave_steps % 2 == 0) SYM_LAUNCH_GATE_UP(2);
   else SYM_LAUNCH_GATE_UP(1);
@@ -528,6 +541,10 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
   hipLaunchKernelGGL((moe_down_kernel<UU>), grid, block, 0, (hipStream_t)stream,                 \
                      (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
                      (const uint16_t*)w_down, y, tiles)
+#ifdef SYM_DOWN_U
+  if (steps % SYM_DOWN_U == 0) SYM_LAUNCH_DOWN(SYM_DOWN_U);
+  else
+#endif
   if (steps % 4 == 0) SYM_LAUNCH_DOWN(4);
   else if (steps % 2 == 0) SYM_LAUNCH_DOWN(2);
   else SYM_LAUNCH_DOWN(1);

@@ -25,6 +25,14 @@ namespace sym {
 constexpr int kHeadDim = 128;
 constexpr int kTPW = 64;           // tokens per wave in the split kernel
 constexpr int kSplit = 4 * kTPW;  // tokens per split (one workgroup of 4 waves)
+// The fp8 cache's split kernel: tokens per wave (a wave of 128 tokens fits the bf16 kernel's
+// registers, but measured slower: 225 against 199 us at batch 128 with 1024-8192 contexts).
+#ifdef SYM_FP8_TPW
+constexpr int kTPW8 = SYM_FP8_TPW;
+#else
+constexpr int kTPW8 = 64;
+#endif
+constexpr int kSplit8 = 4 * kTPW8;
 constexpr int kAttnThreads = 256;
 
 // ---------------------------------------------------------------------------------------------
@@ -515,13 +523,13 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ positions, int B, int Hq, int max_context, int max_splits,
-    uint16_t* __restrict__ out) {
+    int split_tokens, uint16_t* __restrict__ out) {
   constexpr int D = kHeadDim;
   const int lane = threadIdx.x & 63;
   const int idx = blockIdx.x * 4 + (threadIdx.x >> 6);  // b * Hq + head
   if (idx >= B * Hq) return;
   const int ctx = min(positions[idx / Hq] + 1, max_context);
-  const int nsplit = ctx <= 0 ? 0 : (ctx + kSplit - 1) / kSplit;
+  const int nsplit = ctx <= 0 ? 0 : (ctx + split_tokens - 1) / split_tokens;
   if (nsplit <= 1) return;  // written directly by the split kernel
   const float2* ml = reinterpret_cast<const float2*>(ws_ml) + (size_t)idx * max_splits;
   const float2* po = reinterpret_cast<const float2*>(ws_o) + (size_t)idx * max_splits * (D / 2) + lane;
@@ -727,8 +735,9 @@ __device__ __forceinline__ void fp8_append_token(uint8_t* __restrict__ pool,
 //   P.V (the softmax sum uses the unscaled probability), so the dequantised values are never
 //   formed. In the fused step the workgroup of the sequence's last split first appends the new
 //   token's k and v to the pool (with any requantisation of its block), then reads the split
-//   from the pool like every other workgroup; a block never straddles two splits
-//   (256 % block_size == 0), so no other workgroup reads the block being rewritten.
+//   from the pool like every other workgroup; a block never straddles two splits (block_size
+//   divides 256, and the split is a multiple of 256 tokens), so no other workgroup reads the
+//   block being rewritten. A thread owns split / 256 tokens in the softmax.
 template <int G, bool FUSED>
 __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
     const uint16_t* __restrict__ q, FusedQKV fq, uint8_t* __restrict__ k_pool,
@@ -738,10 +747,11 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
     float* __restrict__ ws_o, float* __restrict__ ws_ml, int max_splits,
     uint16_t* __restrict__ out) {
   constexpr int D = kHeadDim;
-  constexpr int TPW = kTPW;
-  constexpr int SPLIT = kSplit;
-  constexpr int KT = TPW / 16;
-  constexpr int VS = TPW / 4;
+  constexpr int TPW = kTPW8;
+  constexpr int SPLIT = kSplit8;
+  constexpr int KT = TPW / 16;                 // 16-token K tiles per wave
+  constexpr int VS = TPW / 4;                  // P.V steps per wave
+  constexpr int TPT = SPLIT / kAttnThreads;    // tokens per thread in the softmax
   __shared__ __align__(16) uint16_t s_q[G][D];
   __shared__ float s_p[G][SPLIT];
   __shared__ float s_red[4][G][D];
@@ -801,18 +811,21 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
           q + ((size_t)b * Hq + g * G + h) * D + c * 8);
     }
   }
-  // token t0 + tid: its pool row (always in bounds), validity and scale index
-  bool my_ok;
-  size_t my_sidx;
-  {
-    const int t = t0 + tid;
+  // tokens t0 + tid + 256 j of the split: their pool rows (always in bounds), validity and
+  // scale indices
+  bool my_ok[TPT];
+  size_t my_sidx[TPT];
+#pragma unroll
+  for (int j = 0; j < TPT; ++j) {
+    const int tl = tid + kAttnThreads * j;
+    const int t = t0 + tl;
     const int tc = min(t, t1 - 1);
     const int blk = tc / block_size;
     int pb = blk < mbps ? block_tables[(size_t)b * mbps + blk] : -1;
-    my_ok = t < t1 && pb >= 0 && pb < num_blocks;
+    my_ok[j] = t < t1 && pb >= 0 && pb < num_blocks;
     if (pb < 0 || pb >= num_blocks) pb = 0;
-    s_row[tid] = (unsigned)(((size_t)pb * Hkv + g) * block_size + (tc - blk * block_size));
-    my_sidx = (size_t)pb * Hkv + g;
+    s_row[tl] = (unsigned)(((size_t)pb * Hkv + g) * block_size + (tc - blk * block_size));
+    my_sidx[j] = (size_t)pb * Hkv + g;
   }
   if constexpr (FUSED) {
 #pragma unroll
@@ -825,7 +838,7 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
   const int wt0 = wave * TPW;
   uint4 kb[KT][2];
   uint2 vreg[VS];
-  float ks_own = 0.f, vs_own = 0.f;
+  float ks_own[TPT], vs_own[TPT];
   auto issue_loads = [&]() {
 #pragma unroll
     for (int tt = 0; tt < KT; ++tt) {
@@ -837,8 +850,11 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
     for (int it = 0; it < VS; ++it)
       vreg[it] = *reinterpret_cast<const uint2*>(v_pool + (size_t)s_row[wt0 + it * 4 + kg] * D +
                                                  r16 * 8);
-    ks_own = k_scale[my_sidx];
-    vs_own = v_scale[my_sidx];
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      ks_own[j] = k_scale[my_sidx[j]];
+      vs_own[j] = v_scale[my_sidx[j]];
+    }
   };
   if (!writer) issue_loads();
   if constexpr (FUSED) {
@@ -895,14 +911,19 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
   }
   __syncthreads();
 
-  // ---- softmax statistics (log2 domain); thread tid owns token t0 + tid ----
-  const float kscale = ks_own * scale_log2;
+  // ---- softmax statistics (log2 domain); thread tid owns tokens t0 + tid + 256 j ----
   float mx[G];
-  float sc[G];
+  float sc[G][TPT];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    sc[h] = my_ok ? s_p[h][tid] * kscale : -INFINITY;
-    const float m = wave_max(sc[h]);
+    float m = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      sc[h][j] = my_ok[j] ? s_p[h][tid + kAttnThreads * j] * (ks_own[j] * scale_log2)
+                          : -INFINITY;
+      m = fmaxf(m, sc[h][j]);
+    }
+    m = wave_max(m);
     if (lane == 0) s_stat[h][wave] = m;
   }
   __syncthreads();
@@ -912,9 +933,15 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
   __syncthreads();
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float pr = (mx[h] == -INFINITY || sc[h] == -INFINITY) ? 0.f : exp2f(sc[h] - mx[h]);
-    s_p[h][tid] = pr * vs_own;
-    const float l = wave_sum(pr);
+    float l = 0.f;
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+      const float pr =
+          (mx[h] == -INFINITY || sc[h][j] == -INFINITY) ? 0.f : exp2f(sc[h][j] - mx[h]);
+      s_p[h][tid + kAttnThreads * j] = pr * vs_own[j];
+      l += pr;
+    }
+    l = wave_sum(l);
     if (lane == 0) s_stat[h][wave] = l;
   }
   __syncthreads();
@@ -1141,7 +1168,8 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
   const size_t need = sym_paged_gqa_decode_workspace_bytes(B, Hq, head_dim, max_context);
   SYM_REQUIRE(workspace_bytes >= need, SYM_ERR_WORKSPACE, "%s: workspace %zu < required %zu",
               what, workspace_bytes, need);
-  const int max_splits = (max_context + kSplit - 1) / kSplit;
+  const int split_tokens = fp8 ? kSplit8 : kSplit;
+  const int max_splits = (max_context + split_tokens - 1) / split_tokens;
   float* ws_o = (float*)workspace;
   float* ws_ml = ws_o + (size_t)B * Hq * max_splits * head_dim;
   const float scale_log2 = scale * 1.4426950408889634f;
@@ -1182,7 +1210,8 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
   rc = sym_host::check_launch(fp8 ? "paged_decode_fp8_kernel" : "paged_decode_kernel");
   if (rc || max_splits == 1) return rc;
   hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((B * Hq + 3) / 4), dim3(256), 0, s, ws_o,
-                     ws_ml, positions, B, Hq, max_context, max_splits, (uint16_t*)out);
+                     ws_ml, positions, B, Hq, max_context, max_splits, split_tokens,
+                     (uint16_t*)out);
   return sym_host::check_launch("paged_decode_merge_kernel");
 }
 

@@ -4,6 +4,11 @@
       per-kernel dispatch count and average / min / max / total duration, from the SQLite
       database written by ``rocprofv3 --kernel-trace``;
 
+  python -m tt_symbiote_amd.rocprof_summary timeline <results.db> --last N
+      the last N dispatches in start order (e.g. the replays of a captured step): per kernel
+      the mean duration and the mean idle gap between the previous dispatch's end and its
+      start, and the window's busy fraction;
+
   python -m tt_symbiote_amd.rocprof_summary pmc --kernel NAME --fetch F.csv --write W.csv
           --calib-fetch CF.csv --calib-write CW.csv --calib-kernel NAME --calib-bytes N [--json]
       HBM bytes per dispatch of kernel NAME from two ``rocprofv3 --pmc FETCH_SIZE`` /
@@ -37,6 +42,33 @@ def print_trace(db_path: str, top: int) -> None:
     for name, n, avg, tot, mn, mx in kernel_stats(db_path)[:top]:
         print(f"{n:6d} {avg / 1e3:9.1f} {mn / 1e3:9.1f} {mx / 1e3:9.1f} {tot / 1e6:9.2f}  "
               f"{name[:110]}")
+
+
+def print_timeline(db_path: str, last: int) -> None:
+    db = sqlite3.connect(db_path)
+    rows = db.execute(
+        "select s.kernel_name, d.start, d.end from rocpd_kernel_dispatch d "
+        "join rocpd_info_kernel_symbol s on d.kernel_id = s.id order by d.start").fetchall()
+    db.close()
+    rows = rows[-last:]
+    dur = defaultdict(list)
+    gap = defaultdict(list)
+    order = []
+    for i, (name, st, en) in enumerate(rows):
+        if name not in dur:
+            order.append(name)
+        dur[name].append(en - st)
+        if i:
+            gap[name].append(max(0, st - rows[i - 1][2]))
+    span = rows[-1][2] - rows[0][1]
+    busy = sum(en - st for _, st, en in rows)
+    print(f"window: {len(rows)} dispatches, {span / 1e3:.1f} us, busy {busy / 1e3:.1f} us "
+          f"({100.0 * busy / span:.1f}%)")
+    print(f"{'calls':>6} {'avg us':>9} {'gap us':>9}  kernel (in order of first start)")
+    for name in order:
+        g = gap[name]
+        print(f"{len(dur[name]):6d} {statistics.mean(dur[name]) / 1e3:9.2f} "
+              f"{(statistics.mean(g) / 1e3 if g else 0.0):9.2f}  {name[:100]}")
 
 
 def counter_per_dispatch(csv_path: str, counter: str) -> dict:
@@ -94,6 +126,9 @@ def main(argv=None) -> None:
     t = sub.add_parser("trace")
     t.add_argument("db")
     t.add_argument("--top", type=int, default=25)
+    tl = sub.add_parser("timeline")
+    tl.add_argument("db")
+    tl.add_argument("--last", type=int, default=100)
     p = sub.add_parser("pmc")
     p.add_argument("--kernel", required=True)
     p.add_argument("--fetch", required=True)
@@ -106,6 +141,9 @@ def main(argv=None) -> None:
     args = ap.parse_args(argv)
     if args.cmd == "trace":
         print_trace(args.db, args.top)
+        return
+    if args.cmd == "timeline":
+        print_timeline(args.db, args.last)
         return
     res = pmc_traffic(args)
     if args.json:
