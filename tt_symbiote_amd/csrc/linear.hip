@@ -303,11 +303,11 @@ template <bool NORM, bool RES>
 static void launch_proj(const void* x, const void* w, const void* bias, int M, int N, int K,
                         const void* gamma, float eps, const void* residual, float* sumsq_parts,
                         void* out_bf16, float* out_f32, hipStream_t s) {
-  // rows in passes of 16 * MT, each pass streaming the weights: one pass up to 64 rows (with
-  // the norm fused, batches of 2 K-steps keep the 64-row pass within the register budget)
-  if (M > 32)
-    hipLaunchKernelGGL((proj_kernel<4, NORM ? 2 : 4, NORM, RES>), dim3(N / 16),
-                       dim3(kLinThreads), 0, s,
+  // rows in passes of 16 * MT, each pass streaming the weights: one pass up to 64 rows. With
+  // the norm fused, 32-row passes keep the single-batch path (a 64-row pass needs two batches
+  // of K-steps and measured slower at 64 rows: 24.4 against 18.7 us for 3072 x 2048)
+  if (M > 32 && !NORM)
+    hipLaunchKernelGGL((proj_kernel<4, 4, NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
                        (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
                        (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
                        (uint16_t*)out_bf16, out_f32);

@@ -145,6 +145,9 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(
           sP[wave][(t * 16 + 4 * kq + i) * kPPStride + j * 16 + r16] = f32_to_bf16(x[j]);
       }
     }
+    // P is written and read by different lanes of this wave: the wavefront-scope fence keeps
+    // the compiler from moving the reads above the writes (a wave's LDS operations run in order)
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
     // ---- O += P V (P rows as A: row r16, keys 8*kq + 32*c; V^T rows as B) ----
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
