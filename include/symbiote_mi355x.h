@@ -242,6 +242,17 @@ int sym_attn_decode_step_fp8(const void* qkv, const void* q_norm_w, const void* 
 int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E, float* parts,
                           void* stream);
 
+/* The same router logits for prefill-size T, on bf16 MFMA tiles (sym_gemm_bf16's kernel):
+ *   w_planes [3, E, H] bf16 with w = hi + mid + lo exactly (the fp32 gate weight split into
+ *   three 8-bit-mantissa planes, e.g. hi = w with its low 16 bits cleared, mid likewise of
+ *   w - hi, lo = w - hi - mid); x [T, H] bf16;
+ *   parts [3, T, E] fp32: parts[z] = x . plane_z^T (each product exact in fp32), summed
+ *   (parts[0] + parts[1]) + parts[2] by sym_moe_route_permute (n_logit_parts = 3).
+ * H % 64 == 0, E % 16 == 0.
+ */
+int sym_moe_router_logits_split(const void* x, const void* w_planes, int T, int H, int E,
+                                float* parts, void* stream);
+
 /* Router logits with the post-attention RMSNorm fused in front (the decoder layer's
  * post_attention_layernorm, modeling_bailing_moe_v2.py:463-465, feeding TTNNMoE.forward):
  *   h [T, H] fp32 residual stream; ss_parts [n_ss, T] fp32 partial sums of squares of h's rows
@@ -330,14 +341,14 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
                      const float* s_down, float* y, void* stream);
 
 /* ---------------------------------------------------------------------------------------
- * Tiled GEMMs for prefill-size batches (MFMA-bound; 128 x 128 output tiles).
+ * Tiled GEMMs for prefill-size batches (MFMA-bound; 128 x 256 output tiles).
  * sym_gemm_bf16: out[M, N] = a[M, K] . w[N, K]^T (+ bias[N] bf16) (+ residual[M, N] fp32),
  *   bf16 out, or fp32 when out_fp32 != 0. Replaces the QKV / dense projections at sequence length
- *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 128 == 0, K % 64 == 0.
+ *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 16 == 0, K % 64 == 0.
  * sym_moe_gate_up_tiled / sym_moe_down_tiled: the grouped expert GEMMs of sym_moe_gate_up /
  *   sym_moe_down (same arguments and results; TTNNExperts.forward, ttnn_moe.py:1250-1289) for
  *   segments of many rows; rows = total rows of the segment list (T*top_k + T with the shared
- *   expert). H % 128 == 0, I % 64 == 0.
+ *   expert). H % 64 == 0, I % 64 == 0.
  */
 int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
                   int N, int K, void* out, int out_fp32, void* stream);

@@ -110,6 +110,10 @@ def test_linear_and_router_reject_bad_shapes():
     assert _call("sym_moe_router_logits", FAKE, FAKE, 4, 2000, 256, FAKE, None)[0] == 2
     assert _call("sym_moe_router_logits", FAKE, FAKE, 4, 2048, 250, FAKE, None)[0] == 2
     assert _call("sym_moe_router_logits", FAKE, None, 4, 2048, 256, FAKE, None)[0] == 1
+    assert _call("sym_moe_router_logits_split", FAKE, FAKE, 4, 2000, 256, FAKE, None)[0] == 2
+    assert _call("sym_moe_router_logits_split", FAKE, FAKE, 4, 2048, 250, FAKE, None)[0] == 2
+    assert _call("sym_moe_router_logits_split", FAKE, None, 4, 2048, 256, FAKE, None)[0] == 1
+    assert _call("sym_moe_router_logits_split", FAKE, FAKE, 0, 2048, 256, FAKE, None)[0] == 0
 
 
 def _prototype_arg_counts():

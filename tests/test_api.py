@@ -151,3 +151,19 @@ def test_ops_reject_cpu_tensors():
     with pytest.raises(ValueError, match="GPU tensor"):
         hip_ops.moe_route_permute(torch.zeros(2, 64), torch.zeros(64), n_group=8, topk_group=4,
                                   top_k=4, routed_scale=1.0)
+
+
+def test_router_weight_splits_exactly_into_three_bf16_planes():
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(256, 2048, generator=g) * 0.02
+    w[0, :8] = torch.tensor([1.0, -3.75, 1e-3, 123.456, -1e-6, 0.0, 2.0 ** -60, 7.1e4])
+    planes = hip_ops.split_router_weight(w)
+    assert planes.shape == (3, 256, 2048) and planes.dtype == torch.bfloat16
+    back = (planes[0].float() + planes[1].float()) + planes[2].float()
+    assert torch.equal(back, w)
+    # the planes are the mantissa bytes from the top: |hi| >= 128|mid| >= 128^2|lo| per value
+    hi, mid, lo = (p.float().abs() for p in planes)
+    assert bool((hi >= 128 * mid).all()) and bool((mid >= 128 * lo).all())
+    # a weight with a single significant byte is all hi
+    assert torch.equal(hip_ops.split_router_weight(torch.full((2, 64), 0.5))[1:].float(),
+                       torch.zeros(2, 2, 64))

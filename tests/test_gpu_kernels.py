@@ -162,6 +162,30 @@ def test_router_logits(device, T, H, E):
     torch.testing.assert_close(parts[1].cpu().double(), ref1, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("T,H,E", [(300, 2048, 256), (4100, 2048, 256), (129, 512, 64)])
+def test_router_logits_split(device, T, H, E):
+    g = torch.Generator().manual_seed(T + E + 1)
+    x = torch.randn(T, H, generator=g).bfloat16()
+    w = (torch.randn(E, H, generator=g) * 0.02).float()
+    planes = hip_ops.split_router_weight(w)
+    parts = hip_ops.moe_router_logits_split(x.to(device), planes.to(device))
+    assert parts.shape == (3, T, E)
+    ref = x.double() @ w.double().T
+    got = (parts[0].cpu() + parts[1].cpu()) + parts[2].cpu()  # the route kernel's order
+    torch.testing.assert_close(got.double(), ref, rtol=1e-5, atol=1e-5)
+    # each part is the exact product with its plane (fp32 accumulation only)
+    ref_lo = x.double() @ planes[2].double().T
+    torch.testing.assert_close(parts[2].cpu().double(), ref_lo, rtol=1e-5, atol=1e-9)
+    # same routing as the fp32 router kernel wherever the choice is not a near tie
+    bias = torch.zeros(E)
+    kw = dict(n_group=8, topk_group=4, top_k=8, routed_scale=2.5)
+    r_split = hip_ops.moe_route_permute(parts, bias.to(device), **kw)
+    r_fp32 = hip_ops.moe_route_permute(hip_ops.moe_router_logits(x.to(device), w.to(device)),
+                                       bias.to(device), **kw)
+    same = (r_split.topk_idx.cpu().sort(1).values == r_fp32.topk_idx.cpu().sort(1).values)
+    assert same.all(1).float().mean() > 0.999
+
+
 @pytest.mark.parametrize("M,N,K,bias,out_dtype", [
     (32, 3072, 2048, False, torch.bfloat16),
     (32, 2048, 2048, True, torch.bfloat16),
@@ -266,6 +290,7 @@ def _gemm_case(T, E, H, I, top_k, seed, device, with_shared=True, skew=False):
     (7, 64, 512, 192, 4, False),
     (200, 64, 256, 128, 6, True),       # segments of > 64 rows (several passes)
     (700, 64, 512, 256, 8, True),       # segments of several 128-row tiles
+    (300, 64, 512, 192, 6, True),       # I not a multiple of the 128 h columns of a tile
 ])
 def test_grouped_swiglu(device, T, E, H, I, top_k, skew, kernel):
     x, wgu, wd, res = _gemm_case(T, E, H, I, top_k, seed=T + E, device=device, skew=skew)
@@ -296,6 +321,8 @@ def test_grouped_swiglu(device, T, E, H, I, top_k, skew, kernel):
     (256, 2048, 2048, True, True, torch.float32),
     (1, 128, 64, False, False, torch.float32),
     (130, 256, 576, True, False, torch.bfloat16),
+    (77, 400, 192, True, True, torch.float32),          # N not a multiple of the 256-wide tile
+    (300, 16, 128, False, False, torch.bfloat16),
 ])
 def test_gemm_tiled(device, M, N, K, bias, res, out_dtype):
     g = torch.Generator().manual_seed(M + N + K)

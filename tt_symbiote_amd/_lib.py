@@ -84,6 +84,7 @@ _SIGNATURES = {
         _c_int, [_vp, _vp, _c_int, _vp, _c_float, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]
     ),
     "sym_moe_router_logits": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "sym_moe_router_logits_split": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "sym_moe_route_workspace_bytes": (_c_size, [_c_int, _c_int]),
     "sym_moe_route_permute": (
         _c_int,

@@ -5,27 +5,35 @@
 // sequence length > 1, and the expert sparse_matmuls of TTNNExperts.forward
 // (ttnn_moe.py:1250-1289) with the shared expert (ttnn_moe.py:656-675), for prefill batches.
 //
-// Design (gfx950): a workgroup of 4 waves computes a 128 x 128 output tile; each wave owns a
-// 64 x 64 quadrant as 4 x 4 v_mfma_f32_16x16x32_bf16 tiles (64 accumulator registers). The K
-// loop moves 64 columns per step: every thread loads 4 x 16 bytes of the A tile and 4 x 16
-// bytes of the B tile (8 threads per 128-byte row, coalesced), stores them to LDS (rows padded
-// to 144 bytes so the 16 rows of an MFMA fragment read fall in distinct banks), and the loads of
-// step k+1 are in flight while step k's 32 MFMAs per wave run from LDS.
+// Design (gfx950): a workgroup of 8 waves computes a 128 x 256 output tile; wave w owns the
+// 64 x 64 block (rows 64*(w/4), columns 64*(w%4)) as 4 x 4 v_mfma_f32_16x16x32_bf16 tiles. The
+// K loop moves 64 columns per step through a 3-stage LDS ring (48 KB per stage, 144 KB): the
+// operand tiles go from global memory straight into LDS (global_load_lds_dwordx4, no register
+// staging), two steps ahead of the MFMAs, with one barrier per step. A wave-wide LDS-DMA
+// instruction writes 1 KB = 8 rows of 64 bf16 contiguously (lane l -> row l/8, 16-byte slot
+// l%8), so each lane fetches the global 16-byte chunk (l%8) ^ (row%8): chunk c of row r sits
+// in slot c ^ (r%8), and the 16 rows of an MFMA fragment read (one chunk each) spread over all
+// eight slots of a 128-byte row instead of hitting the same banks.
 //   DENSE:   out[M, N] = A[M, K] . W[N, K]^T (+ bias) (+ residual fp32), bf16 or fp32 out.
-//   GATE_UP: rows of a segment gather x[sorted_tokens[row]]; the B tile holds 64 gate rows and
-//            the matching 64 up rows of the expert, so each wave's quadrant pairs 32 gate with 32
+//   GATE_UP: rows of a segment gather x[sorted_tokens[row]]; the B tile holds 128 gate rows and
+//            the matching 128 up rows of the expert, so each wave's block pairs 32 gate with 32
 //            up columns and the epilogue writes h = silu(gate) * up (bf16).
 //   DOWN:    rows of a segment are h rows (contiguous); y = h . W_down^T (fp32).
-// Grouped modes: the workgroup's row tile is found from the device-side segment list (prefix
-// of ceil(count / 128) over the segments, in LDS); workgroups past the last tile exit.
+// Rows past a tile's valid rows and columns past N repeat the last row / column in the loads
+// (always in bounds) and are not stored.
+// Grouped modes: the workgroup's row tile is found from the device-side segment list (each
+// segment owns ceil(count / 128) consecutive tiles of the grid's y range); workgroups past the
+// last tile exit.
 #include "common.h"
 
 namespace sym {
 
-constexpr int kTM = 128, kTN = 128, kTK = 64;
-constexpr int kTileThreads = 256;
-constexpr int kLdsStride = kTK + 8;  // bf16 elements per LDS row (144 bytes)
-constexpr int kMaxGemmSegments = 4096;
+constexpr int kTM = 128, kTN = 256, kTK = 64;
+constexpr int kTileThreads = 512;
+constexpr int kAStage = kTM * kTK;  // bf16 elements of one A stage (16 KB)
+constexpr int kBStage = kTN * kTK;  // bf16 elements of one B stage (32 KB)
+constexpr int kDmaPerStep = (kAStage + kBStage) * 2 / 1024 / (kTileThreads / 64);  // per wave
+constexpr int kMaxGemmSegments = 4096;  // grid bound on segments (y range)
 
 enum TileMode { kDense = 0, kGateUp = 1, kDown = 2 };
 
@@ -42,22 +50,38 @@ struct TileArgs {
   int M, N, K;              // GATE_UP: N = I (h columns); DOWN: N = H
   uint16_t* out_bf16;
   float* out_f32;
+  long long w_zstride;      // DENSE: grid z selects weight plane w + z * w_zstride ...
+  long long out_zstride;    // ... and output plane out + z * out_zstride (elements)
 };
 
-__device__ __forceinline__ uint4 ld_g16(const uint16_t* p) {
-  return *reinterpret_cast<const uint4*>(p);
+// 16 bytes per lane from global memory into LDS at base + 16 * lane (base wave-uniform, in M0).
+// Written as asm so that the compiler does not add its own (conservative) waits for these LDS
+// writes: the kernel waits for them explicitly (SYM_TILE_SYNC) before the barrier that
+// publishes a stage.
+// (M0 is written here only; no other instruction of these kernels reads it.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const uint16_t* g, const uint16_t* lds_base) {
+  const uint32_t lds = (uint32_t)(uintptr_t)lds_base;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
+               : "memory", "m0");
 }
+#pragma clang diagnostic pop
+
+// Wait until at most N of this wave's vector-memory loads are outstanding (the LDS-DMA of the
+// later steps), then the workgroup barrier. The asm is a compiler memory barrier, so no LDS
+// access moves across it; a plain __syncthreads would also wait for every DMA in flight.
+#define SYM_TILE_SYNC(N) \
+  asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 template <int MODE>
 __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
-  __shared__ __align__(16) uint16_t sA[kTM * kLdsStride];
-  __shared__ __align__(16) uint16_t sB[kTN * kLdsStride];
-  __shared__ int s_tile_start[MODE == kDense ? 1 : kMaxGemmSegments + 1];
-  __shared__ int s_info[4];
+  __shared__ __align__(1024) uint16_t sA0[kAStage], sA1[kAStage], sA2[kAStage];
+  __shared__ __align__(1024) uint16_t sB0[kBStage], sB1[kBStage], sB2[kBStage];
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wm = wave >> 2, wn = wave & 3;
   const int r16 = lane & 15, kq = lane >> 4;
   const int K = p.K;
 
@@ -67,63 +91,93 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
   if constexpr (MODE == kDense) {
     row0 = blockIdx.y * kTM;
     rows = min(kTM, p.M - row0);
+    p.w += blockIdx.z * p.w_zstride;
+    if (p.out_f32) p.out_f32 += blockIdx.z * p.out_zstride;
+    else p.out_bf16 += blockIdx.z * p.out_zstride;
   } else {
+    // Every wave scans the segment list 64 segments at a time (prefix sum by lane shuffles)
+    // and stops at the one holding tile g: no LDS and no barrier, and all waves agree.
     const int nseg = p.n_segments[0];
-    if (wave == 0) {
-      int run = 0;
-      for (int s0 = 0; s0 < nseg; s0 += 64) {
-        const int s = s0 + lane;
-        const int nt = s < nseg ? (p.seg_count[s] + kTM - 1) / kTM : 0;
-        int x = nt;
-#pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const int y = __shfl_up(x, off);
-          if (lane >= off) x += y;
-        }
-        if (s < nseg) s_tile_start[s] = run + x - nt;
-        run += __shfl(x, 63);
-      }
-      if (lane == 0) s_tile_start[nseg] = run;
-    }
-    __syncthreads();
     const int g = blockIdx.y;
-    if (g >= s_tile_start[nseg]) return;
-    if (tid == 0) s_info[0] = 0;
-    __syncthreads();
-    for (int s = tid; s < nseg; s += kTileThreads)
-      if (s_tile_start[s] <= g && g < s_tile_start[s + 1]) s_info[0] = s;
-    __syncthreads();
-    const int seg = s_info[0];
-    const int rt = g - s_tile_start[seg];
+    int seg = -1, start = 0, run = 0;
+    for (int s0 = 0; s0 < nseg; s0 += 64) {
+      const int s = s0 + lane;
+      const int nt = s < nseg ? (p.seg_count[s] + kTM - 1) / kTM : 0;
+      int x = nt;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off);
+        if (lane >= off) x += y;
+      }
+      const int st = run + x - nt;
+      const unsigned long long hit = __ballot(nt > 0 && st <= g && g < st + nt);
+      if (hit) {
+        const int l = __ffsll((long long)hit) - 1;
+        seg = s0 + l;
+        start = __shfl(st, l);
+        break;
+      }
+      run += __shfl(x, 63);
+    }
+    if (seg < 0) return;  // past the last tile (the grid is sized for the worst case)
+    const int rt = g - start;
     e = p.seg_expert[seg];
     row0 = p.seg_offset[seg] + rt * kTM;
     rows = min(kTM, p.seg_count[seg] - rt * kTM);
   }
 
-  // ---- global -> register mapping: thread loads rows (tid/8) + 32j, 16-byte chunk tid%8 ----
-  const int lrow = tid >> 3, lchunk = tid & 7;
-  const uint16_t* a_ptr[4];
-  const uint16_t* b_ptr[4];
+  // ---- LDS-DMA sources: this wave fills A rows 16w .. 16w+15 (2 instructions) and B rows
+  // 32w .. 32w+31 (4 instructions) of every stage; lane l takes row +l/8, chunk (l%8)^(row%8)
+  const int lr = lane >> 3;
+  const int a_row_l = wave * 16 + lr;   // + 8i; row % 8 == lr
+  const int b_row_l = wave * 32 + lr;   // + 8i
+  const int chunk = ((lane & 7) ^ lr) * 8;
+  const uint16_t* a_src[2];
+  const uint16_t* b_src[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int r = min(lrow + 32 * j, rows - 1);  // rows past the tile repeat its last row
+  for (int i = 0; i < 2; ++i) {
+    const int r = min(a_row_l + 8 * i, rows - 1);
     size_t arow;
     if constexpr (MODE == kGateUp) arow = (size_t)p.sorted_tokens[row0 + r];
     else arow = (size_t)(row0 + r);
-    a_ptr[j] = p.a + arow * K + lchunk * 8;
-    const int br = lrow + 32 * j;  // B tile row 0..127
+    a_src[i] = p.a + arow * K + chunk;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int br = b_row_l + 8 * i;  // B tile row 0..255
     size_t brow;
     if constexpr (MODE == kGateUp) {
-      // 64 gate rows then the matching 64 up rows of expert e
-      const int col = ct * 64 + (br & 63);
-      brow = (size_t)e * 2 * p.N + (br < 64 ? col : p.N + col);
+      // 128 gate rows then the matching 128 up rows of expert e
+      const int col = min(ct * 128 + (br & 127), p.N - 1);
+      brow = (size_t)e * 2 * p.N + (br < 128 ? col : p.N + col);
     } else if constexpr (MODE == kDown) {
-      brow = (size_t)e * p.N + ct * kTN + br;
+      brow = (size_t)e * p.N + min(ct * kTN + br, p.N - 1);
     } else {
-      brow = (size_t)(ct * kTN + br);
+      brow = (size_t)min(ct * kTN + br, p.N - 1);
     }
-    b_ptr[j] = p.w + brow * K + lchunk * 8;
+    b_src[i] = p.w + brow * K + chunk;
   }
+  const int a_dst = wave * 16 * kTK;  // element offset of this wave's first A row in a stage
+  const int b_dst = wave * 32 * kTK;
+
+  auto issue = [&](int kt, uint16_t* sA, uint16_t* sB) {
+    const int k = kt * kTK;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(a_src[i] + k, sA + a_dst + i * 8 * kTK);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) dma16(b_src[i] + k, sB + b_dst + i * 8 * kTK);
+  };
+
+  // fragment rows of this wave: A rows wm*64 + 16i + r16; B rows per column tile j
+  int b_frag[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if constexpr (MODE == kGateUp)
+      b_frag[j] = (j < 2 ? 0 : 128) + wn * 32 + (j & 1) * 16 + r16;
+    else
+      b_frag[j] = wn * 64 + j * 16 + r16;
+  }
+  const int sw = r16 & 7;  // every fragment row r has r % 8 == r16 % 8
 
   floatx4 acc[4][4];
 #pragma unroll
@@ -131,54 +185,42 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  uint4 ra[4], rb[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    ra[j] = ld_g16(a_ptr[j]);
-    rb[j] = ld_g16(b_ptr[j]);
-  }
-  // B fragment rows of this wave's 4 column tiles
-  int brow_frag[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    if constexpr (MODE == kGateUp)
-      brow_frag[j] = (j < 2 ? 0 : 64) + wn * 32 + (j & 1) * 16 + r16;
-    else
-      brow_frag[j] = wn * 64 + j * 16 + r16;
-  }
-
-  const int nk = K / kTK;
-  for (int kt = 0; kt < nk; ++kt) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      *reinterpret_cast<uint4*>(&sA[(lrow + 32 * j) * kLdsStride + lchunk * 8]) = ra[j];
-      *reinterpret_cast<uint4*>(&sB[(lrow + 32 * j) * kLdsStride + lchunk * 8]) = rb[j];
-    }
-    __syncthreads();
-    if (kt + 1 < nk) {
-      const int k = (kt + 1) * kTK;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        ra[j] = ld_g16(a_ptr[j] + k);
-        rb[j] = ld_g16(b_ptr[j] + k);
-      }
-    }
+  auto compute = [&](const uint16_t* sA, const uint16_t* sB) {
 #pragma unroll
     for (int kh = 0; kh < 2; ++kh) {
-      const int ko = kh * 32 + kq * 8;
+      const int slot = ((kh * 4 + kq) ^ sw) * 8;
       uint4 fa[4], fb[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        fa[i] = *reinterpret_cast<const uint4*>(&sA[(wm * 64 + i * 16 + r16) * kLdsStride + ko]);
+        fa[i] = *reinterpret_cast<const uint4*>(&sA[(wm * 64 + i * 16 + r16) * kTK + slot]);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        fb[j] = *reinterpret_cast<const uint4*>(&sB[brow_frag[j] * kLdsStride + ko]);
+        fb[j] = *reinterpret_cast<const uint4*>(&sB[b_frag[j] * kTK + slot]);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(fa[i], fb[j], acc[i][j]);
     }
-    __syncthreads();
+  };
+
+  // Step k: wait for its stage (the DMA of step k + 1 may still be in flight), barrier (every
+  // wave is also done with step k - 1's stage), issue step k + 2 into that stage, MFMAs.
+  static_assert(kDmaPerStep == 6, "SYM_TILE_SYNC count");
+  const int nk = K / kTK;
+  issue(0, sA0, sB0);
+  if (nk > 1) issue(1, sA1, sB1);
+  auto step = [&](int kt, const uint16_t* cA, const uint16_t* cB, uint16_t* nA, uint16_t* nB) {
+    if (kt + 1 < nk) SYM_TILE_SYNC(6);
+    else SYM_TILE_SYNC(0);
+    if (kt + 2 < nk) issue(kt + 2, nA, nB);
+    compute(cA, cB);
+  };
+  for (int kt = 0; kt < nk; kt += 3) {
+    step(kt, sA0, sB0, sA2, sB2);
+    if (kt + 1 >= nk) break;
+    step(kt + 1, sA1, sB1, sA0, sB0);
+    if (kt + 2 >= nk) break;
+    step(kt + 2, sA2, sB2, sA1, sB1);
   }
 
   // ---- epilogue: lane holds rows 4*(l/16)+q, column l%16 of each 16 x 16 tile ----
@@ -192,14 +234,16 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
       if constexpr (MODE == kGateUp) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
+          const int col = ct * 128 + wn * 32 + j * 16 + r16;
+          if (col >= p.N) continue;
           const float g = acc[i][j][q], u = acc[i][j + 2][q];
-          const int col = ct * 64 + wn * 32 + j * 16 + r16;
           p.out_bf16[orow * p.N + col] = f32_to_bf16(g / (1.0f + expf(-g)) * u);
         }
       } else {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int col = ct * kTN + wn * 64 + j * 16 + r16;
+          if (col >= p.N) continue;
           float v = acc[i][j][q];
           if constexpr (MODE == kDense) {
             if (p.bias) v += bf16_to_f32(p.bias[col]);
@@ -222,8 +266,8 @@ extern "C" int sym_gemm_bf16(const void* a, const void* w, const void* bias, con
   SYM_REQUIRE(M >= 0, SYM_ERR_INVALID, "gemm_bf16: M=%d < 0", M);
   if (M == 0) return SYM_OK;
   SYM_REQUIRE(a && w && out, SYM_ERR_INVALID, "gemm_bf16: null pointer argument");
-  SYM_REQUIRE(N > 0 && N % kTN == 0 && N / kTN <= 2147483647, SYM_ERR_UNSUPPORTED,
-              "gemm_bf16: N=%d must be a positive multiple of %d", N, kTN);
+  SYM_REQUIRE(N > 0 && N % 16 == 0, SYM_ERR_UNSUPPORTED,
+              "gemm_bf16: N=%d must be a positive multiple of 16", N);
   SYM_REQUIRE(K > 0 && K % kTK == 0, SYM_ERR_UNSUPPORTED,
               "gemm_bf16: K=%d must be a positive multiple of %d", K, kTK);
   SYM_REQUIRE((M + kTM - 1) / kTM <= 65535, SYM_ERR_UNSUPPORTED, "gemm_bf16: M=%d too large", M);
@@ -238,17 +282,48 @@ extern "C" int sym_gemm_bf16(const void* a, const void* w, const void* bias, con
   p.out_bf16 = out_fp32 ? nullptr : (uint16_t*)out;
   p.out_f32 = out_fp32 ? (float*)out : nullptr;
   (void)hipGetLastError();
-  hipLaunchKernelGGL((gemm_tile_kernel<kDense>), dim3(N / kTN, (M + kTM - 1) / kTM),
+  hipLaunchKernelGGL((gemm_tile_kernel<kDense>), dim3((N + kTN - 1) / kTN, (M + kTM - 1) / kTM),
+                     dim3(kTileThreads), 0, (hipStream_t)stream, p);
+  return sym_host::check_launch("gemm_tile_kernel");
+}
+
+// Router logits for prefill-size T on MFMA. The fp32 gate weight w [E, H] comes as three bf16
+// planes [3, E, H] with w = hi + mid + lo exactly (24 mantissa bits = 3 x 8); x is bf16, so each
+// product x * plane is exact in fp32 and parts[z] = x . plane_z^T (fp32 accumulation) are the
+// three partial logits, summed (hi + mid) + lo by sym_moe_route_permute (n_logit_parts = 3).
+extern "C" int sym_moe_router_logits_split(const void* x, const void* w_planes, int T, int H,
+                                           int E, float* parts, void* stream) {
+  SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "moe_router_logits_split: T=%d < 0", T);
+  if (T == 0) return SYM_OK;
+  SYM_REQUIRE(x && w_planes && parts, SYM_ERR_INVALID,
+              "moe_router_logits_split: null pointer argument");
+  SYM_REQUIRE(E > 0 && E % 16 == 0, SYM_ERR_UNSUPPORTED,
+              "moe_router_logits_split: E=%d must be a positive multiple of 16", E);
+  SYM_REQUIRE(H > 0 && H % kTK == 0, SYM_ERR_UNSUPPORTED,
+              "moe_router_logits_split: H=%d must be a positive multiple of %d", H, kTK);
+  SYM_REQUIRE((T + kTM - 1) / kTM <= 65535, SYM_ERR_UNSUPPORTED,
+              "moe_router_logits_split: T=%d too large", T);
+  TileArgs p{};
+  p.a = (const uint16_t*)x;
+  p.w = (const uint16_t*)w_planes;
+  p.M = T;
+  p.N = E;
+  p.K = H;
+  p.out_f32 = parts;
+  p.w_zstride = (long long)E * H;
+  p.out_zstride = (long long)T * E;
+  (void)hipGetLastError();
+  hipLaunchKernelGGL((gemm_tile_kernel<kDense>), dim3((E + kTN - 1) / kTN, (T + kTM - 1) / kTM, 3),
                      dim3(kTileThreads), 0, (hipStream_t)stream, p);
   return sym_host::check_launch("gemm_tile_kernel");
 }
 
 static int check_grouped(const char* what, int T, int H, int I, int rows, int max_segments) {
   SYM_REQUIRE(T >= 0 && rows >= 0, SYM_ERR_INVALID, "%s: T=%d rows=%d", what, T, rows);
-  SYM_REQUIRE(H > 0 && H % kTN == 0, SYM_ERR_UNSUPPORTED, "%s: H=%d must be a multiple of %d",
-              what, H, kTN);
-  SYM_REQUIRE(I > 0 && I % 64 == 0, SYM_ERR_UNSUPPORTED, "%s: I=%d must be a multiple of 64",
-              what, I);
+  SYM_REQUIRE(H > 0 && H % kTK == 0, SYM_ERR_UNSUPPORTED, "%s: H=%d must be a multiple of %d",
+              what, H, kTK);
+  SYM_REQUIRE(I > 0 && I % kTK == 0, SYM_ERR_UNSUPPORTED, "%s: I=%d must be a multiple of %d",
+              what, I, kTK);
   SYM_REQUIRE(max_segments >= 1 && max_segments <= kMaxGemmSegments, SYM_ERR_INVALID,
               "%s: max_segments=%d out of range", what, max_segments);
   SYM_REQUIRE((long long)rows / kTM + max_segments <= 65535, SYM_ERR_UNSUPPORTED,
@@ -266,7 +341,6 @@ extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int row
   SYM_REQUIRE(x && sorted_tokens && seg_expert && seg_offset && seg_count && n_segments &&
                   w_gate_up && h,
               SYM_ERR_INVALID, "moe_gate_up_tiled: null pointer argument");
-  SYM_REQUIRE(H % kTK == 0, SYM_ERR_UNSUPPORTED, "moe_gate_up_tiled: H=%d", H);
   TileArgs p{};
   p.a = (const uint16_t*)x;
   p.w = (const uint16_t*)w_gate_up;
@@ -280,8 +354,9 @@ extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int row
   p.K = H;
   p.out_bf16 = (uint16_t*)h;
   (void)hipGetLastError();
-  hipLaunchKernelGGL((gemm_tile_kernel<kGateUp>), dim3(I / 64, rows / kTM + max_segments),
-                     dim3(kTileThreads), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL((gemm_tile_kernel<kGateUp>),
+                     dim3((I + 127) / 128, rows / kTM + max_segments), dim3(kTileThreads), 0,
+                     (hipStream_t)stream, p);
   return sym_host::check_launch("gemm_tile_kernel");
 }
 
@@ -305,7 +380,8 @@ extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
   p.K = I;
   p.out_f32 = y;
   (void)hipGetLastError();
-  hipLaunchKernelGGL((gemm_tile_kernel<kDown>), dim3(H / kTN, rows / kTM + max_segments),
-                     dim3(kTileThreads), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL((gemm_tile_kernel<kDown>),
+                     dim3((H + kTN - 1) / kTN, rows / kTM + max_segments), dim3(kTileThreads), 0,
+                     (hipStream_t)stream, p);
   return sym_host::check_launch("gemm_tile_kernel");
 }

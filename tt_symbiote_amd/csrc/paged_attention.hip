@@ -230,7 +230,8 @@ __global__ __launch_bounds__(256) void paged_kv_fill_kernel(
 //   v_mfma_f32_16x16x32_bf16 (query heads are rows 0..G-1 of the A operand; lane l streams
 //   dims 8*(l/16) + 32*j of token l%16, so one wave-wide load covers 64 contiguous bytes of 16
 //   K rows). P.V on the VALU: a lane owns 8 dims of one token per step (16 lanes per token).
-//   All K and V loads of the wave are issued before the first use.
+//   All K loads of the wave are issued before the first use, and all V loads right after the
+//   scores (the softmax statistics are reduced while they arrive).
 // Each split writes its unnormalised output and (max, sum) in the log2 domain for the merge
 // kernel; a sequence with a single split writes its normalised output directly. (Merging in the
 // last split to finish would need a device-scope release per workgroup; on this chip that
@@ -361,13 +362,11 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
 #pragma unroll
     for (int j = 0; j < 4; ++j) kb[tt][j] = *reinterpret_cast<const uint4*>(kr + 32 * j);
   }
-  // V for P.V: step it covers tokens it*4 + kg (4 per step), lane r16 owns dims r16*8 .. +8
+  // V is loaded after the scores, into the registers K used: holding K and V together takes 164
+  // VGPRs (3 workgroups per CU), V late 124 VGPRs (4 per CU; 2 us faster at batch 32)
   uint4 vreg[VS];
-#pragma unroll
-  for (int it = 0; it < VS; ++it)
-    vreg[it] = *reinterpret_cast<const uint4*>(v_pool + row_offset(wt0 + it * 4 + kg) + r16 * 8);
   if constexpr (FUSED) {
-    // QK-norm + RoPE of this wave's heads (K/V loads in flight), into LDS; the writer also
+    // QK-norm + RoPE of this wave's heads (K loads in flight), into LDS; the writer also
     // stores k and v into the pool slot of the new token
 #pragma unroll
     for (int jj = 0; jj < JPW; ++jj) {
@@ -401,8 +400,9 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
       qa[j] = r16 < G ? v : make_uint4(0, 0, 0, 0);
     }
   }
-  if (FUSED && writer && pos < t1) {
-    // the new token's rows come from LDS (the pool slot is being written by this workgroup)
+  // the new token's rows come from LDS (the pool slot is being written by this workgroup)
+  const bool patch_new = FUSED && writer && pos < t1;
+  if (patch_new) {
     const int tn = pos - t0;
 #pragma unroll
     for (int tt = 0; tt < KT; ++tt)
@@ -410,9 +410,6 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           kb[tt][j] = *reinterpret_cast<const uint4*>(&s_new[0][8 * kg + 32 * j]);
-#pragma unroll
-    for (int it = 0; it < VS; ++it)
-      if (wt0 + it * 4 + kg == tn) vreg[it] = *reinterpret_cast<const uint4*>(&s_new[1][r16 * 8]);
   }
 
   // ---- scores on MFMA ----
@@ -428,6 +425,17 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
       const int h = 4 * kg + i;
       if (h < G) s_p[h][tl] = valid ? sacc[i] * scale_log2 : -INFINITY;
     }
+  }
+  // V for P.V: step it covers tokens it*4 + kg (4 per step), lane r16 owns dims r16*8 .. +8;
+  // it arrives while the softmax statistics are reduced
+#pragma unroll
+  for (int it = 0; it < VS; ++it)
+    vreg[it] = *reinterpret_cast<const uint4*>(v_pool + row_offset(wt0 + it * 4 + kg) + r16 * 8);
+  if (patch_new) {
+    const int tn = pos - t0;
+#pragma unroll
+    for (int it = 0; it < VS; ++it)
+      if (wt0 + it * 4 + kg == tn) vreg[it] = *reinterpret_cast<const uint4*>(&s_new[1][r16 * 8]);
   }
   __syncthreads();
 

@@ -131,8 +131,9 @@ class HIPBailingMoE(StatelessHIPModule):
         if self.weight_format == "fp8_e4m3":
             gate_up = hip_ops.quantize_block_fp8(gate_up)
             down = hip_ops.quantize_block_fp8(down)
+        gate_w = h["gate_w"].detach().float().contiguous()
         self._host = dict(
-            gate_w=h["gate_w"].detach().float().contiguous(),
+            gate_w=gate_w, gate_w_planes=hip_ops.split_router_weight(gate_w),
             bias=h["bias"].detach().float().contiguous(),
             gate_up=gate_up, down=down)
         return super().preprocess_weights_impl()
@@ -151,8 +152,12 @@ class HIPBailingMoE(StatelessHIPModule):
         return super().deallocate_weights_impl()
 
     def route(self, x: torch.Tensor) -> hip_ops.RouteResult:
-        """Router logits (fp32 MFMA) + fused top-k/permute for tokens x [T, H] (bf16)."""
-        logits = hip_ops.moe_router_logits(x, self._dev["gate_w"])
+        """Router logits (fp32 MFMA, or for many tokens bf16 MFMA tiles over the exact
+        three-plane split of the fp32 gate weight) + fused top-k/permute for x [T, H] (bf16)."""
+        if x.shape[0] >= hip_ops.ROUTER_SPLIT_MIN_TOKENS:
+            logits = hip_ops.moe_router_logits_split(x, self._dev["gate_w_planes"])
+        else:
+            logits = hip_ops.moe_router_logits(x, self._dev["gate_w"])
         return hip_ops.moe_route_permute(
             logits, self._dev["bias"], n_group=self.n_group, topk_group=self.topk_group,
             top_k=self.top_k, routed_scale=self.routed_scaling_factor, renormalize=True,
