@@ -558,15 +558,16 @@ def test_decode_step_matches_prologue_then_decode(device, B, Hq, Hkv, rd, use_no
     assert not bool(out[0].any())                    # no position: zero output
 
 
-@pytest.mark.parametrize("lens,Hq,Hkv", [
-    ([1, 5, 64, 127, 128, 129, 300], 16, 4),
-    ([200, 77], 8, 8),
-    ([513], 16, 2),
+@pytest.mark.parametrize("lens,Hq,Hkv,qscale", [
+    ([1, 5, 64, 127, 128, 129, 300], 16, 4, 1.0),
+    ([200, 77], 8, 8, 1.0),
+    ([513], 16, 2, 1.0),
+    ([1500, 37], 16, 4, 4.0),     # many key blocks, peaked softmax (frequent max changes)
 ])
-def test_prefill_attention(device, lens, Hq, Hkv):
+def test_prefill_attention(device, lens, Hq, Hkv, qscale):
     g = torch.Generator().manual_seed(sum(lens) + Hq)
     T = sum(lens)
-    q = torch.randn(T, Hq, 128, generator=g).bfloat16()
+    q = (torch.randn(T, Hq, 128, generator=g) * qscale).bfloat16()
     k = torch.randn(T, Hkv, 128, generator=g).bfloat16()
     v = torch.randn(T, Hkv, 128, generator=g).bfloat16()
     cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32)

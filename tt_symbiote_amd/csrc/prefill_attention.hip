@@ -7,12 +7,15 @@
 // cu_seqlens (positions 0 .. L-1 of each sequence).
 //
 // Attention design (gfx950): one workgroup of 4 waves per (128-query block, query head,
-// sequence); each wave owns 32 query rows (two 16-row MFMA tiles) and keeps its Q fragments in
-// registers. Key blocks of 64 tokens are staged in LDS (K row-major, V transposed so the
-// P.V operand reads 16 contiguous bytes); S = Q K^T and O += P V run on
-// v_mfma_f32_16x16x32_bf16; the online softmax (log2 domain) reduces each row over the 16
-// lanes that hold it with xor shuffles; P goes through a per-wave LDS tile from the MFMA output
-// layout to the operand layout. Only key blocks at or before the query block are visited.
+// sequence); each wave owns 32 queries (two 16-query tiles) and keeps its Q fragments in
+// registers. Key blocks of 64 tokens are staged in LDS (K row-major, V transposed). The wave
+// computes the transposed scores S^T = K Q^T on v_mfma_f32_16x16x32_bf16, so a lane holds 16
+// keys of one query per tile: the online softmax (log2 domain) reduces a query over the lane's
+// own values and two xor shuffles, and the exponentiated scores, packed to bf16, are already the
+// B operand of O^T += V^T P^T (the MFMA's k index is free to follow the score layout: lane group
+// kq takes keys 4kq .. 4kq+3 of two adjacent 16-key tiles, and reads the matching V^T columns as
+// two 8-byte pieces). Only key blocks at or before the query block are visited, and only the
+// blocks that cross the diagonal or the sequence end are masked.
 #include "common.h"
 
 namespace sym {
@@ -21,18 +24,49 @@ constexpr int kPD = 128;           // head dim
 constexpr int kPQ = 128;           // queries per workgroup
 constexpr int kPK = 64;            // keys per block
 constexpr int kPKStride = kPD + 8; // LDS row stride of K (elements)
-constexpr int kPVStride = kPK + 8; // LDS row stride of transposed V
-constexpr int kPPStride = kPK + 8; // LDS row stride of a wave's P tile
+constexpr int kPVStride = kPK + 4; // LDS row stride of V^T: 34 dwords, so the 16 rows of an
+                                   // 8-byte fragment read start in distinct bank pairs
 
-__global__ __launch_bounds__(256) void prefill_attention_kernel(
+// 16 bytes as a native vector (an array of these stays in registers across the key-block loop;
+// one of HIP's uint4 struct was left in scratch memory)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Loads of one key block (keys k0 .. k0+63 of a sequence, clamped to its last key L-1) for the
+// staging below: kreg[j] = K chunk (idx%16) of key idx/16, vreg[i][u] = V chunk idx/32 of key
+// 2(idx%32)+u, with idx = tid + 256j (resp. 256i). k / v point at the sequence's first token of
+// this kv head.
+__device__ __forceinline__ void load_kv_block(const uint16_t* __restrict__ k,
+                                              const uint16_t* __restrict__ v, int Hkv, int L,
+                                              int k0, int tid, u32x4 (&kreg)[4],
+                                              u32x4 (&vreg)[2][2]) {
+  const size_t row = (size_t)Hkv * kPD;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int idx = tid + 256 * j;
+    const int kr = min(k0 + (idx >> 4), L - 1);
+    kreg[j] = *reinterpret_cast<const u32x4*>(k + kr * row + (idx & 15) * 8);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int idx = tid + 256 * i;
+    const int p = idx & 31, c = idx >> 5;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int kr = min(k0 + 2 * p + u, L - 1);
+      vreg[i][u] = *reinterpret_cast<const u32x4*>(v + kr * row + c * 8);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const int32_t* __restrict__ cu_seqlens, int Hq, int Hkv,
     float scale_log2, uint16_t* __restrict__ out) {
   __shared__ __align__(16) uint16_t sK[kPK * kPKStride];
   __shared__ __align__(16) uint16_t sVt[kPD * kPVStride];
-  __shared__ __align__(16) uint16_t sP[4][32 * kPPStride];
 
-  const int qb = blockIdx.x, h = blockIdx.y, sq = blockIdx.z;
+  // the last query blocks (the most key blocks under the causal mask) are dispatched first
+  const int qb = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, sq = blockIdx.z;
   const int s0 = cu_seqlens[sq];
   const int L = cu_seqlens[sq + 1] - s0;
   const int q0 = qb * kPQ;
@@ -41,53 +75,65 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int r16 = lane & 15, kq = lane >> 4;
 
-  // Q fragments (A operand): row tile t, query q0 + wave*32 + t*16 + r16 (clamped), dims
-  // 8*kq + 32*c
-  uint4 qa[2][4];
+  // Q fragments (B operand of S^T): column r16 = query q0 + wave*32 + t*16 + r16 (clamped),
+  // dims 8*kq + 32*c
+  const int wq0 = q0 + wave * 32;
+  int qrow[2];
+  uint4 qf[2][4];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    const int qi = min(q0 + wave * 32 + t * 16 + r16, L - 1);
+    qrow[t] = wq0 + t * 16 + r16;
+    const int qi = min(qrow[t], L - 1);
     const uint16_t* qr = q + ((size_t)(s0 + qi) * Hq + h) * kPD + 8 * kq;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) qa[t][c] = *reinterpret_cast<const uint4*>(qr + 32 * c);
+    for (int c = 0; c < 4; ++c) qf[t][c] = *reinterpret_cast<const uint4*>(qr + 32 * c);
   }
+  // O^T: lane holds dims d*16 + 4*kq + i of its query (tile t)
   floatx4 o[2][8];
 #pragma unroll
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[t][d] = floatx4{0.f, 0.f, 0.f, 0.f};
-  // running max / sum of the 4 rows 4*kq + i of each row tile (identical in the 16 lanes of a
-  // row group)
-  float m[2][4], l[2][4];
-#pragma unroll
-  for (int t = 0; t < 2; ++t)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      m[t][i] = -INFINITY;
-      l[t][i] = 0.f;
-    }
+  // running max (log2 domain) / sum of the lane's query (the same in its 4 lanes r16 + 16*kq)
+  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
 
   const int q_last = min(q0 + kPQ, L) - 1;
   const int nkb = q_last / kPK + 1;
+  // Staging of a key block (keys k0 .. k0+63, rows past the sequence clamped to its last):
+  //   K: item j = tid + 256j is (key idx/16, 16-byte chunk idx%16), stored row-major;
+  //   V: item i = tid + 256i is (key pair p = idx%32, chunk c = idx/32): the chunk of keys 2p and
+  //      2p+1 is transposed into 8 dwords (dim c*8+e: key 2p in the low half, 2p+1 in the high
+  //      half), so the 32 lanes of a pair-row write 128 contiguous bytes of sVt (no bank
+  //      conflicts).
+  //   The next block's K / V are loaded into registers while the current block computes.
+  u32x4 kreg[4], vreg[2][2];
+  const uint16_t* kbase = k + ((size_t)s0 * Hkv + g) * kPD;
+  const uint16_t* vbase = v + ((size_t)s0 * Hkv + g) * kPD;
+  load_kv_block(kbase, vbase, Hkv, L, 0, tid, kreg, vreg);
   for (int kb = 0; kb < nkb; ++kb) {
     const int k0 = kb * kPK;
-    // ---- stage K (row-major) and V (transposed) of keys k0 .. k0+63 (clamped rows) ----
-    __syncthreads();
+    __syncthreads();  // every wave is done with the previous block's K / V^T
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int idx = tid + 256 * j;        // 64 keys x 16 chunks of 8 dims
-      const int key = idx >> 4, ch = idx & 15;
-      const int kr = min(k0 + key, L - 1);
-      const size_t src = ((size_t)(s0 + kr) * Hkv + g) * kPD + ch * 8;
-      *reinterpret_cast<uint4*>(&sK[key * kPKStride + ch * 8]) =
-          *reinterpret_cast<const uint4*>(k + src);
-      const uint4 vv = *reinterpret_cast<const uint4*>(v + src);
-      const uint16_t* ve = reinterpret_cast<const uint16_t*>(&vv);
+      const int idx = tid + 256 * j;
+      *reinterpret_cast<u32x4*>(&sK[(idx >> 4) * kPKStride + (idx & 15) * 8]) = kreg[j];
+    }
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sVt[(ch * 8 + e) * kPVStride + key] = ve[e];
+    for (int i = 0; i < 2; ++i) {
+      const int idx = tid + 256 * i;
+      const int p = idx & 31, c = idx >> 5;
+      const u32x4 a = vreg[i][0], b = vreg[i][1];
+      uint32_t* dst = reinterpret_cast<uint32_t*>(&sVt[(c * 8) * kPVStride + 2 * p]);
+#pragma unroll
+      for (int mm = 0; mm < 4; ++mm) {
+        // dims 2mm (low halves) and 2mm+1 (high halves) of keys 2p (low) and 2p+1 (high)
+        dst[(2 * mm) * (kPVStride / 2)] = __builtin_amdgcn_perm(b[mm], a[mm], 0x05040100u);
+        dst[(2 * mm + 1) * (kPVStride / 2)] = __builtin_amdgcn_perm(b[mm], a[mm], 0x07060302u);
+      }
     }
     __syncthreads();
-    // ---- S = Q K^T for this wave's 32 rows x 64 keys ----
+    if (kb + 1 < nkb) load_kv_block(kbase, vbase, Hkv, L, k0 + kPK, tid, kreg, vreg);
+    // ---- S^T = K Q^T: lane holds keys k0 + 16j + 4*kq + i of query qrow[t] ----
     floatx4 sc[2][4];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -95,88 +141,92 @@ __global__ __launch_bounds__(256) void prefill_attention_kernel(
       for (int j = 0; j < 4; ++j) sc[t][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      uint4 kbf[4];
+      uint4 kf[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        kbf[j] = *reinterpret_cast<const uint4*>(&sK[(j * 16 + r16) * kPKStride + 8 * kq + 32 * c]);
+        kf[j] = *reinterpret_cast<const uint4*>(&sK[(j * 16 + r16) * kPKStride + 8 * kq + 32 * c]);
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sc[t][j] = mfma16x16x32(qa[t][c], kbf[j], sc[t][j]);
+        for (int j = 0; j < 4; ++j) sc[t][j] = mfma16x16x32(kf[j], qf[t][c], sc[t][j]);
     }
-    // ---- online softmax: lane holds rows 4*kq + i, key column j*16 + r16 ----
+    // keys past a query of this wave (the diagonal) or past the sequence are masked
+    const bool masked = k0 + kPK - 1 > wq0 || k0 + kPK > L;
+    uint4 pf[2][2];  // P^T operands: [t][32-key chunk]
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int qi = q0 + wave * 32 + t * 16 + 4 * kq + i;
-        float x[4];
-        float mx = -INFINITY;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int kj = k0 + j * 16 + r16;
-          x[j] = (kj <= qi && kj < L) ? sc[t][j][i] * scale_log2 : -INFINITY;
-          mx = fmaxf(mx, x[j]);
-        }
-        mx = fmaxf(mx, __shfl_xor(mx, 1));
-        mx = fmaxf(mx, __shfl_xor(mx, 2));
-        mx = fmaxf(mx, __shfl_xor(mx, 4));
-        mx = fmaxf(mx, __shfl_xor(mx, 8));
-        const float mn = fmaxf(m[t][i], mx);
-        const float alpha = mn == -INFINITY ? 1.f : exp2f(m[t][i] - mn);
-        float rs = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float pj = mn == -INFINITY ? 0.f : exp2f(x[j] - mn);
-          x[j] = pj;
-          rs += pj;
-        }
-        rs += __shfl_xor(rs, 1);
-        rs += __shfl_xor(rs, 2);
-        rs += __shfl_xor(rs, 4);
-        rs += __shfl_xor(rs, 8);
-        m[t][i] = mn;
-        l[t][i] = l[t][i] * alpha + rs;
-#pragma unroll
-        for (int d = 0; d < 8; ++d) o[t][d][i] *= alpha;
-        // P (bf16) into this wave's LDS tile: row t*16 + 4*kq + i, key j*16 + r16
+      if (masked) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-          sP[wave][(t * 16 + 4 * kq + i) * kPPStride + j * 16 + r16] = f32_to_bf16(x[j]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int key = k0 + 16 * j + 4 * kq + i;
+            if (key > qrow[t] || key >= L) sc[t][j][i] = -INFINITY;
+          }
       }
+      float mx = sc[t][0][0];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[t][j][i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // key 0 of block 0 is visible to every query, so mn is finite from the first block on
+      const float mn = fmaxf(m[t], mx * scale_log2);
+      const float alpha = exp2f(m[t] - mn);
+      float rs = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pj = exp2f(fmaf(sc[t][j][i], scale_log2, -mn));
+          sc[t][j][i] = pj;
+          rs += pj;
+        }
+      rs += __shfl_xor(rs, 16);
+      rs += __shfl_xor(rs, 32);
+      m[t] = mn;
+      l[t] = l[t] * alpha + rs;
+      if (__any(alpha != 1.f)) {
+#pragma unroll
+        for (int d = 0; d < 8; ++d)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[t][d][i] *= alpha;
+      }
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc)
+        pf[t][cc] = make_uint4(pack_bf16x2(sc[t][2 * cc][0], sc[t][2 * cc][1]),
+                               pack_bf16x2(sc[t][2 * cc][2], sc[t][2 * cc][3]),
+                               pack_bf16x2(sc[t][2 * cc + 1][0], sc[t][2 * cc + 1][1]),
+                               pack_bf16x2(sc[t][2 * cc + 1][2], sc[t][2 * cc + 1][3]));
     }
-    // P is written and read by different lanes of this wave: the wavefront-scope fence keeps
-    // the compiler from moving the reads above the writes (a wave's LDS operations run in order)
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-    // ---- O += P V (P rows as A: row r16, keys 8*kq + 32*c; V^T rows as B) ----
+    // ---- O^T += V^T P^T: A = V^T rows d*16 + r16, keys 32cc + 4kq + {0..3, 16..19} ----
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      uint4 pa[2], vb[8];
+    for (int cc = 0; cc < 2; ++cc) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-        pa[t] = *reinterpret_cast<const uint4*>(&sP[wave][(t * 16 + r16) * kPPStride + 8 * kq + 32 * c]);
+      for (int d = 0; d < 8; ++d) {
+        const uint16_t* vr = &sVt[(d * 16 + r16) * kPVStride + 32 * cc + 4 * kq];
+        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+        const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
-      for (int d = 0; d < 8; ++d)
-        vb[d] = *reinterpret_cast<const uint4*>(&sVt[(d * 16 + r16) * kPVStride + 8 * kq + 32 * c]);
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int d = 0; d < 8; ++d) o[t][d] = mfma16x16x32(pa[t], vb[d], o[t][d]);
+        for (int t = 0; t < 2; ++t) o[t][d] = mfma16x16x32(vf, pf[t][cc], o[t][d]);
+      }
     }
   }
-  // ---- normalise and store: lane holds rows 4*kq + i, dim d*16 + r16 ----
+  // ---- normalise and store: lane holds dims d*16 + 4*kq + i of query qrow[t] ----
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int t = 0; t < 2; ++t) {
+    if (qrow[t] < L) {
+      const float inv = l[t] > 0.f ? 1.f / l[t] : 0.f;
+      uint16_t* orow = out + ((size_t)(s0 + qrow[t]) * Hq + h) * kPD + 4 * kq;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int qi = q0 + wave * 32 + t * 16 + 4 * kq + i;
-      if (qi < L) {
-        const float inv = l[t][i] > 0.f ? 1.f / l[t][i] : 0.f;
-        uint16_t* orow = out + ((size_t)(s0 + qi) * Hq + h) * kPD;
-#pragma unroll
-        for (int d = 0; d < 8; ++d) orow[d * 16 + r16] = f32_to_bf16(o[t][d][i] * inv);
-      }
+      for (int d = 0; d < 8; ++d)
+        *reinterpret_cast<uint2*>(orow + d * 16) =
+            make_uint2(pack_bf16x2(o[t][d][0] * inv, o[t][d][1] * inv),
+                       pack_bf16x2(o[t][d][2] * inv, o[t][d][3] * inv));
     }
+  }
 }
 
 }  // namespace sym
