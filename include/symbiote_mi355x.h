@@ -348,7 +348,8 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
  * sym_moe_gate_up_tiled / sym_moe_down_tiled: the grouped expert GEMMs of sym_moe_gate_up /
  *   sym_moe_down (same arguments and results; TTNNExperts.forward, ttnn_moe.py:1250-1289) for
  *   segments of many rows; rows = total rows of the segment list (T*top_k + T with the shared
- *   expert). H % 64 == 0, I % 64 == 0.
+ *   expert). y is fp32, or bf16 when y_bf16 != 0 (half the bytes written here and read back by
+ *   sym_moe_unpermute_combine). H % 64 == 0, I % 64 == 0.
  */
 int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
                   int N, int K, void* out, int out_fp32, void* stream);
@@ -359,8 +360,8 @@ int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int rows,
                           void* h, void* stream);
 int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows, const int32_t* seg_expert,
                        const int32_t* seg_offset, const int32_t* seg_count,
-                       const int32_t* n_segments, int max_segments, const void* w_down, float* y,
-                       void* stream);
+                       const int32_t* n_segments, int max_segments, const void* w_down, void* y,
+                       int y_bf16, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Model ends of greedy generation (the embedding and final-norm swap of TTNNBailingMoeV2Model,
@@ -392,11 +393,12 @@ int sym_greedy_advance(const int32_t* ids, int B, int32_t* positions, int32_t* h
  *   out[t] = bf16( sum_k topk_w[t,k] * y[inv_perm[t,k]]  (k ascending)
  *                  + (shared_row0 >= 0 ? y[shared_row0 + t] : 0)
  *                  + (residual ? residual[t] : 0) )
+ *   y fp32, or bf16 when y_bf16 != 0 (widened exactly; the sum is fp32 either way);
  *   out [T, H] bf16; residual [T, H] fp32 (the residual stream) or NULL. H % 8 == 0.
  */
-int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm, const float* topk_w, int T,
-                              int top_k, int H, int shared_row0, const float* residual, void* out,
-                              void* stream);
+int sym_moe_unpermute_combine(const void* y, int y_bf16, const int32_t* inv_perm,
+                              const float* topk_w, int T, int top_k, int H, int shared_row0,
+                              const float* residual, void* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Streaming-read bandwidth probe (measurement only; no counterpart in the reference): reads

@@ -314,6 +314,12 @@ def test_grouped_swiglu(device, T, E, H, I, top_k, skew, kernel):
         _close(hk[rows], h_ref, atol=2e-3, rtol=8e-3)
         y_ref = hk[rows].float() @ wd[e].float().T
         torch.testing.assert_close(yk[rows], y_ref, rtol=1e-4, atol=1e-4)
+    if kernel == "tiled":
+        # bf16 y: the same fp32 results, rounded once to bf16 (round to nearest even)
+        _, yb = hip_ops.moe_grouped_swiglu(x.to(device), res, wgu.to(device), wd.to(device),
+                                           kernel=kernel, y_dtype=torch.bfloat16)
+        assert yb.dtype == torch.bfloat16
+        assert torch.equal(yb.cpu(), yk.bfloat16())
 
 
 @pytest.mark.parametrize("M,N,K,bias,res,out_dtype", [
@@ -356,6 +362,12 @@ def test_combine(device):
     _close(out, ref, atol=1e-2, rtol=8e-3)
     out2 = hip_ops.moe_unpermute_combine(y, res)
     _close(out2, (yc[inv] * w[..., None]).sum(1) + yc[T * K:T * K + T], atol=1e-2, rtol=8e-3)
+    # bf16 y: widened exactly, summed in fp32 as above
+    yb = y.bfloat16()
+    out3 = hip_ops.moe_unpermute_combine(yb, res, residual=resid.to(device))
+    ybc = yb.cpu().float()
+    ref3 = (ybc[inv] * w[..., None]).sum(1) + ybc[T * K:T * K + T] + resid
+    _close(out3, ref3, atol=1e-2, rtol=8e-3)
 
 
 # ------------------------------------------------------------------------------- attention

@@ -109,7 +109,7 @@ _SIGNATURES = {
         _c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp, _vp]
     ),
     "sym_moe_unpermute_combine": (
-        _c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]
+        _c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]
     ),
     "sym_hbm_read_probe": (_c_int, [_vp, _c_size, _vp, _vp]),
     "sym_attn_prefill_prologue": (
@@ -128,7 +128,7 @@ _SIGNATURES = {
     ),
     "sym_moe_down_tiled": (
         _c_int,
-        [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp],
+        [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _c_int, _vp],
     ),
 }
 

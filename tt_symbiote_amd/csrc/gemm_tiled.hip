@@ -18,7 +18,7 @@
 //   GATE_UP: rows of a segment gather x[sorted_tokens[row]]; the B tile holds 128 gate rows and
 //            the matching 128 up rows of the expert, so each wave's block pairs 32 gate with 32
 //            up columns and the epilogue writes h = silu(gate) * up (bf16).
-//   DOWN:    rows of a segment are h rows (contiguous); y = h . W_down^T (fp32).
+//   DOWN:    rows of a segment are h rows (contiguous); y = h . W_down^T (fp32 or bf16).
 // Rows past a tile's valid rows and columns past N repeat the last row / column in the loads
 // (always in bounds) and are not stored.
 // Grouped modes: the workgroup's row tile is found from the device-side segment list (each
@@ -363,7 +363,8 @@ extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int row
 extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
                                   const int32_t* seg_expert, const int32_t* seg_offset,
                                   const int32_t* seg_count, const int32_t* n_segments,
-                                  int max_segments, const void* w_down, float* y, void* stream) {
+                                  int max_segments, const void* w_down, void* y, int y_bf16,
+                                  void* stream) {
   int rc = check_grouped("moe_down_tiled", T, H, I, rows, max_segments);
   if (rc || rows == 0 || T == 0) return rc;
   SYM_REQUIRE(h && seg_expert && seg_offset && seg_count && n_segments && w_down && y,
@@ -378,7 +379,8 @@ extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
   p.M = rows;
   p.N = H;
   p.K = I;
-  p.out_f32 = y;
+  if (y_bf16) p.out_bf16 = (uint16_t*)y;
+  else p.out_f32 = (float*)y;
   (void)hipGetLastError();
   hipLaunchKernelGGL((gemm_tile_kernel<kDown>),
                      dim3((H + kTN - 1) / kTN, rows / kTM + max_segments), dim3(kTileThreads), 0,

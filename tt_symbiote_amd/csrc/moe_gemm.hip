@@ -442,8 +442,19 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_fp8_kernel(
   }
 }
 
+// 8 consecutive values of a y row (fp32, or bf16 widened exactly)
+__device__ __forceinline__ void load_y8(const float* p, float (&f)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ void load_y8(const uint16_t* p, float (&f)[8]) {
+  unpack8(*reinterpret_cast<const uint4*>(p), f);
+}
+
+template <typename YT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
-    const float* __restrict__ y, const int32_t* __restrict__ inv_perm,
+    const YT* __restrict__ y, const int32_t* __restrict__ inv_perm,
     const float* __restrict__ topk_w, int K, int H, int shared_row0,
     const float* __restrict__ residual, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
@@ -454,16 +465,16 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
     for (int k = 0; k < K; ++k) {
       const int row = inv_perm[(size_t)t * K + k];
       const float wk = topk_w[(size_t)t * K + k];
-      const float4* yp = reinterpret_cast<const float4*>(y + (size_t)row * H + c);
-      const float4 f0 = yp[0], f1 = yp[1];
-      acc[0] += wk * f0.x; acc[1] += wk * f0.y; acc[2] += wk * f0.z; acc[3] += wk * f0.w;
-      acc[4] += wk * f1.x; acc[5] += wk * f1.y; acc[6] += wk * f1.z; acc[7] += wk * f1.w;
+      float f[8];
+      load_y8(y + (size_t)row * H + c, f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += wk * f[i];
     }
     if (shared_row0 >= 0) {
-      const float4* yp = reinterpret_cast<const float4*>(y + (size_t)(shared_row0 + t) * H + c);
-      const float4 f0 = yp[0], f1 = yp[1];
-      acc[0] += f0.x; acc[1] += f0.y; acc[2] += f0.z; acc[3] += f0.w;
-      acc[4] += f1.x; acc[5] += f1.y; acc[6] += f1.z; acc[7] += f1.w;
+      float f[8];
+      load_y8(y + (size_t)(shared_row0 + t) * H + c, f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += f[i];
     }
     if (residual) {
       const float4* rp = reinterpret_cast<const float4*>(residual + (size_t)t * H + c);
@@ -565,7 +576,7 @@ extern "C" int sym_moe_grouped_swiglu(const void* x, int T, int H, int I,
                       w_down, y, stream);
 }
 
-extern "C" int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm,
+extern "C" int sym_moe_unpermute_combine(const void* y, int y_bf16, const int32_t* inv_perm,
                                          const float* topk_w, int T, int top_k, int H,
                                          int shared_row0, const float* residual, void* out,
                                          void* stream) {
@@ -578,8 +589,14 @@ extern "C" int sym_moe_unpermute_combine(const float* y, const int32_t* inv_perm
   SYM_REQUIRE(top_k >= 1 && top_k <= 64, SYM_ERR_INVALID, "moe_unpermute_combine: top_k=%d",
               top_k);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(moe_combine_kernel, dim3(T), dim3(256), 0, (hipStream_t)stream, y, inv_perm,
-                     topk_w, top_k, H, shared_row0, residual, (uint16_t*)out);
+  if (y_bf16)
+    hipLaunchKernelGGL(moe_combine_kernel<uint16_t>, dim3(T), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)y, inv_perm, topk_w, top_k, H, shared_row0, residual,
+                       (uint16_t*)out);
+  else
+    hipLaunchKernelGGL(moe_combine_kernel<float>, dim3(T), dim3(256), 0, (hipStream_t)stream,
+                       (const float*)y, inv_perm, topk_w, top_k, H, shared_row0, residual,
+                       (uint16_t*)out);
   return sym_host::check_launch("moe_combine_kernel");
 }
 

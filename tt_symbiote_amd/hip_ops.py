@@ -833,12 +833,14 @@ def quantize_block_fp8(w: torch.Tensor) -> BlockFp8:
 
 def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
                        w_down, h: Optional[torch.Tensor] = None,
-                       y: Optional[torch.Tensor] = None, kernel: str = "auto"):
+                       y: Optional[torch.Tensor] = None, kernel: str = "auto",
+                       y_dtype: torch.dtype = torch.float32):
     """h = silu(x Wg^T) * (x Wu^T), y = h Wd^T per segment; returns (h [rows, I], y [rows, H]).
     The weights are bf16 tensors, or BlockFp8 (fp8 e4m3fn + 128 x 128 block scales, dequantized
     in the kernel). ``kernel``: "stream" (weight-streaming kernels for decode-size segments),
-    "tiled" (128 x 128 MFMA tiles for prefill-size segments, bf16 only) or "auto" (tiled from
-    TILED_MIN_TOKENS tokens with bf16 weights)."""
+    "tiled" (128 x 256 MFMA tiles for prefill-size segments, bf16 only) or "auto" (tiled from
+    TILED_MIN_TOKENS tokens with bf16 weights). ``y_dtype``: fp32, or bf16 with the tiled kernels
+    (half the bytes of y written and read back by the combine)."""
     _check(x, "x", torch.bfloat16)
     if x.dim() != 2:
         raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
@@ -870,15 +872,20 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
     rows = route.rows
     if h is None:
         h = torch.empty(rows, I, dtype=torch.bfloat16, device=dev)
-    if y is None:
-        y = torch.empty(rows, H, dtype=torch.float32, device=dev)
-    _check(h, "h", torch.bfloat16, dev)
-    _check_shape(h, "h", (rows, I))
-    _check(y, "y", torch.float32, dev)
-    _check_shape(y, "y", (rows, H))
-    stream = _stream()
     if kernel not in ("auto", "stream", "tiled"):
         raise ValueError(f"kernel {kernel!r}")
+    tiled = not fp8 and (kernel == "tiled" or (kernel == "auto" and T >= TILED_MIN_TOKENS))
+    if y_dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"y_dtype {y_dtype} (fp32 or bf16)")
+    if y_dtype == torch.bfloat16 and not tiled:
+        raise ValueError("a bf16 y needs the tiled kernels")
+    if y is None:
+        y = torch.empty(rows, H, dtype=y_dtype, device=dev)
+    _check(h, "h", torch.bfloat16, dev)
+    _check_shape(h, "h", (rows, I))
+    _check(y, "y", y_dtype, dev)
+    _check_shape(y, "y", (rows, H))
+    stream = _stream()
     if fp8:
         if kernel == "tiled":
             raise NotImplementedError("fp8 expert weights: only the streaming kernels")
@@ -892,7 +899,6 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
             _ptr(route.seg_count), _ptr(route.n_segments), max_segments, _ptr(w_down),
             _ptr(s_down), _ptr(y), stream))
         return h, y
-    tiled = kernel == "tiled" or (kernel == "auto" and T >= TILED_MIN_TOKENS)
     if tiled:
         _timed("moe_gate_up", lambda: _lib.call(
             "sym_moe_gate_up_tiled", _ptr(x), T, H, I, rows, _ptr(route.sorted_tokens),
@@ -901,7 +907,7 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
         _timed("moe_down", lambda: _lib.call(
             "sym_moe_down_tiled", _ptr(h), T, H, I, rows, _ptr(route.seg_expert),
             _ptr(route.seg_offset), _ptr(route.seg_count), _ptr(route.n_segments), max_segments,
-            _ptr(w_down), _ptr(y), stream))
+            _ptr(w_down), _ptr(y), 1 if y.dtype == torch.bfloat16 else 0, stream))
         return h, y
     _timed("moe_gate_up", lambda: _lib.call(
         "sym_moe_gate_up", _ptr(x), T, H, I, _ptr(route.sorted_tokens), _ptr(route.seg_expert),
@@ -917,8 +923,11 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
 def moe_unpermute_combine(y: torch.Tensor, route: RouteResult,
                           residual: Optional[torch.Tensor] = None,
                           out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """out[t] = sum_k w[t,k] y[inv[t,k]] (+ shared row) (+ residual[t], fp32), bf16 [T, H]."""
-    _check(y, "y", torch.float32)
+    """out[t] = sum_k w[t,k] y[inv[t,k]] (+ shared row) (+ residual[t], fp32), bf16 [T, H];
+    y is fp32 or bf16."""
+    if y.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError(f"y: dtype {y.dtype} (fp32 or bf16)")
+    _check(y, "y", y.dtype)
     T, K = route.topk_idx.shape
     H = y.shape[1]
     dev = y.device
@@ -931,7 +940,8 @@ def moe_unpermute_combine(y: torch.Tensor, route: RouteResult,
     _check(out, "out", torch.bfloat16, dev)
     _check_shape(out, "out", (T, H))
     shared_row0 = T * K if route.with_shared else -1
-    _lib.call("sym_moe_unpermute_combine", _ptr(y), _ptr(route.inv_perm), _ptr(route.topk_w), T,
+    _lib.call("sym_moe_unpermute_combine", _ptr(y), 1 if y.dtype == torch.bfloat16 else 0,
+              _ptr(route.inv_perm), _ptr(route.topk_w), T,
               K, H, shared_row0, _ptr(residual), _ptr(out), _stream())
     return out
 

@@ -177,7 +177,8 @@ class HIPBailingMoE(StatelessHIPModule):
         route = self.route(x)
         if self.keep_last_route:
             self.last_route = route
-        _, y = hip_ops.moe_grouped_swiglu(x, route, self._dev["gate_up"], self._dev["down"])
+        _, y = hip_ops.moe_grouped_swiglu(x, route, self._dev["gate_up"], self._dev["down"],
+                                          y_dtype=_y_dtype(self.weight_format, x.shape[0]))
         out = hip_ops.moe_unpermute_combine(y, route, residual=res)
         return out.view(shape)
 
@@ -197,6 +198,14 @@ class HIPBailingMoE(StatelessHIPModule):
             self.last_route = route
         _, y = hip_ops.moe_grouped_swiglu(xn, route, self._dev["gate_up"], self._dev["down"])
         return hip_ops.moe_unpermute_combine(y, route, residual=h)
+
+
+def _y_dtype(weight_format: str, T: int) -> torch.dtype:
+    """Expert outputs y in bf16 where the tiled (prefill-size) kernels run: the down GEMM writes
+    half the bytes and the combine reads half; it sums in fp32 either way."""
+    if weight_format == "bf16" and T >= hip_ops.TILED_MIN_TOKENS:
+        return torch.bfloat16
+    return torch.float32
 
 
 class HIPBailingMoeV2MLP(StatelessHIPModule):
@@ -258,6 +267,7 @@ class HIPBailingMoeV2MLP(StatelessHIPModule):
         H = shape[-1]
         x = hidden_states.reshape(-1, H).to(torch.bfloat16).contiguous()
         route = self._route(x.shape[0])
-        _, y = hip_ops.moe_grouped_swiglu(x, route, self._dev["gate_up"], self._dev["down"])
+        _, y = hip_ops.moe_grouped_swiglu(x, route, self._dev["gate_up"], self._dev["down"],
+                                          y_dtype=_y_dtype("bf16", x.shape[0]))
         res = None if residual is None else residual.reshape(-1, H).to(torch.float32).contiguous()
         return hip_ops.moe_unpermute_combine(y, route, residual=res).view(shape)
