@@ -248,7 +248,7 @@ int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E, fl
  *   w - hi, lo = w - hi - mid); x [T, H] bf16;
  *   parts [3, T, E] fp32: parts[z] = x . plane_z^T (each product exact in fp32), summed
  *   (parts[0] + parts[1]) + parts[2] by sym_moe_route_permute (n_logit_parts = 3).
- * H % 64 == 0, E % 16 == 0.
+ * H % 32 == 0, E % 16 == 0.
  */
 int sym_moe_router_logits_split(const void* x, const void* w_planes, int T, int H, int E,
                                 float* parts, void* stream);
@@ -285,9 +285,12 @@ int sym_moe_router_logits_norm(const float* h, const float* ss_parts, int n_ss,
  *   top_k <= 32; topk_group <= n_group; 1 <= n_logit_parts <= 4.
  * Output sizes: topk_idx/topk_w/inv_perm [T*top_k]; expert_counts [E]; expert_offsets [E+1];
  * sorted_tokens [T*top_k + T]; seg_* [E+1]; n_segments [1].
- * Two launches: routing (one wave per token) and the permute (one workgroup).
- * workspace: sym_moe_route_workspace_bytes() is 0 (state lives in LDS); the arguments stay
- * for interface stability and may be NULL / 0.
+ * Launches: routing (one wave per token), then the permute: one workgroup up to 2048 tokens
+ * (state in LDS), else three launches over 256-token chunks (counts, per-expert scan, scatter)
+ * with the same outputs bit for bit.
+ * workspace: sym_moe_route_workspace_bytes(T, E) bytes (0 up to 2048 tokens, then
+ * ceil(T/256) * E * 4: per-chunk counts; no initial contents needed); NULL / 0 when the query
+ * gives 0. A smaller workspace returns SYM_ERR_WORKSPACE.
  */
 size_t sym_moe_route_workspace_bytes(int T, int E);
 int sym_moe_route_permute(const float* logits, int n_logit_parts, const float* bias, int T, int E,
@@ -344,12 +347,12 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
  * Tiled GEMMs for prefill-size batches (MFMA-bound; 128 x 256 output tiles).
  * sym_gemm_bf16: out[M, N] = a[M, K] . w[N, K]^T (+ bias[N] bf16) (+ residual[M, N] fp32),
  *   bf16 out, or fp32 when out_fp32 != 0. Replaces the QKV / dense projections at sequence length
- *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 16 == 0, K % 64 == 0.
+ *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 16 == 0, K % 32 == 0.
  * sym_moe_gate_up_tiled / sym_moe_down_tiled: the grouped expert GEMMs of sym_moe_gate_up /
  *   sym_moe_down (same arguments and results; TTNNExperts.forward, ttnn_moe.py:1250-1289) for
  *   segments of many rows; rows = total rows of the segment list (T*top_k + T with the shared
  *   expert). y is fp32, or bf16 when y_bf16 != 0 (half the bytes written here and read back by
- *   sym_moe_unpermute_combine). H % 64 == 0, I % 64 == 0.
+ *   sym_moe_unpermute_combine). H % 32 == 0, I % 32 == 0.
  */
 int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
                   int N, int K, void* out, int out_fp32, void* stream);

@@ -32,9 +32,12 @@ def test_workspace_queries():
     q = _lib.query
     assert q("sym_paged_gqa_decode_workspace_bytes", 32, 16, 128, 4128) >= 32 * 16 * 17 * 130 * 4
     assert q("sym_paged_gqa_decode_workspace_bytes", 0, 16, 128, 100) == 0
-    # routing keeps its intermediate state in LDS: no workspace at any size
+    # the permute keeps its state in LDS up to 2048 tokens, then per-(256-token chunk, expert)
+    # counts
     assert q("sym_moe_route_workspace_bytes", 32, 256) == 0
-    assert q("sym_moe_route_workspace_bytes", 4096, 256) == 0
+    assert q("sym_moe_route_workspace_bytes", 2048, 256) == 0
+    assert q("sym_moe_route_workspace_bytes", 2049, 256) == 9 * 256 * 4
+    assert q("sym_moe_route_workspace_bytes", 9942, 512) == 39 * 512 * 4
 
 
 def _call(name, *args):
@@ -77,6 +80,10 @@ def test_route_rejects_bad_configs():
     bad_parts[1] = 0
     assert _call("sym_moe_route_permute", *bad_parts)[0] == 1
     assert _call("sym_moe_route_permute", *args(0, 256, 8, 4, 8))[0] == 0     # empty batch
+    small_ws = list(args(5000, 256, 8, 4, 8))
+    small_ws[-2] = 100
+    rc, msg = _call("sym_moe_route_permute", *small_ws)
+    assert rc == 3 and "workspace" in msg
 
 
 def test_gemm_and_norm_reject_bad_shapes():

@@ -61,7 +61,10 @@ ROUTE_CASES = [
     (300, 128, 4, 2, 6, "randn"),
     (200, 512, 16, 8, 8, "randn"),
     (1500, 512, 16, 8, 8, "randn"),     # permute in passes of 512 tokens
-    (5000, 64, 8, 4, 4, "zipf"),        # permute in passes of 4096 tokens
+    (5000, 64, 8, 4, 4, "zipf"),        # three-launch permute over 256-token chunks
+    (2049, 256, 8, 4, 8, "ties"),       # one token past the single-workgroup permute
+    (4100, 512, 16, 8, 8, "zipf"),      # E = 512: four mask words per expert and chunk
+    (2304, 128, 4, 2, 6, "randn"),      # whole chunks only
     (200, 64, 1, 1, 8, "randn"),
     (500, 256, 8, 4, 8, "ties"),
     (100, 256, 8, 4, 8, "extreme"),

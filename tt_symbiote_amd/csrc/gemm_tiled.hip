@@ -7,13 +7,15 @@
 //
 // Design (gfx950): a workgroup of 8 waves computes a 128 x 256 output tile; wave w owns the
 // 64 x 64 block (rows 64*(w/4), columns 64*(w%4)) as 4 x 4 v_mfma_f32_16x16x32_bf16 tiles. The
-// K loop moves 64 columns per step through a 3-stage LDS ring (48 KB per stage, 144 KB): the
-// operand tiles go from global memory straight into LDS (global_load_lds_dwordx4, no register
-// staging), two steps ahead of the MFMAs, with one barrier per step. A wave-wide LDS-DMA
-// instruction writes 1 KB = 8 rows of 64 bf16 contiguously (lane l -> row l/8, 16-byte slot
-// l%8), so each lane fetches the global 16-byte chunk (l%8) ^ (row%8): chunk c of row r sits
-// in slot c ^ (r%8), and the 16 rows of an MFMA fragment read (one chunk each) spread over all
-// eight slots of a 128-byte row instead of hitting the same banks.
+// K loop moves 32 columns per step through a 3-stage LDS ring (24 KB per stage, 72 KB, so two
+// workgroups share a CU and one's barrier waits are covered by the other's MFMAs): the operand
+// tiles go from global memory straight into LDS (global_load_lds_dwordx4, no register staging),
+// two steps ahead of the MFMAs, with one barrier per step; a step's fragment reads are all
+// issued before its MFMAs. A wave-wide LDS-DMA instruction writes 1 KB = 16 rows of 32 bf16
+// contiguously (lane l -> row l/4, 16-byte slot l%4), so each lane fetches the global chunk
+// (l%4) ^ swz(row) with swz(r) = (r/2) % 4: chunk c of row r sits in slot c ^ swz(r), and the 16
+// rows of an MFMA fragment read (one chunk each) fall in distinct banks. (A 64-wide step with
+// 144 KB of LDS, one workgroup per CU, measured 10% slower on the dense projections.)
 //   DENSE:   out[M, N] = A[M, K] . W[N, K]^T (+ bias) (+ residual fp32), bf16 or fp32 out.
 //   GATE_UP: rows of a segment gather x[sorted_tokens[row]]; the B tile holds 128 gate rows and
 //            the matching 128 up rows of the expert, so each wave's block pairs 32 gate with 32
@@ -28,11 +30,27 @@
 
 namespace sym {
 
-constexpr int kTM = 128, kTN = 256, kTK = 64;
+#ifdef SYM_TILE_K
+constexpr int kTK = SYM_TILE_K;  // 32 or 64
+#else
+constexpr int kTK = 32;  // 72 KB of LDS: two workgroups per CU (64: 144 KB, one; 10% slower)
+#endif
+constexpr int kTM = 128, kTN = 256;
 constexpr int kTileThreads = 512;
-constexpr int kAStage = kTM * kTK;  // bf16 elements of one A stage (16 KB)
+constexpr int kAStage = kTM * kTK;  // bf16 elements of one A stage (16 KB at kTK = 64)
 constexpr int kBStage = kTN * kTK;  // bf16 elements of one B stage (32 KB)
+constexpr int kStage = kAStage + kBStage;
 constexpr int kDmaPerStep = (kAStage + kBStage) * 2 / 1024 / (kTileThreads / 64);  // per wave
+constexpr int kChunksPerRow = kTK / 8;          // 16-byte chunks per LDS row
+constexpr int kRowsPerDma = 64 / kChunksPerRow;  // rows one wave-wide LDS-DMA instruction fills
+static_assert(kTK == 32 || kTK == 64, "tile K");
+
+// LDS slot of chunk c in row r: c ^ swz(r), chosen so that the 16 rows of a fragment read (one
+// chunk each) fall in distinct banks: 8 chunks per 128-byte row -> r % 8; 4 chunks per 64-byte
+// row (two rows per 128 bytes) -> (r / 2) % 4.
+__device__ __forceinline__ int tile_swz(int r) {
+  return kChunksPerRow == 8 ? (r & 7) : ((r >> 1) & 3);
+}
 constexpr int kMaxGemmSegments = 4096;  // grid bound on segments (y range)
 
 enum TileMode { kDense = 0, kGateUp = 1, kDown = 2 };
@@ -53,6 +71,8 @@ struct TileArgs {
   long long w_zstride;      // DENSE: grid z selects weight plane w + z * w_zstride ...
   long long out_zstride;    // ... and output plane out + z * out_zstride (elements)
 };
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // 16 bytes per lane from global memory into LDS at base + 16 * lane (base wave-uniform, in M0).
 // Written as asm so that the compiler does not add its own (conservative) waits for these LDS
@@ -76,8 +96,9 @@ __device__ __forceinline__ void dma16(const uint16_t* g, const uint16_t* lds_bas
 
 template <int MODE>
 __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
-  __shared__ __align__(1024) uint16_t sA0[kAStage], sA1[kAStage], sA2[kAStage];
-  __shared__ __align__(1024) uint16_t sB0[kBStage], sB1[kBStage], sB2[kBStage];
+  // stage s = [A (16 KB) | B (32 KB)] at smem + s * kStage: one base address per stage keeps every
+  // fragment read of the stage within the 64 KB immediate offset of an LDS instruction
+  __shared__ __align__(1024) uint16_t smem[3 * kStage];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -87,9 +108,9 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
 
   // ---- locate the tile ----
   int row0, rows, e = 0;  // first output row, valid rows in the tile, expert
-  const int ct = blockIdx.x;
+  const int ct = blockIdx.x, gy = blockIdx.y;
   if constexpr (MODE == kDense) {
-    row0 = blockIdx.y * kTM;
+    row0 = gy * kTM;
     rows = min(kTM, p.M - row0);
     p.w += blockIdx.z * p.w_zstride;
     if (p.out_f32) p.out_f32 += blockIdx.z * p.out_zstride;
@@ -98,7 +119,7 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
     // Every wave scans the segment list 64 segments at a time (prefix sum by lane shuffles)
     // and stops at the one holding tile g: no LDS and no barrier, and all waves agree.
     const int nseg = p.n_segments[0];
-    const int g = blockIdx.y;
+    const int g = gy;
     int seg = -1, start = 0, run = 0;
     for (int s0 = 0; s0 < nseg; s0 += 64) {
       const int s = s0 + lane;
@@ -126,25 +147,27 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
     rows = min(kTM, p.seg_count[seg] - rt * kTM);
   }
 
-  // ---- LDS-DMA sources: this wave fills A rows 16w .. 16w+15 (2 instructions) and B rows
-  // 32w .. 32w+31 (4 instructions) of every stage; lane l takes row +l/8, chunk (l%8)^(row%8)
-  const int lr = lane >> 3;
-  const int a_row_l = wave * 16 + lr;   // + 8i; row % 8 == lr
-  const int b_row_l = wave * 32 + lr;   // + 8i
-  const int chunk = ((lane & 7) ^ lr) * 8;
-  const uint16_t* a_src[2];
-  const uint16_t* b_src[4];
+  // ---- LDS-DMA sources: this wave fills A rows 16w .. 16w+15 and B rows 32w .. 32w+31 of
+  // every stage; lane l takes row + l / kChunksPerRow, slot l % kChunksPerRow, i.e. global chunk
+  // slot ^ swz(row)
+  constexpr int kADma = 16 / kRowsPerDma, kBDma = 32 / kRowsPerDma;
+  const int lr = lane / kChunksPerRow;
+  const int a_row_l = wave * 16 + lr;   // + kRowsPerDma * i
+  const int b_row_l = wave * 32 + lr;
+  const int chunk = ((lane % kChunksPerRow) ^ tile_swz(lr)) * 8;  // swz(row) == swz(lr)
+  const uint16_t* a_src[kADma];
+  const uint16_t* b_src[kBDma];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = min(a_row_l + 8 * i, rows - 1);
+  for (int i = 0; i < kADma; ++i) {
+    const int r = min(a_row_l + kRowsPerDma * i, rows - 1);
     size_t arow;
     if constexpr (MODE == kGateUp) arow = (size_t)p.sorted_tokens[row0 + r];
     else arow = (size_t)(row0 + r);
     a_src[i] = p.a + arow * K + chunk;
   }
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int br = b_row_l + 8 * i;  // B tile row 0..255
+  for (int i = 0; i < kBDma; ++i) {
+    const int br = b_row_l + kRowsPerDma * i;  // B tile row 0..255
     size_t brow;
     if constexpr (MODE == kGateUp) {
       // 128 gate rows then the matching 128 up rows of expert e
@@ -160,12 +183,12 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
   const int a_dst = wave * 16 * kTK;  // element offset of this wave's first A row in a stage
   const int b_dst = wave * 32 * kTK;
 
-  auto issue = [&](int kt, uint16_t* sA, uint16_t* sB) {
+  auto issue = [&](int kt, uint16_t* stage) {
     const int k = kt * kTK;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dma16(a_src[i] + k, sA + a_dst + i * 8 * kTK);
+    for (int i = 0; i < kADma; ++i) dma16(a_src[i] + k, stage + a_dst + i * 512);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dma16(b_src[i] + k, sB + b_dst + i * 8 * kTK);
+    for (int i = 0; i < kBDma; ++i) dma16(b_src[i] + k, stage + kAStage + b_dst + i * 512);
   };
 
   // fragment rows of this wave: A rows wm*64 + 16i + r16; B rows per column tile j
@@ -177,7 +200,7 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
     else
       b_frag[j] = wn * 64 + j * 16 + r16;
   }
-  const int sw = r16 & 7;  // every fragment row r has r % 8 == r16 % 8
+  const int sw = tile_swz(r16);  // every fragment row r has swz(r) == swz(r16)
 
   floatx4 acc[4][4];
 #pragma unroll
@@ -185,42 +208,49 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const uint16_t* sA, const uint16_t* sB) {
+  // all fragment reads of the step are issued before its MFMAs
+  auto compute = [&](const uint16_t* stage) {
+    const uint16_t* sA = stage;
+    const uint16_t* sB = stage + kAStage;
+    u32x4 fa[2][4], fb[2][4];
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
+    for (int kh = 0; kh < kTK / 32; ++kh) {
       const int slot = ((kh * 4 + kq) ^ sw) * 8;
-      uint4 fa[4], fb[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        fa[i] = *reinterpret_cast<const uint4*>(&sA[(wm * 64 + i * 16 + r16) * kTK + slot]);
+        fa[kh][i] = *reinterpret_cast<const u32x4*>(&sA[(wm * 64 + i * 16 + r16) * kTK + slot]);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        fb[j] = *reinterpret_cast<const uint4*>(&sB[b_frag[j] * kTK + slot]);
+        fb[kh][j] = *reinterpret_cast<const u32x4*>(&sB[b_frag[j] * kTK + slot]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int kh = 0; kh < kTK / 32; ++kh)
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(fa[i], fb[j], acc[i][j]);
-    }
+        for (int j = 0; j < 4; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, fa[kh][i]), __builtin_bit_cast(bf16x8, fb[kh][j]),
+              acc[i][j], 0, 0, 0);
   };
 
   // Step k: wait for its stage (the DMA of step k + 1 may still be in flight), barrier (every
-  // wave is also done with step k - 1's stage), issue step k + 2 into that stage, MFMAs.
-  static_assert(kDmaPerStep == 6, "SYM_TILE_SYNC count");
+  // wave is also done with step k - 1's stage), issue step k + 2 into that stage, MFMAs. Step k
+  // uses stage k % 3.
+  static_assert(kDmaPerStep == 6 || kDmaPerStep == 3, "SYM_TILE_SYNC count");
   const int nk = K / kTK;
-  issue(0, sA0, sB0);
-  if (nk > 1) issue(1, sA1, sB1);
-  auto step = [&](int kt, const uint16_t* cA, const uint16_t* cB, uint16_t* nA, uint16_t* nB) {
-    if (kt + 1 < nk) SYM_TILE_SYNC(6);
-    else SYM_TILE_SYNC(0);
-    if (kt + 2 < nk) issue(kt + 2, nA, nB);
-    compute(cA, cB);
-  };
-  for (int kt = 0; kt < nk; kt += 3) {
-    step(kt, sA0, sB0, sA2, sB2);
-    if (kt + 1 >= nk) break;
-    step(kt + 1, sA1, sB1, sA0, sB0);
-    if (kt + 2 >= nk) break;
-    step(kt + 2, sA2, sB2, sA1, sB1);
+  issue(0, smem);
+  if (nk > 1) issue(1, smem + kStage);
+  int cur = 0;  // stage of step kt (element offset)
+  for (int kt = 0; kt < nk; ++kt) {
+    if (kt + 1 >= nk) SYM_TILE_SYNC(0);
+    else if constexpr (kDmaPerStep == 6) SYM_TILE_SYNC(6);
+    else SYM_TILE_SYNC(3);
+    const int nxt = cur == 0 ? 2 * kStage : cur - kStage;  // stage of step kt + 2
+    if (kt + 2 < nk) issue(kt + 2, smem + nxt);
+    compute(smem + cur);
+    cur = cur == 2 * kStage ? 0 : cur + kStage;
   }
 
   // ---- epilogue: lane holds rows 4*(l/16)+q, column l%16 of each 16 x 16 tile ----

@@ -336,6 +336,115 @@ __global__ __launch_bounds__(kPermuteThreads) void moe_permute_kernel(
   }
 }
 
+// Permute of many tokens across the GPU (the same outputs as moe_permute_kernel, bit for bit),
+// in three launches over chunks of kChunkTokens tokens:
+//   1. moe_permute_count_kernel: per (chunk, expert) assignment counts (LDS atomics);
+//   2. moe_permute_scan_kernel (one workgroup, thread e owns expert e): each expert's exclusive
+//      prefix over the chunks (in place), its total count, the expert offsets and the segment
+//      list exactly as moe_permute_kernel builds them;
+//   3. moe_permute_scatter_kernel: per chunk, one 64-bit token mask per (64 tokens, expert)
+//      (atomic OR, order independent); an assignment's row is its expert's offset + the expert's
+//      tokens in earlier chunks + those in earlier words of this chunk + popcount of the lower
+//      tokens of its own word, i.e. rows of an expert follow token order.
+constexpr int kChunkTokens = 256;
+constexpr int kChunkWords = kChunkTokens / 64;
+constexpr int kPermuteSingleMaxTokens = 2048;  // above this the three-launch permute runs
+
+__global__ __launch_bounds__(256) void moe_permute_count_kernel(
+    const int32_t* __restrict__ topk_idx, int T, int K, int E, int32_t* __restrict__ chunk_cnt) {
+  __shared__ int s_cnt[512];
+  const int c = blockIdx.x, tid = threadIdx.x;
+  for (int e = tid; e < E; e += 256) s_cnt[e] = 0;
+  __syncthreads();
+  const int a0 = c * kChunkTokens * K, a1 = min(T, (c + 1) * kChunkTokens) * K;
+  for (int a = a0 + tid; a < a1; a += 256) atomicAdd(&s_cnt[topk_idx[a]], 1);
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) chunk_cnt[(size_t)c * E + e] = s_cnt[e];
+}
+
+__global__ __launch_bounds__(kPermuteThreads) void moe_permute_scan_kernel(
+    int T, int K, int E, int with_shared, int n_chunks, int32_t* __restrict__ chunk_cnt,
+    int32_t* __restrict__ expert_counts, int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ sorted_tokens, int32_t* __restrict__ seg_expert,
+    int32_t* __restrict__ seg_offset, int32_t* __restrict__ seg_count,
+    int32_t* __restrict__ n_segments) {
+  __shared__ int s_wave[16];
+  const int tid = threadIdx.x;
+  const int e = tid;
+  const int TK = T * K;
+  int cnt = 0;
+  if (e < E)
+    for (int c0 = 0; c0 < n_chunks; c0 += 8) {
+      // the loads of 8 chunks are issued before any store (the stores could alias them)
+      int v[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        v[i] = c0 + i < n_chunks ? chunk_cnt[(size_t)(c0 + i) * E + e] : 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        if (c0 + i < n_chunks) chunk_cnt[(size_t)(c0 + i) * E + e] = cnt;
+        cnt += v[i];
+      }
+    }
+  int total = 0;
+  const int off = block_exclusive_scan(cnt, s_wave, &total);
+  int n_routed = 0;
+  const int flag = (e < E && cnt > 0) ? 1 : 0;
+  const int slot = block_exclusive_scan(flag, s_wave, &n_routed);
+  if (e < E) {
+    expert_counts[e] = cnt;
+    expert_offsets[e] = off;
+    if (flag) {
+      seg_expert[slot] = e;
+      seg_offset[slot] = off;
+      seg_count[slot] = cnt;
+    }
+  }
+  if (tid == 0) {
+    expert_offsets[E] = total;
+    if (with_shared) {
+      seg_expert[n_routed] = E;
+      seg_offset[n_routed] = TK;
+      seg_count[n_routed] = T;
+    }
+    n_segments[0] = n_routed + (with_shared ? 1 : 0);
+  }
+  if (with_shared)
+    for (int t = tid; t < T; t += kPermuteThreads) sorted_tokens[TK + t] = t;
+}
+
+__global__ __launch_bounds__(256) void moe_permute_scatter_kernel(
+    const int32_t* __restrict__ topk_idx, int T, int K, int E,
+    const int32_t* __restrict__ chunk_cnt, const int32_t* __restrict__ expert_offsets,
+    int32_t* __restrict__ sorted_tokens, int32_t* __restrict__ inv_perm) {
+  __shared__ unsigned long long s_mask[kChunkWords * 512];
+  __shared__ int s_base[512];
+  const int c = blockIdx.x, tid = threadIdx.x;
+  const int t0 = c * kChunkTokens;
+  for (int i = tid; i < kChunkWords * E; i += 256) s_mask[i] = 0ull;
+  for (int e = tid; e < E; e += 256)
+    s_base[e] = expert_offsets[e] + chunk_cnt[(size_t)c * E + e];
+  __syncthreads();
+  const int a0 = t0 * K, a1 = min(T, t0 + kChunkTokens) * K;
+  for (int a = a0 + tid; a < a1; a += 256) {
+    const int tl = a / K - t0;
+    atomicOr(&s_mask[(tl >> 6) * E + topk_idx[a]], 1ull << (tl & 63));
+  }
+  __syncthreads();
+  for (int a = a0 + tid; a < a1; a += 256) {
+    const int t = a / K;
+    const int tl = t - t0;
+    const int ex = topk_idx[a];
+    const int w = tl >> 6, bit = tl & 63;
+    int row = s_base[ex];
+    for (int ww = 0; ww < w; ++ww) row += __popcll(s_mask[ww * E + ex]);
+    const unsigned long long m = s_mask[w * E + ex];
+    row += __popcll(bit ? (m & ((1ull << bit) - 1ull)) : 0ull);
+    sorted_tokens[row] = t;
+    inv_perm[a] = row;
+  }
+}
+
 // Router logits in fp32 with v_mfma_f32_16x16x4_f32: parts[q][t][e] = sum over the q-th
 // quarter of H of x[t][k] * w[e][k]. One workgroup of 8 waves per (16 experts, quarter of H);
 // each wave owns H/32 consecutive k of the quarter and issues its weight loads (16 bytes per lane
@@ -496,10 +605,10 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
 using namespace sym;
 
 extern "C" size_t sym_moe_route_workspace_bytes(int T, int E) {
-  // routing keeps its intermediate state in LDS
-  (void)T;
-  (void)E;
-  return 0;
+  // up to kPermuteSingleMaxTokens tokens the permute keeps its state in LDS; above, the
+  // per-(chunk, expert) prefix counts of the three-launch permute
+  if (T <= kPermuteSingleMaxTokens || E <= 0) return 0;
+  return (size_t)((T + kChunkTokens - 1) / kChunkTokens) * E * sizeof(int32_t);
 }
 
 static int check_router_logits(const char* what, int T, int H, int E) {
@@ -582,8 +691,10 @@ extern "C" int sym_moe_route_permute(const float* logits, int n_logit_parts, con
               "moe_route_permute: top_k=%d exceeds the experts of the kept groups", top_k);
   SYM_REQUIRE((long long)T * top_k + T < (1ll << 30), SYM_ERR_INVALID,
               "moe_route_permute: T=%d too large", T);
-  (void)workspace;
-  (void)workspace_bytes;
+  const size_t ws_need = sym_moe_route_workspace_bytes(T, E);
+  SYM_REQUIRE(ws_need == 0 || (workspace && workspace_bytes >= ws_need), SYM_ERR_WORKSPACE,
+              "moe_route_permute: workspace of %zu bytes needed for T=%d (got %zu)", ws_need, T,
+              workspace ? workspace_bytes : (size_t)0);
 
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
@@ -600,8 +711,24 @@ extern "C" int sym_moe_route_permute(const float* logits, int n_logit_parts, con
 #undef SYM_LAUNCH_ROUTE
   int rc = sym_host::check_launch("moe_route_kernel");
   if (rc) return rc;
-  hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(kPermuteThreads), 0, s, topk_idx, T, top_k,
-                     E, with_shared, expert_counts, expert_offsets, sorted_tokens, inv_perm,
-                     seg_expert, seg_offset, seg_count, n_segments);
-  return sym_host::check_launch("moe_permute_kernel");
+  if (ws_need == 0) {
+    hipLaunchKernelGGL(moe_permute_kernel, dim3(1), dim3(kPermuteThreads), 0, s, topk_idx, T,
+                       top_k, E, with_shared, expert_counts, expert_offsets, sorted_tokens,
+                       inv_perm, seg_expert, seg_offset, seg_count, n_segments);
+    return sym_host::check_launch("moe_permute_kernel");
+  }
+  const int n_chunks = (T + kChunkTokens - 1) / kChunkTokens;
+  int32_t* chunk_cnt = (int32_t*)workspace;
+  hipLaunchKernelGGL(moe_permute_count_kernel, dim3(n_chunks), dim3(256), 0, s, topk_idx, T, top_k,
+                     E, chunk_cnt);
+  rc = sym_host::check_launch("moe_permute_count_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(moe_permute_scan_kernel, dim3(1), dim3(kPermuteThreads), 0, s, T, top_k, E,
+                     with_shared, n_chunks, chunk_cnt, expert_counts, expert_offsets,
+                     sorted_tokens, seg_expert, seg_offset, seg_count, n_segments);
+  rc = sym_host::check_launch("moe_permute_scan_kernel");
+  if (rc) return rc;
+  hipLaunchKernelGGL(moe_permute_scatter_kernel, dim3(n_chunks), dim3(256), 0, s, topk_idx, T,
+                     top_k, E, chunk_cnt, expert_offsets, sorted_tokens, inv_perm);
+  return sym_host::check_launch("moe_permute_scatter_kernel");
 }

@@ -89,6 +89,32 @@ def counter_per_dispatch(csv_path: str, counter: str) -> dict:
     return out
 
 
+def print_counters(csv_paths, kernels) -> None:
+    """For each kernel whose name contains one of ``kernels``: every counter of the CSVs, as the
+    median over its dispatches of the sum over a dispatch's rows (per-XCD / per-SE instances)
+    and of their maximum (GRBM_GUI_ACTIVE is a per-instance clock: use its max)."""
+    sums = defaultdict(lambda: defaultdict(lambda: defaultdict(float)))
+    maxs = defaultdict(lambda: defaultdict(lambda: defaultdict(float)))
+    for path in csv_paths:
+        with open(path, newline="") as f:
+            for row in csv.DictReader(f):
+                name = row["Kernel_Name"]
+                if not any(k in name for k in kernels):
+                    continue
+                v = float(row["Counter_Value"])
+                key = (row["Dispatch_Id"], row.get("Grid_Size", ""))
+                sums[name][row["Counter_Name"]][key] += v
+                cur = maxs[name][row["Counter_Name"]]
+                cur[key] = max(cur[key], v)
+    for name in sorted(sums):
+        print(name[:110])
+        for c in sorted(sums[name]):
+            s_med = statistics.median(sums[name][c].values())
+            m_med = statistics.median(maxs[name][c].values())
+            print(f"  {c:32s} sum {s_med:16.0f}   max {m_med:14.0f}   "
+                  f"({len(sums[name][c])} dispatches)")
+
+
 def _match(table: dict, needle: str) -> list:
     hits = [k for k in table if needle in k]
     if not hits:
@@ -129,6 +155,9 @@ def main(argv=None) -> None:
     tl = sub.add_parser("timeline")
     tl.add_argument("db")
     tl.add_argument("--last", type=int, default=100)
+    c = sub.add_parser("counters")
+    c.add_argument("csv", nargs="+")
+    c.add_argument("--kernel", action="append", required=True)
     p = sub.add_parser("pmc")
     p.add_argument("--kernel", required=True)
     p.add_argument("--fetch", required=True)
@@ -144,6 +173,9 @@ def main(argv=None) -> None:
         return
     if args.cmd == "timeline":
         print_timeline(args.db, args.last)
+        return
+    if args.cmd == "counters":
+        print_counters(args.csv, args.kernel)
         return
     res = pmc_traffic(args)
     if args.json:
