@@ -33,6 +33,25 @@ constexpr int kTPW8 = SYM_FP8_TPW;
 constexpr int kTPW8 = 64;
 #endif
 constexpr int kSplit8 = 4 * kTPW8;
+// fp8 split kernel: V is loaded after the scores (into the registers K used) and the kernel is
+// held to 5 workgroups per CU (92 VGPRs at 4 query heads per kv head; 8 heads per kv head would
+// spill and keep the default): 197 against 210 us at batch 128 with 1024-8192 contexts. Late V
+// alone (98 registers, still 4 per CU) measured 218 us.
+#ifdef SYM_FP8_LATE_V
+constexpr bool kLateV8 = SYM_FP8_LATE_V != 0;
+#else
+constexpr bool kLateV8 = true;
+#endif
+#ifdef SYM_FP8_MIN_BLOCKS
+constexpr int kFp8MinBlocks = SYM_FP8_MIN_BLOCKS;
+#else
+constexpr int kFp8MinBlocks = 5;
+#endif
+#ifdef SYM_BF16_MIN_BLOCKS
+constexpr int kBf16MinBlocks = SYM_BF16_MIN_BLOCKS;
+#else
+constexpr int kBf16MinBlocks = 1;
+#endif
 constexpr int kAttnThreads = 256;
 
 // ---------------------------------------------------------------------------------------------
@@ -249,7 +268,7 @@ struct FusedQKV {
 };
 
 template <int G, int TPW, bool FUSED>
-__global__ __launch_bounds__(kAttnThreads) void paged_decode_kernel(
+__global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_kernel(
     const uint16_t* __restrict__ q, FusedQKV fq, uint16_t* __restrict__ k_pool,
     uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ positions, int Hkv, int block_size, int mbps, int num_blocks,
@@ -747,7 +766,7 @@ __device__ __forceinline__ void fp8_append_token(uint8_t* __restrict__ pool,
 //   divides 256, and the split is a multiple of 256 tokens), so no other workgroup reads the
 //   block being rewritten. A thread owns split / 256 tokens in the softmax.
 template <int G, bool FUSED>
-__global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
+__global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void paged_decode_fp8_kernel(
     const uint16_t* __restrict__ q, FusedQKV fq, uint8_t* __restrict__ k_pool,
     uint8_t* __restrict__ v_pool, float* __restrict__ k_scale, float* __restrict__ v_scale,
     const int32_t* __restrict__ block_tables, const int32_t* __restrict__ positions, int Hkv,
@@ -847,6 +866,12 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
   uint4 kb[KT][2];
   uint2 vreg[VS];
   float ks_own[TPT], vs_own[TPT];
+  auto load_v = [&]() {
+#pragma unroll
+    for (int it = 0; it < VS; ++it)
+      vreg[it] = *reinterpret_cast<const uint2*>(v_pool + (size_t)s_row[wt0 + it * 4 + kg] * D +
+                                                 r16 * 8);
+  };
   auto issue_loads = [&]() {
 #pragma unroll
     for (int tt = 0; tt < KT; ++tt) {
@@ -854,10 +879,7 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
       kb[tt][0] = *reinterpret_cast<const uint4*>(kr);
       kb[tt][1] = *reinterpret_cast<const uint4*>(kr + 16);
     }
-#pragma unroll
-    for (int it = 0; it < VS; ++it)
-      vreg[it] = *reinterpret_cast<const uint2*>(v_pool + (size_t)s_row[wt0 + it * 4 + kg] * D +
-                                                 r16 * 8);
+    if constexpr (!kLateV8) load_v();
 #pragma unroll
     for (int j = 0; j < TPT; ++j) {
       ks_own[j] = k_scale[my_sidx[j]];
@@ -917,6 +939,7 @@ __global__ __launch_bounds__(kAttnThreads) void paged_decode_fp8_kernel(
       if (h < G) s_p[h][tl] = sacc[i];
     }
   }
+  if constexpr (kLateV8) load_v();  // into the registers K used; arrives during the softmax
   __syncthreads();
 
   // ---- softmax statistics (log2 domain); thread tid owns tokens t0 + tid + 256 j ----
