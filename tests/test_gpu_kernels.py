@@ -68,6 +68,11 @@ ROUTE_CASES = [
     (200, 64, 1, 1, 8, "randn"),
     (500, 256, 8, 4, 8, "ties"),
     (100, 256, 8, 4, 8, "extreme"),
+    # small batches at the other expert counts
+    (17, 64, 8, 4, 4, "randn"),
+    (50, 128, 4, 2, 6, "ties"),
+    (64, 512, 16, 8, 8, "zipf"),
+    (3, 512, 16, 8, 8, "extreme"),
 ]
 
 
