@@ -21,7 +21,15 @@
 namespace sym {
 
 constexpr int kGemmThreads = 256;  // 4 waves; each wave owns 16 output columns
-constexpr int kColsPerWG = 128;  // down projection: 4 waves x 32 columns
+// 16-column tiles per wave of the down projection: one tile needs 90 + 4 registers (5 waves per
+// SIMD), two need 124 + 8 (3 per SIMD); 62.1 against 65.3 us at batch 32.
+#ifdef SYM_DOWN_NT
+constexpr int kDownNT = SYM_DOWN_NT;
+#else
+constexpr int kDownNT = 1;
+#endif
+constexpr int kColsPerWG = 4 * 16 * kDownNT;  // down projection: 4 waves x 16 * kDownNT columns
+constexpr int kColsPerWG8 = 128;              // fp8 down projection: 4 waves x 32 columns
 
 __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
   return *reinterpret_cast<const uint4*>(p);
@@ -160,10 +168,10 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
   }
 }
 
-// One pass of the down projection over MT row tiles: this wave's 32 output columns (two
-// 16-column tiles sharing the activation fragments) over the full reduction dim I, in batches
-// of U K-steps (weights first, then activations, then MFMAs).
-template <int MT, int U>
+// One pass of the down projection over MT row tiles: this wave's NT 16-column tiles (sharing
+// the activation fragments) over the full reduction dim I, in batches of U K-steps (weights
+// first, then activations, then MFMAs).
+template <int MT, int U, int NT = 2>
 __device__ __forceinline__ void down_pass(const uint16_t* __restrict__ hrow, int I, int rows,
                                           const uint16_t* __restrict__ wd0,
                                           const uint16_t* __restrict__ wd1, int r16, int kq,
@@ -181,8 +189,10 @@ __device__ __forceinline__ void down_pass(const uint16_t* __restrict__ hrow, int
       const int k = (st + s) << 6;
       b0[s][0] = ld16(wd0 + k);
       b0[s][1] = ld16(wd0 + k + kKHalf);
-      b1[s][0] = ld16(wd1 + k);
-      b1[s][1] = ld16(wd1 + k + kKHalf);
+      if constexpr (NT == 2) {
+        b1[s][0] = ld16(wd1 + k);
+        b1[s][1] = ld16(wd1 + k + kKHalf);
+      }
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -202,13 +212,15 @@ __device__ __forceinline__ void down_pass(const uint16_t* __restrict__ hrow, int
       for (int mt = 0; mt < MT; ++mt) {
         acc0[mt] = mfma16x16x32(a[mt][s][0], b0[s][0], acc0[mt]);
         acc0[mt] = mfma16x16x32(a[mt][s][1], b0[s][1], acc0[mt]);
-        acc1[mt] = mfma16x16x32(a[mt][s][0], b1[s][0], acc1[mt]);
-        acc1[mt] = mfma16x16x32(a[mt][s][1], b1[s][1], acc1[mt]);
+        if constexpr (NT == 2) {
+          acc1[mt] = mfma16x16x32(a[mt][s][0], b1[s][0], acc1[mt]);
+          acc1[mt] = mfma16x16x32(a[mt][s][1], b1[s][1], acc1[mt]);
+        }
       }
   }
 }
 
-template <int MT>
+template <int MT, int NT = 2>
 __device__ __forceinline__ void down_store(const floatx4 (&acc0)[MT], const floatx4 (&acc1)[MT],
                                            int rows, float* __restrict__ yrow, int H, int r16,
                                            int kq) {
@@ -220,13 +232,13 @@ __device__ __forceinline__ void down_store(const floatx4 (&acc0)[MT], const floa
       if (r < rows) {
         float* yr = yrow + (size_t)r * H + r16;
         yr[0] = acc0[mt][i];
-        yr[16] = acc1[mt][i];
+        if constexpr (NT == 2) yr[16] = acc1[mt][i];
       }
     }
 }
 
-// down projection. One wave per (segment, 32 output columns); segment metadata in one round
-// trip before the exit test; rows in passes of 16.
+// down projection. One wave per (segment, 16 * kDownNT output columns); segment metadata in one
+// round trip before the exit test; rows in passes of 16.
 template <int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
     const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
@@ -246,7 +258,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
   const int tile = blockIdx.x - seg * tiles_per_seg;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int col0 = (tile * 4 + wave) * 32;
+  const int col0 = (tile * 4 + wave) * (16 * kDownNT);
   if (col0 >= H) return;
   const int r16 = lane & 15;
   const int kq = lane >> 4;
@@ -256,8 +268,9 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
   for (int mb = 0; mb < cnt; mb += 16) {
     const int rows = min(16, cnt - mb);
     floatx4 acc0[1], acc1[1];
-    down_pass<1, U>(hbuf + (size_t)(row0 + mb) * I, I, rows, wd0, wd1, r16, kq, acc0, acc1);
-    down_store<1>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
+    down_pass<1, U, kDownNT>(hbuf + (size_t)(row0 + mb) * I, I, rows, wd0, wd1, r16, kq, acc0,
+                             acc1);
+    down_store<1, kDownNT>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
   }
 }
 
@@ -338,7 +351,10 @@ __device__ __forceinline__ void gate_up_pass_fp8(const uint16_t* __restrict__ x,
 }
 
 // gate/up + SwiGLU with fp8 weights: w_gu [E+1, 2I, H] e4m3fn bytes, s_gu [E+1, 2I/128, H/128].
-// Workgroup = (segment, 16 columns of h) as in moe_gate_up_kernel.
+// Workgroup = (segment, 16 columns of h) as in moe_gate_up_kernel. Both fp8 kernels launch with
+// one 128-wide K-step per load batch (U = 1): 82-90 VGPRs and 4-5 waves per SIMD, where U = 4
+// needs 190 registers (2 per SIMD): 124 against 137 us (gate/up), 79 against 84 us (down) at
+// batch 128.
 template <int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_fp8_kernel(
     const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
@@ -631,9 +647,11 @@ extern "C" int sym_moe_gate_up_fp8(const void* x, int T, int H, int I,
   hipLaunchKernelGGL((moe_gate_up_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,          \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
                      n_segments, (const uint8_t*)w_gate_up, s_gate_up, (uint16_t*)h, tiles)
-  if (wave_steps % 4 == 0) SYM_LAUNCH_GATE_UP_FP8(4);
-  else if (wave_steps % 2 == 0) SYM_LAUNCH_GATE_UP_FP8(2);
-  else SYM_LAUNCH_GATE_UP_FP8(1);
+#ifdef SYM_FP8_GATE_UP_U
+  if (wave_steps % SYM_FP8_GATE_UP_U == 0) SYM_LAUNCH_GATE_UP_FP8(SYM_FP8_GATE_UP_U);
+  else
+#endif
+  SYM_LAUNCH_GATE_UP_FP8(1);
 #undef SYM_LAUNCH_GATE_UP_FP8
   return sym_host::check_launch("moe_gate_up_fp8_kernel");
 }
@@ -648,16 +666,18 @@ extern "C" int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_
   SYM_REQUIRE(h && seg_expert && seg_offset && seg_count && n_segments && w_down && s_down && y,
               SYM_ERR_INVALID, "moe_down_fp8: null pointer argument");
   (void)hipGetLastError();
-  const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
+  const int tiles = (H + kColsPerWG8 - 1) / kColsPerWG8;
   const int steps = I / 128;  // K-steps of 128 per wave (one wave covers all of I)
   const dim3 grid(max_segments * tiles), block(kGemmThreads);
 #define SYM_LAUNCH_DOWN_FP8(UU)                                                                 \
   hipLaunchKernelGGL((moe_down_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,             \
                      (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
                      (const uint8_t*)w_down, s_down, y, tiles)
-  if (steps % 4 == 0) SYM_LAUNCH_DOWN_FP8(4);
-  else if (steps % 2 == 0) SYM_LAUNCH_DOWN_FP8(2);
-  else SYM_LAUNCH_DOWN_FP8(1);
+#ifdef SYM_FP8_DOWN_U
+  if (steps % SYM_FP8_DOWN_U == 0) SYM_LAUNCH_DOWN_FP8(SYM_FP8_DOWN_U);
+  else
+#endif
+  SYM_LAUNCH_DOWN_FP8(1);
 #undef SYM_LAUNCH_DOWN_FP8
   return sym_host::check_launch("moe_down_fp8_kernel");
 }
