@@ -67,6 +67,11 @@ __device__ __forceinline__ float clamp_fp8(float x) {
   return fminf(fmaxf(x, -kFp8Max), kFp8Max);
 }
 
+// 2^x with the hardware v_exp_f32 alone, for softmax weights. exp2f compiles to a longer
+// sequence here (the library keeps results below 2^-126 as denormals: five instructions instead
+// of one); a softmax weight that small is 0 for every purpose.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // 8 bf16 packed in a uint4 -> 8 floats.
 __device__ __forceinline__ void unpack8(const uint4& v, float* f) {
   f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x);

@@ -475,7 +475,7 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
 #pragma unroll
   for (int h = 0; h < G; ++h) {
     const float v = s_p[h][tm];
-    const float pr = (mx[h] == -INFINITY || v == -INFINITY) ? 0.f : exp2f(v - mx[h]);
+    const float pr = (mx[h] == -INFINITY || v == -INFINITY) ? 0.f : fast_exp2(v - mx[h]);
     if (mine) s_p[h][tm] = pr;
     const float l = wave_sum(mine ? pr : 0.f);
     if (lane == 0) s_stat[h][wave] = l;
@@ -568,7 +568,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
     float w = 0.f;
     if (c + lane < nsplit) {
       const float2 v = ml[c + lane];
-      w = (v.x == -INFINITY) ? 0.f : exp2f(v.x - M);
+      w = (v.x == -INFINITY) ? 0.f : fast_exp2(v.x - M);
       L = fmaf(w, v.y, L);
     }
     const int n = min(64, nsplit - c);
@@ -968,7 +968,7 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
 #pragma unroll
     for (int j = 0; j < TPT; ++j) {
       const float pr =
-          (mx[h] == -INFINITY || sc[h][j] == -INFINITY) ? 0.f : exp2f(sc[h][j] - mx[h]);
+          (mx[h] == -INFINITY || sc[h][j] == -INFINITY) ? 0.f : fast_exp2(sc[h][j] - mx[h]);
       s_p[h][tid + kAttnThreads * j] = pr * vs_own[j];
       l += pr;
     }

@@ -39,21 +39,22 @@ __device__ __forceinline__ void load_kv_block(const uint16_t* __restrict__ k,
                                               const uint16_t* __restrict__ v, int Hkv, int L,
                                               int k0, int tid, u32x4 (&kreg)[4],
                                               u32x4 (&vreg)[2][2]) {
-  const size_t row = (size_t)Hkv * kPD;
+  // element offsets from the sequence's first row in 32 bits with 24-bit multiplies (the host
+  // checks max_seqlen * Hkv * 128 < 2^31)
+  const unsigned row = (unsigned)Hkv * kPD;
+  const int kk = k0 + (tid >> 4), kc = (tid & 15) * 8;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const int idx = tid + 256 * j;
-    const int kr = min(k0 + (idx >> 4), L - 1);
-    kreg[j] = *reinterpret_cast<const u32x4*>(k + kr * row + (idx & 15) * 8);
+    const unsigned kr = (unsigned)min(kk + 16 * j, L - 1);
+    kreg[j] = *reinterpret_cast<const u32x4*>(k + (__umul24(kr, row) + kc));
   }
+  const int vk = k0 + 2 * (tid & 31), vc = (tid >> 5) * 8;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
-    const int idx = tid + 256 * i;
-    const int p = idx & 31, c = idx >> 5;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int kr = min(k0 + 2 * p + u, L - 1);
-      vreg[i][u] = *reinterpret_cast<const u32x4*>(v + kr * row + c * 8);
+      const unsigned kr = (unsigned)min(vk + u, L - 1);
+      vreg[i][u] = *reinterpret_cast<const u32x4*>(v + (__umul24(kr, row) + vc + 64 * i));
     }
   }
 }
@@ -72,7 +73,8 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
   const int q0 = qb * kPQ;
   if (q0 >= L) return;
   const int g = h / (Hq / Hkv);
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar mask branches
   const int r16 = lane & 15, kq = lane >> 4;
 
   // Q fragments (B operand of S^T): column r16 = query q0 + wave*32 + t*16 + r16 (clamped),
@@ -173,13 +175,13 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
       mx = fmaxf(mx, __shfl_xor(mx, 32));
       // key 0 of block 0 is visible to every query, so mn is finite from the first block on
       const float mn = fmaxf(m[t], mx * scale_log2);
-      const float alpha = exp2f(m[t] - mn);
+      const float alpha = fast_exp2(m[t] - mn);
       float rs = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float pj = exp2f(fmaf(sc[t][j][i], scale_log2, -mn));
+          const float pj = fast_exp2(fmaf(sc[t][j][i], scale_log2, -mn));
           sc[t][j][i] = pj;
           rs += pj;
         }
@@ -247,6 +249,8 @@ extern "C" int sym_prefill_attention(const void* q, const void* k, const void* v
   SYM_REQUIRE(Hkv >= 1 && Hq >= Hkv && Hq % Hkv == 0 && Hq <= 65535, SYM_ERR_INVALID,
               "prefill_attention: Hq=%d Hkv=%d", Hq, Hkv);
   SYM_REQUIRE(n_seqs <= 65535, SYM_ERR_INVALID, "prefill_attention: n_seqs=%d", n_seqs);
+  SYM_REQUIRE((long long)max_seqlen * Hkv * kPD < (1LL << 31), SYM_ERR_UNSUPPORTED,
+              "prefill_attention: max_seqlen=%d x Hkv=%d too large", max_seqlen, Hkv);
   (void)hipGetLastError();
   hipLaunchKernelGGL(prefill_attention_kernel, dim3((max_seqlen + kPQ - 1) / kPQ, Hq, n_seqs),
                      dim3(256), 0, (hipStream_t)stream, (const uint16_t*)q, (const uint16_t*)k,
