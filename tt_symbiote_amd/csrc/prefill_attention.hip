@@ -24,6 +24,7 @@ constexpr int kPD = 128;           // head dim
 constexpr int kPQ = 128;           // queries per workgroup
 constexpr int kPK = 64;            // keys per block
 constexpr int kPKStride = kPD + 8; // LDS row stride of K (elements)
+constexpr float kLazyMax = 8.f;      // log2 headroom of the lazily rescaled softmax
 constexpr int kPVStride = kPK + 4; // LDS row stride of V^T: 34 dwords, so the 16 rows of an
                                    // 8-byte fragment read start in distinct bank pairs
 
@@ -173,9 +174,14 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[t][j][i]);
       mx = fmaxf(mx, __shfl_xor(mx, 16));
       mx = fmaxf(mx, __shfl_xor(mx, 32));
-      // key 0 of block 0 is visible to every query, so mn is finite from the first block on
-      const float mn = fmaxf(m[t], mx * scale_log2);
-      const float alpha = fast_exp2(m[t] - mn);
+      // Lazy rescaling: the running max (log2 domain) moves only when a score exceeds it by more
+      // than kLazyMax, so the weights stay below 2^kLazyMax and most blocks skip the rescale of
+      // the output; the result is the same softmax. Key 0 of block 0 is visible to every query,
+      // so the max is finite from the first block on.
+      const float mxs = mx * scale_log2;
+      const bool grow = mxs > m[t] + kLazyMax;  // true on the first block (m = -inf)
+      const float mn = grow ? mxs : m[t];
+      const float alpha = grow ? fast_exp2(m[t] - mn) : 1.f;
       float rs = 0.f;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
