@@ -447,7 +447,7 @@ def decode_main(args, fp8: bool) -> None:
         kq, ks = fp8_kv_pools(ctx.k_pool)
         vq, vs = fp8_kv_pools(ctx.v_pool)
         cache.key_cache(0).copy_(kq)
-        cache.value_cache(0).copy_(vq)
+        cache.value_cache(0).copy_(hip_ops.fp8_v_pool(vq))
         cache.key_scale(0).copy_(ks)
         cache.value_scale(0).copy_(vs)
         del kq, vq
@@ -596,6 +596,7 @@ def cpu_baseline_fp8(layer, w_gpu, shape, ctx, cache, x, steps: int) -> dict:
     import torch
 
     from oracle.fp8 import decode_e4m3, dequant_blocks
+    from tt_symbiote_amd import hip_ops
 
     E = shape.num_experts
     dq = {}
@@ -608,11 +609,12 @@ def cpu_baseline_fp8(layer, w_gpu, shape, ctx, cache, x, steps: int) -> dict:
     n = min(16, x.shape[0])
 
     def pool(codes, scales):
-        vals = torch.from_numpy(decode_e4m3(codes.view(torch.uint8).cpu().numpy()))
+        vals = torch.from_numpy(decode_e4m3(codes.contiguous().view(torch.uint8).cpu().numpy()))
         return vals * scales.cpu()[..., None, None]
 
     sub = types.SimpleNamespace(k_pool=pool(cache.key_cache(0), cache.key_scale(0)),
-                                v_pool=pool(cache.value_cache(0), cache.value_scale(0)),
+                                v_pool=pool(hip_ops.fp8_v_rows(cache.value_cache(0)),
+                                            cache.value_scale(0)),
                                 page_table=ctx.page_table[:n], positions=ctx.positions[:n])
     r = cpu_baseline(w, shape, sub, x[:n], steps)
     r["sample"] = (f"{steps} decode steps (median, after 2 warm-up) of the same layer on the "

@@ -188,13 +188,14 @@ int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const void* k_no
                          void* stream);
 
 /* ---------------------------------------------------------------------------------------
- * fp8 KV cache (the "fp8-KV variant with kv_scales" of the paged decode). Pools
- * [num_blocks, Hkv, block_size, 128] hold OCP fp8 e4m3fn bytes; k_scale / v_scale
- * [num_blocks, Hkv] fp32 hold one power-of-two scale per (block, kv head); a stored value is
- * byte value * scale. Appending tokens to a block: s_new = max(s_old, pow2_ceil(amax / 448))
+ * fp8 KV cache (the "fp8-KV variant with kv_scales" of the paged decode). The K pool
+ * [num_blocks, Hkv, block_size, 128] and the V pool [num_blocks, Hkv, 128, block_size] (dim-major
+ * inside each (block, head): byte (d, slot) at d * block_size + slot, the operand layout of the
+ * attention's P.V MFMA) hold OCP fp8 e4m3fn bytes; k_scale / v_scale [num_blocks, Hkv] fp32 hold
+ * one power-of-two scale per (block, kv head); a stored value is byte value * scale. Appending tokens to a block: s_new = max(s_old, pow2_ceil(amax / 448))
  * (s_old = 0 for an empty block); when the scale grows, the block's earlier bytes c become
  * e4m3(value(c) * s_old / s_new); new tokens are e4m3(x / s_new) with x their bf16 values
- * (round to nearest even). block_size must divide 256. The reference's cache is bf16
+ * (round to nearest even). block_size is a multiple of 8 dividing 256. The reference's cache is bf16
  * (TTNNPagedAttentionKVCache, ttnn_attention.py:116-137); the layout and page-table semantics
  * are the same.
  * sym_paged_kv_fill_fp8: appends tokens cu_seqlens[s] + i (i < L_s) of n_seqs sequences at

@@ -79,9 +79,11 @@ def test_grouped_swiglu_fp8(device, T, E, H, I, top_k, skew):
 
 # ------------------------------------------------------------------------------ KV fill
 def _fp8_pools(nb, Hkv, bs, device):
-    z = torch.zeros(nb, Hkv, bs, 128, dtype=torch.float8_e4m3fn, device=device)
+    """Empty fp8 pools: K [nb, Hkv, bs, 128], V dim-major [nb, Hkv, 128, bs], and scales."""
+    zk = torch.zeros(nb, Hkv, bs, 128, dtype=torch.float8_e4m3fn, device=device)
+    zv = torch.zeros(nb, Hkv, 128, bs, dtype=torch.float8_e4m3fn, device=device)
     s = torch.zeros(nb, Hkv, dtype=torch.float32, device=device)
-    return z, z.clone(), s, s.clone()
+    return zk, zv, s, s.clone()
 
 
 def _oracle_fill(kp, vp, ks, vs, k, v, cu, starts, table, bs):
@@ -145,7 +147,8 @@ def test_kv_fill_fp8_bit_exact(device):
     assert np.array_equal(ks.cpu().numpy(), oks)
     assert np.array_equal(vs.cpu().numpy(), ovs)
     assert np.array_equal(kp.view(torch.uint8).cpu().numpy(), okp)
-    assert np.array_equal(vp.view(torch.uint8).cpu().numpy(), ovp)
+    # the V pool is dim-major inside each (block, head); the oracle keeps token rows
+    assert np.array_equal(hip_ops.fp8_v_rows(vp.view(torch.uint8)).cpu().numpy(), ovp)
 
 
 def test_kv_fill_fp8_htd_layout_and_skips(device):
@@ -179,7 +182,7 @@ def _random_fp8_cache(nb, Hkv, bs, seed, device):
     codes = codes.to(torch.uint8)
     scales = 2.0 ** torch.randint(-9, -4, (2, nb, Hkv), generator=g).float()
     kp = codes[0].view(torch.float8_e4m3fn).to(device)
-    vp = codes[1].view(torch.float8_e4m3fn).to(device)
+    vp = hip_ops.fp8_v_pool(codes[1].view(torch.float8_e4m3fn)).to(device)  # dim-major V
     return kp, vp, scales[0].to(device), scales[1].to(device), codes, scales
 
 
@@ -305,6 +308,7 @@ def test_decoder_layer_fp8(device):
     vp, vs = fp8_kv_pools(ctx.v_pool.to(device))
     codes = torch.stack([kp.view(torch.uint8).cpu(), vp.view(torch.uint8).cpu()])
     scales = torch.stack([ks.cpu(), vs.cpu()])
+    vp = hip_ops.fp8_v_pool(vp)  # the cache's V layout
     pcfg = ts.PagedAttentionConfig(block_size=cfg["block_size"], max_num_blocks=nb, batch_size=1)
     cache = ts.HIPPagedAttentionKVCache(1, 4, 128, pcfg, dtype=torch.float8_e4m3fn)
     cache.to_device(device)

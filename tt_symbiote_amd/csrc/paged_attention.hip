@@ -34,9 +34,10 @@ constexpr int kTPW8 = 64;
 #endif
 constexpr int kSplit8 = 4 * kTPW8;
 // fp8 split kernel: V is loaded after the scores (into the registers K used) and the kernel is
-// held to 5 workgroups per CU (92 VGPRs at 4 query heads per kv head; 8 heads per kv head would
-// spill and keep the default): 197 against 210 us at batch 128 with 1024-8192 contexts. Late V
-// alone (98 registers, still 4 per CU) measured 218 us.
+// held to 6 workgroups per CU at up to 4 query heads per kv head (80 VGPRs with P.V on MFMA, 2
+// of them spilled: 164 against 170 us at 5 per CU, 82 VGPRs, at batch 128 with 1024-8192
+// contexts); 8 heads per kv head keep the default. (With P.V on the VALU: late V and 5 per CU,
+// 92 VGPRs, 197 us; late V alone at 4 per CU 218 us; V with K 210 us.)
 #ifdef SYM_FP8_LATE_V
 constexpr bool kLateV8 = SYM_FP8_LATE_V != 0;
 #else
@@ -45,7 +46,7 @@ constexpr bool kLateV8 = true;
 #ifdef SYM_FP8_MIN_BLOCKS
 constexpr int kFp8MinBlocks = SYM_FP8_MIN_BLOCKS;
 #else
-constexpr int kFp8MinBlocks = 5;
+constexpr int kFp8MinBlocks = 6;
 #endif
 #ifdef SYM_BF16_MIN_BLOCKS
 constexpr int kBf16MinBlocks = SYM_BF16_MIN_BLOCKS;
@@ -597,8 +598,11 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
 }
 
 // ---------------------------------------------------------------------------------------------
-// fp8 e4m3fn KV cache: pools [num_blocks, Hkv, block_size, 128] of e4m3fn bytes and one fp32
-// scale per (block, kv head), scales [num_blocks, Hkv]; a stored value is byte value * scale.
+// fp8 e4m3fn KV cache: K pool [num_blocks, Hkv, block_size, 128] and V pool
+// [num_blocks, Hkv, 128, block_size] of e4m3fn bytes (V dim-major inside each (block, head):
+// the bytes of one dim for consecutive slots are contiguous, which is the layout of the P.V
+// MFMA operand), and one fp32 scale per (block, kv head), scales [num_blocks, Hkv]; a stored
+// value is byte value * scale. block_size is a multiple of 8 that divides 256.
 // Scales are powers of two. Appending tokens to a block (prefill fill or the decode write):
 //   s_new = max(s_old, pow2_ceil(amax(new tokens) / 448))     (s_old = 0 for an empty block)
 //   if the block already holds tokens and s_new > s_old, each of their bytes c becomes
@@ -621,14 +625,19 @@ __device__ __forceinline__ uint32_t fp8x4_rescale(uint32_t w, float r) {
   return f32x4_to_fp8x4(lo.x * r, lo.y * r, hi.x * r, hi.y * r);
 }
 
-// 8 e4m3fn bytes (lo word: dims 0-3, hi word: dims 4-7) -> 8 floats.
-__device__ __forceinline__ void fp8x8_to_f32(uint2 w, float* f) {
-  const floatx2 a = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, false);
-  const floatx2 b = __builtin_amdgcn_cvt_pk_f32_fp8(w.x, true);
-  const floatx2 c = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, false);
-  const floatx2 d = __builtin_amdgcn_cvt_pk_f32_fp8(w.y, true);
-  f[0] = a.x; f[1] = a.y; f[2] = b.x; f[3] = b.y;
-  f[4] = c.x; f[5] = c.y; f[6] = d.x; f[7] = d.y;
+// value(c) * r for one byte c, re-encoded (r <= 1).
+__device__ __forceinline__ uint8_t fp8_rescale1(uint8_t c, float r) {
+  const floatx2 v = __builtin_amdgcn_cvt_pk_f32_fp8((uint32_t)c, false);
+  return (uint8_t)(__builtin_amdgcn_cvt_pk_fp8_f32(v.x * r, 0.f, 0, false) & 0xff);
+}
+
+// Byte mask of 8 flags: byte i (lo word bytes 0-3, hi word bytes 4-7) is 0xff when bit i of m
+// is set. (m & 0xf) * 0x00204081 moves bit i to bit 8i (the other partial products land
+// elsewhere), & 0x01010101 keeps those, * 0xff fills the bytes.
+__device__ __forceinline__ uint2 byte_mask8(uint32_t m) {
+  const uint32_t lo = (((m & 0xfu) * 0x00204081u) & 0x01010101u) * 0xffu;
+  const uint32_t hi = ((((m >> 4) & 0xfu) * 0x00204081u) & 0x01010101u) * 0xffu;
+  return make_uint2(lo, hi);
 }
 
 // Fill: grid (ceil(max_seqlen / block_size) + 1, Hkv, n_seqs), 256 threads; workgroup = the
@@ -696,9 +705,13 @@ __global__ __launch_bounds__(256) void paged_kv_fill_fp8_kernel(
     for (int i = tid; i < nw_old; i += 256) w[i] = fp8x4_rescale(w[i], r);
   }
   if (sv > sv_old && n_old > 0) {
+    // V is dim-major: the earlier tokens are bytes [0, n_old) of each of the 128 dim rows
     const float r = sv_old / sv;
-    uint32_t* w = reinterpret_cast<uint32_t*>(vb);
-    for (int i = tid; i < nw_old; i += 256) w[i] = fp8x4_rescale(w[i], r);
+    for (int i = tid; i < n_old * kHeadDim; i += 256) {
+      const int d = i / n_old, sl = i - d * n_old;
+      uint8_t* pv = vb + (size_t)d * block_size + sl;
+      *pv = fp8_rescale1(*pv, r);
+    }
   }
   // the new tokens
   for (int c = tid; c < nchunk; c += 256) {
@@ -721,7 +734,13 @@ __global__ __launch_bounds__(256) void paged_kv_fill_fp8_kernel(
       q.y = f32x4_to_fp8x4(clamp_fp8(f[4] / sv), clamp_fp8(f[5] / sv), clamp_fp8(f[6] / sv),
                            clamp_fp8(f[7] / sv));
     }
-    *reinterpret_cast<uint2*>(vb + dst) = q;
+    // dim-major V: byte i of the chunk goes to dim (c % 16) * 8 + i, slot n_old + c / 16
+    uint8_t* vd = vb + (size_t)((c % 16) * 8) * block_size + n_old + c / 16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      vd[(size_t)i * block_size] = (uint8_t)(q.x >> (8 * i));
+      vd[(size_t)(i + 4) * block_size] = (uint8_t)(q.y >> (8 * i));
+    }
   }
   if (tid == 0) {
     k_scale[sidx] = sk;
@@ -734,7 +753,7 @@ __global__ __launch_bounds__(256) void paged_kv_fill_fp8_kernel(
 __device__ __forceinline__ void fp8_append_token(uint8_t* __restrict__ pool,
                                                  float* __restrict__ scales, int phys, int g,
                                                  int Hkv, int block_size, int off, float x0,
-                                                 float x1, int lane) {
+                                                 float x1, int lane, bool dim_major) {
   const float amax = wave_max(fmaxf(fabsf(x0), fabsf(x1)));
   const size_t sidx = (size_t)phys * Hkv + g;
   const float s_old = off > 0 ? scales[sidx] : 0.f;
@@ -742,25 +761,42 @@ __device__ __forceinline__ void fp8_append_token(uint8_t* __restrict__ pool,
   uint8_t* blk = pool + sidx * block_size * kHeadDim;
   if (off > 0 && s_new > s_old) {
     const float r = s_old / s_new;
-    uint32_t* w = reinterpret_cast<uint32_t*>(blk);
-    for (int i = lane; i < off * (kHeadDim / 4); i += 64) w[i] = fp8x4_rescale(w[i], r);
+    if (dim_major) {
+      // the earlier tokens are bytes [0, off) of each of the 128 dim rows
+      for (int i = lane; i < off * kHeadDim; i += 64) {
+        const int d = i / off, sl = i - d * off;
+        uint8_t* p = blk + (size_t)d * block_size + sl;
+        *p = fp8_rescale1(*p, r);
+      }
+    } else {
+      uint32_t* w = reinterpret_cast<uint32_t*>(blk);
+      for (int i = lane; i < off * (kHeadDim / 4); i += 64) w[i] = fp8x4_rescale(w[i], r);
+    }
   }
   uint32_t q = 0;
   if (s_new > 0.f)
     q = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(clamp_fp8(x0 / s_new), clamp_fp8(x1 / s_new),
                                                   0, false);
-  blk[(size_t)off * kHeadDim + lane] = (uint8_t)(q & 0xffu);
-  blk[(size_t)off * kHeadDim + lane + 64] = (uint8_t)((q >> 8) & 0xffu);
+  if (dim_major) {
+    blk[(size_t)lane * block_size + off] = (uint8_t)(q & 0xffu);
+    blk[(size_t)(lane + 64) * block_size + off] = (uint8_t)((q >> 8) & 0xffu);
+  } else {
+    blk[(size_t)off * kHeadDim + lane] = (uint8_t)(q & 0xffu);
+    blk[(size_t)off * kHeadDim + lane + 64] = (uint8_t)((q >> 8) & 0xffu);
+  }
   if (lane == 0) scales[sidx] = s_new;
 }
 
 // Split-K decode over the fp8 cache, same workgroup shape and outputs as paged_decode_kernel.
 //   K in the MFMA B layout: lane l holds bytes [32*(l/16), +32) of token l%16 of a 16-token tile
 //   (two 16-byte loads); MFMA j takes its bytes 8j .. 8j+7, converted exactly to bf16, against
-//   the query dims 32*(l/16) + 8j .. +7 from LDS. V for P.V: 8 bytes (dims r16*8 .. +7) of one
-//   token per step. A token's K scale multiplies its score and its V scale its probability in
-//   P.V (the softmax sum uses the unscaled probability), so the dequantised values are never
-//   formed. In the fused step the workgroup of the sequence's last split first appends the new
+//   the query dims 32*(l/16) + 8j .. +7 from LDS. P.V on MFMA too: per 32-token k-step the A
+//   operand is P (query heads as rows, bf16, lanes of rows >= G zero) and the B operand of
+//   column tile j is V dim-major: lane l takes the 8 bytes of dim 16j + l%16 for the tokens
+//   8*(l/16) .. +7 of the k-step (one aligned 8-byte piece of a block's dim row), bytes of
+//   tokens outside the sequence zeroed. A token's K scale multiplies its score and its V scale
+//   its probability in P.V (the softmax sum uses the unscaled probability), so the dequantised
+//   values are never formed. In the fused step the workgroup of the sequence's last split first appends the new
 //   token's k and v to the pool (with any requantisation of its block), then reads the split
 //   from the pool like every other workgroup; a block never straddles two splits (block_size
 //   divides 256, and the split is a multiple of 256 tokens), so no other workgroup reads the
@@ -777,10 +813,9 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
   constexpr int TPW = kTPW8;
   constexpr int SPLIT = kSplit8;
   constexpr int KT = TPW / 16;                 // 16-token K tiles per wave
-  constexpr int VS = TPW / 4;                  // P.V steps per wave
   constexpr int TPT = SPLIT / kAttnThreads;    // tokens per thread in the softmax
   __shared__ __align__(16) uint16_t s_q[G][D];
-  __shared__ float s_p[G][SPLIT];
+  __shared__ __align__(16) float s_p[G][SPLIT];
   __shared__ float s_red[4][G][D];
   __shared__ float s_stat[G][4];
   __shared__ float s_fin[2][G];
@@ -864,13 +899,23 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
 
   const int wt0 = wave * TPW;
   uint4 kb[KT][2];
-  uint2 vreg[VS];
+  // P.V operands: k-step ks covers tokens wt0 + 32 ks .. +31; lane l's 8 tokens start at
+  // wt0 + 32 ks + 8 kg, all in one block (block_size % 8 == 0, aligned). A group past the
+  // sequence reads the aligned piece of the split's last token (its row in s_row), in bounds.
+  static_assert(TPW == 64 && TPT == 1, "P.V MFMA tiling assumes 64 tokens per wave");
+  constexpr int KS = TPW / 32;
+  uint2 vreg[KS][D / 16];
   float ks_own[TPT], vs_own[TPT];
   auto load_v = [&]() {
 #pragma unroll
-    for (int it = 0; it < VS; ++it)
-      vreg[it] = *reinterpret_cast<const uint2*>(v_pool + (size_t)s_row[wt0 + it * 4 + kg] * D +
-                                                 r16 * 8);
+    for (int ks = 0; ks < KS; ++ks) {
+      const unsigned row = s_row[wt0 + 32 * ks + 8 * kg];
+      const unsigned o = row & (unsigned)(block_size - 1);
+      const uint8_t* vb = v_pool + (size_t)(row - o) * D + (o & ~7u) + (size_t)r16 * block_size;
+#pragma unroll
+      for (int j = 0; j < D / 16; ++j)
+        vreg[ks][j] = *reinterpret_cast<const uint2*>(vb + (size_t)(16 * j) * block_size);
+    }
   };
   auto issue_loads = [&]() {
 #pragma unroll
@@ -905,7 +950,8 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
           const int phys = slot_block(block_tables, b, pos, mbps, block_size, num_blocks, &off);
           if (phys >= 0)
             fp8_append_token(job == G ? k_pool : v_pool, job == G ? k_scale : v_scale, phys, g,
-                             Hkv, block_size, off, bf16_to_f32(y0), bf16_to_f32(y1), lane);
+                             Hkv, block_size, off, bf16_to_f32(y0), bf16_to_f32(y1), lane,
+                             job != G);
         }
       }
     }
@@ -977,39 +1023,37 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
   }
   __syncthreads();
 
-  // ---- P.V ----
-  float acc[G][8];
+  // ---- P.V on MFMA: O[head][dim] += P[head][token] . V[token][dim] per 32-token k-step ----
+  const unsigned long long okw = __ballot(my_ok[0]);  // validity of this wave's 64 tokens
+  floatx4 oacc[D / 16];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int j = 0; j < D / 16; ++j) oacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
+  for (int ks = 0; ks < KS; ++ks) {
+    const int tl0 = wt0 + 32 * ks + 8 * kg;
+    // A: P of head r16 (P already carries the V scale) for the lane's 8 tokens, in bf16
+    const float4 p0 = *reinterpret_cast<const float4*>(&s_p[min(r16, G - 1)][tl0]);
+    const float4 p1 = *reinterpret_cast<const float4*>(&s_p[min(r16, G - 1)][tl0 + 4]);
+    uint4 pa = make_uint4(pack_bf16x2(p0.x, p0.y), pack_bf16x2(p0.z, p0.w),
+                          pack_bf16x2(p1.x, p1.y), pack_bf16x2(p1.z, p1.w));
+    if (r16 >= G) pa = make_uint4(0u, 0u, 0u, 0u);
+    // bytes of tokens outside the sequence (or of an invalid block) are zeroed: their P is 0,
+    // and a slot never written may hold any byte
+    const uint2 m = byte_mask8((uint32_t)(okw >> (32 * ks + 8 * kg)) & 0xffu);
 #pragma unroll
-  for (int it = 0; it < VS; ++it) {
-    const int tl = wt0 + it * 4 + kg;
-    float vf[8];
-    fp8x8_to_f32(vreg[it], vf);
-#pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float pr = s_p[h][tl];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(pr, vf[i], acc[h][i]);
+    for (int j = 0; j < D / 16; ++j) {
+      const uint2 w = make_uint2(vreg[ks][j].x & m.x, vreg[ks][j].y & m.y);
+      oacc[j] = mfma16x16x32(pa, fp8x8_to_bf16x8(w.x, w.y), oacc[j]);
     }
   }
+  // lane l holds rows 4*(l/16) + i (heads) of column 16j + l%16
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int j = 0; j < D / 16; ++j)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = acc[h][i];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      acc[h][i] = v;
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kg + i;
+      if (h < G) s_red[wave][h][16 * j + r16] = oacc[j][i];
     }
-  if (kg == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s_red[wave][h][r16 * 8 + i] = acc[h][i];
-  }
   if (tid < G) {
     s_fin[0][tid] = mx[tid];
     s_fin[1][tid] = (s_stat[tid][0] + s_stat[tid][1]) + (s_stat[tid][2] + s_stat[tid][3]);
@@ -1185,8 +1229,9 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
               SYM_ERR_INVALID, "%s: null pointer argument", what);
   const bool fp8 = k_scale != nullptr;
   SYM_REQUIRE(fp8 == (v_scale != nullptr), SYM_ERR_INVALID, "%s: k_scale and v_scale", what);
-  SYM_REQUIRE(!fp8 || kSplit % block_size == 0, SYM_ERR_UNSUPPORTED,
-              "%s: fp8 cache needs block_size dividing %d (got %d)", what, kSplit, block_size);
+  SYM_REQUIRE(!fp8 || (kSplit % block_size == 0 && block_size % 8 == 0), SYM_ERR_UNSUPPORTED,
+              "%s: fp8 cache needs block_size a multiple of 8 dividing %d (got %d)", what, kSplit,
+              block_size);
   SYM_REQUIRE(Hq >= Hkv && Hq % Hkv == 0, SYM_ERR_INVALID, "%s: Hq=%d not a multiple of Hkv=%d",
               what, Hq, Hkv);
   const int G = Hq / Hkv;
@@ -1350,8 +1395,9 @@ extern "C" int sym_paged_kv_fill_fp8(const void* k, const void* v, long long tok
   if (n_seqs == 0 || max_seqlen == 0) return SYM_OK;
   SYM_REQUIRE(k && v && cu_seqlens && k_pool && v_pool && k_scale && v_scale && block_tables,
               SYM_ERR_INVALID, "paged_kv_fill_fp8: null pointer argument");
-  SYM_REQUIRE(kSplit % block_size == 0, SYM_ERR_UNSUPPORTED,
-              "paged_kv_fill_fp8: block_size=%d must divide %d", block_size, kSplit);
+  SYM_REQUIRE(kSplit % block_size == 0 && block_size % 8 == 0, SYM_ERR_UNSUPPORTED,
+              "paged_kv_fill_fp8: block_size=%d must be a multiple of 8 dividing %d", block_size,
+              kSplit);
   SYM_REQUIRE(n_seqs <= 65535 && Hkv <= 65535, SYM_ERR_INVALID, "paged_kv_fill_fp8: grid");
   SYM_REQUIRE(tok_stride > 0 && head_stride > 0 && tok_stride % 8 == 0 && head_stride % 8 == 0,
               SYM_ERR_INVALID, "paged_kv_fill_fp8: strides %lld, %lld must be positive multiples"

@@ -253,11 +253,18 @@ def _check_pools(k_pool, v_pool, block_tables, batch: int, k_scale=None,
         for t, n in ((k_scale, "k_scale"), (v_scale, "v_scale")):
             _check(t, n, torch.float32, k_pool.device)
             _check_shape(t, n, tuple(k_pool.shape[:2]))
-        if 256 % k_pool.shape[2]:
-            raise ValueError(f"fp8 KV cache: block_size {k_pool.shape[2]} must divide 256")
+        bs = k_pool.shape[2] if k_pool.dim() == 4 else 0
+        if bs < 8 or 256 % bs:
+            raise ValueError(f"fp8 KV cache: block_size {bs} must be a multiple of 8 dividing 256")
+        # the fp8 V pool is dim-major inside each (block, head): [num_blocks, Hkv, D, block_size]
+        if k_pool.dim() != 4 or v_pool.dim() != 4 or \
+                tuple(v_pool.shape) != (k_pool.shape[0], k_pool.shape[1], k_pool.shape[3], bs):
+            raise ValueError(f"fp8 pools must be K [num_blocks, Hkv, block_size, D] and V "
+                             f"[num_blocks, Hkv, D, block_size], got {tuple(k_pool.shape)} / "
+                             f"{tuple(v_pool.shape)}")
     elif k_scale is not None or v_scale is not None:
         raise ValueError("k_scale / v_scale given for a bf16 KV cache")
-    if k_pool.dim() != 4 or k_pool.shape != v_pool.shape:
+    if not fp8 and (k_pool.dim() != 4 or k_pool.shape != v_pool.shape):
         raise ValueError(f"k_pool/v_pool must be [num_blocks, Hkv, block_size, D] and equal, got "
                          f"{tuple(k_pool.shape)} / {tuple(v_pool.shape)}")
     nb, hkv, bs, d = k_pool.shape
@@ -269,6 +276,18 @@ def _check_pools(k_pool, v_pool, block_tables, batch: int, k_scale=None,
                          f"{tuple(block_tables.shape)}")
     return PagedLayout(nb, hkv, bs, d, block_tables.shape[1])
 
+
+
+def fp8_v_rows(v_pool: torch.Tensor) -> torch.Tensor:
+    """The fp8 V pool [num_blocks, Hkv, D, block_size] (dim-major inside each (block, head)) seen
+    as token rows [num_blocks, Hkv, block_size, D] (a transposed view)."""
+    return v_pool.transpose(-1, -2)
+
+
+def fp8_v_pool(rows: torch.Tensor) -> torch.Tensor:
+    """Token rows [num_blocks, Hkv, block_size, D] of fp8 V codes in the V pool's layout
+    [num_blocks, Hkv, D, block_size] (a contiguous copy)."""
+    return rows.transpose(-1, -2).contiguous()
 
 def attn_decode_prologue(qkv: torch.Tensor, positions: torch.Tensor, k_pool: torch.Tensor,
                          v_pool: torch.Tensor, block_tables: torch.Tensor, *, num_heads: int,

@@ -9,10 +9,13 @@ table ``[batch, blocks_per_sequence]`` int32 mapping logical to physical blocks 
 ``paged_sdpa_decode``, ``update_seq_length``, ``get_seq_length``, ``get_max_cache_shape``,
 ``update`` and ``reset``, with the same host-side counter semantics.
 
-An fp8 variant (``dtype=torch.float8_e4m3fn``) keeps the same pools in OCP e4m3fn bytes with
-one power-of-two fp32 scale per (block, kv head) per layer (``key_scale`` / ``value_scale``,
+An fp8 variant (``dtype=torch.float8_e4m3fn``) keeps the pools in OCP e4m3fn bytes with one
+power-of-two fp32 scale per (block, kv head) per layer (``key_scale`` / ``value_scale``,
 ``[max_num_blocks, num_kv_heads]``); appends requantise a block's earlier tokens when its scale
-grows. The reference's cache is bf16 only; the format and its rule are this build's.
+grows. Its V pool is dim-major inside each (block, head), ``[max_num_blocks, num_kv_heads,
+head_dim, block_size]`` (the operand layout of the attention's P.V; ``hip_ops.fp8_v_rows``
+views it as token rows), and block_size is a multiple of 8. The reference's cache is bf16 only;
+the format and its rule are this build's.
 
 Differences: pools are torch tensors in HBM (one allocation per pool); the page table is
 validated on the host when installed (every entry must name a block of the pool) and copied in
@@ -59,8 +62,9 @@ class HIPPagedAttentionKVCache(_CacheBase):
                 super().__init__()
         if dtype not in (torch.bfloat16, torch.float8_e4m3fn):
             raise NotImplementedError(f"KV cache dtype {dtype} (bf16 or float8_e4m3fn)")
-        if dtype == torch.float8_e4m3fn and 256 % config.block_size:
-            raise ValueError(f"fp8 KV cache: block_size {config.block_size} must divide 256")
+        if dtype == torch.float8_e4m3fn and (config.block_size % 8 or 256 % config.block_size):
+            raise ValueError(f"fp8 KV cache: block_size {config.block_size} must be a multiple "
+                             f"of 8 dividing 256")
         if head_dim != hip_ops.HEAD_DIM:
             raise NotImplementedError(f"head_dim {head_dim} (kernels implement {hip_ops.HEAD_DIM})")
         if config.blocks_per_sequence < 1:
@@ -94,9 +98,11 @@ class HIPPagedAttentionKVCache(_CacheBase):
             return self
         shape = (self.config.max_num_blocks, self.num_kv_heads, self.config.block_size,
                  self.head_dim)
+        # fp8: V dim-major inside each (block, head), [num_blocks, Hkv, head_dim, block_size]
+        v_shape = shape[:2] + (shape[3], shape[2]) if self.is_fp8 else shape
         for i in range(self.num_layers):
             self._key_cache[i] = torch.zeros(shape, dtype=self.dtype, device=device)
-            self._value_cache[i] = torch.zeros(shape, dtype=self.dtype, device=device)
+            self._value_cache[i] = torch.zeros(v_shape, dtype=self.dtype, device=device)
             if self.is_fp8:
                 self._key_scale[i] = torch.zeros(shape[:2], dtype=torch.float32, device=device)
                 self._value_scale[i] = torch.zeros(shape[:2], dtype=torch.float32, device=device)

@@ -147,7 +147,8 @@ def paged_context(batch: int, ctx_lo: int, ctx_hi: int, *, block_size: int = 32,
 def fp8_kv_pools(pool: torch.Tensor):
     """Synthetic contents of an fp8 KV cache from a bf16 pool [nb, Hkv, bs, D]: per (block,
     head) the power-of-two scale at or above amax / 448 and the e4m3fn bytes of pool / scale
-    (what appending the block's tokens to an empty block produces). Setup only."""
+    (what appending the block's tokens to an empty block produces), as token rows [nb, Hkv, bs,
+    D] (``hip_ops.fp8_v_pool`` gives a V pool's layout). Setup only."""
     amax = pool.float().abs().amax(dim=(2, 3))
     scale = torch.where(amax > 0, torch.exp2(torch.ceil(torch.log2(amax / 448.0))),
                         torch.zeros_like(amax))
