@@ -483,39 +483,49 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
   }
   __syncthreads();
 
-  // ---- P.V ----
-  float acc[G][8];
+  // ---- P.V on MFMA ----
+  // k-step ks covers steps it = 8 ks .. 8 ks + 7: lane group kg holds tokens wt0 + 4 it + kg, lane
+  // r16 dims r16*8 .. +7 of each (vreg[it]). The MFMA's k and n orders only have to agree between
+  // its operands, so MFMA c of the step takes, as column n = r16, dim r16*8 + c: B = element c of
+  // the lane's 8 tokens (v_perm of the 16-bit halves, it ascending), A = P of the same 8 tokens
+  // for head r16 (rows >= G zero). Lane (kg, r16) then holds rows 4 kg + i (heads) of the dims
+  // r16*8 + c in acc[c][i]: the layout the VALU version had after reducing over kg.
+  floatx4 pacc[8];
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int c = 0; c < 8; ++c) pacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[h][i] = 0.f;
+  for (int ks = 0; ks < VS / 8; ++ks) {
+    float pf[8];
 #pragma unroll
-  for (int it = 0; it < VS; ++it) {
-    const int tl = wt0 + it * 4 + kg;
-    float vf[8];
-    unpack8(vreg[it], vf);
+    for (int m = 0; m < 8; ++m) pf[m] = s_p[min(r16, G - 1)][wt0 + 4 * (8 * ks + m) + kg];
+    uint4 pa = make_uint4(pack_bf16x2(pf[0], pf[1]), pack_bf16x2(pf[2], pf[3]),
+                          pack_bf16x2(pf[4], pf[5]), pack_bf16x2(pf[6], pf[7]));
+    if (r16 >= G) pa = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
-    for (int h = 0; h < G; ++h) {
-      const float pr = s_p[h][tl];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[h][i] = fmaf(pr, vf[i], acc[h][i]);
+    for (int c = 0; c < 8; ++c) {
+      // 16-bit element c of vreg[it] is half c % 2 of word c / 2
+      const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
+      const uint4* v0 = &vreg[8 * ks];
+      auto word = [&](int m) -> uint32_t {
+        const uint4 x = v0[m];
+        return (c >> 1) == 0 ? x.x : (c >> 1) == 1 ? x.y : (c >> 1) == 2 ? x.z : x.w;
+      };
+      const uint4 vb = make_uint4(__builtin_amdgcn_perm(word(1), word(0), sel),
+                                  __builtin_amdgcn_perm(word(3), word(2), sel),
+                                  __builtin_amdgcn_perm(word(5), word(4), sel),
+                                  __builtin_amdgcn_perm(word(7), word(6), sel));
+      pacc[c] = mfma16x16x32(pa, vb, pacc[c]);
+      // one operand built at a time (building them all first needs 32 more registers)
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
-  for (int h = 0; h < G; ++h)
+  for (int c = 0; c < 8; ++c)
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float v = acc[h][i];
-      v += __shfl_xor(v, 16);
-      v += __shfl_xor(v, 32);
-      acc[h][i] = v;
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kg + i;
+      if (h < G) s_red[wave][h][r16 * 8 + c] = pacc[c][i];
     }
-  if (kg == 0) {
-#pragma unroll
-    for (int h = 0; h < G; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s_red[wave][h][r16 * 8 + i] = acc[h][i];
-  }
   if (tid < G) {
     s_fin[0][tid] = mx[tid];
     s_fin[1][tid] = (s_stat[tid][0] + s_stat[tid][1]) + (s_stat[tid][2] + s_stat[tid][3]);
