@@ -36,11 +36,20 @@ constexpr int kTK = SYM_TILE_K;  // 32 or 64
 constexpr int kTK = 32;  // 72 KB of LDS: two workgroups per CU (64: 144 KB, one; 10% slower)
 #endif
 constexpr int kTM = 128, kTN = 256;
-constexpr int kTileThreads = 512;
+#ifdef SYM_TILE_WN
+constexpr int kWavesN = SYM_TILE_WN;  // waves along N (2 along M, 64 rows each)
+#else
+constexpr int kWavesN = 4;
+#endif
+static_assert(kWavesN == 2 || kWavesN == 4, "waves along N");
+constexpr int kTileWaves = 2 * kWavesN;
+constexpr int kTileThreads = 64 * kTileWaves;
+constexpr int kWN = kTN / kWavesN;  // output columns per wave (B rows of its fragments)
+constexpr int kNJ = kWN / 16;       // 16-column MFMA tiles per wave
 constexpr int kAStage = kTM * kTK;  // bf16 elements of one A stage (16 KB at kTK = 64)
 constexpr int kBStage = kTN * kTK;  // bf16 elements of one B stage (32 KB)
 constexpr int kStage = kAStage + kBStage;
-constexpr int kDmaPerStep = (kAStage + kBStage) * 2 / 1024 / (kTileThreads / 64);  // per wave
+constexpr int kDmaPerStep = (kAStage + kBStage) * 2 / 1024 / kTileWaves;  // per wave
 constexpr int kChunksPerRow = kTK / 8;          // 16-byte chunks per LDS row
 constexpr int kRowsPerDma = 64 / kChunksPerRow;  // rows one wave-wide LDS-DMA instruction fills
 static_assert(kTK == 32 || kTK == 64, "tile K");
@@ -95,14 +104,15 @@ __device__ __forceinline__ void dma16(const uint16_t* g, const uint16_t* lds_bas
   asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 template <int MODE>
-__global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
+__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kTileWaves / 4 * 2)))
+void gemm_tile_kernel(TileArgs p) {
   // stage s = [A (16 KB) | B (32 KB)] at smem + s * kStage: one base address per stage keeps every
   // fragment read of the stage within the 64 KB immediate offset of an LDS instruction
   __shared__ __align__(1024) uint16_t smem[3 * kStage];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
   const int r16 = lane & 15, kq = lane >> 4;
   const int K = p.K;
 
@@ -150,10 +160,11 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
   // ---- LDS-DMA sources: this wave fills A rows 16w .. 16w+15 and B rows 32w .. 32w+31 of
   // every stage; lane l takes row + l / kChunksPerRow, slot l % kChunksPerRow, i.e. global chunk
   // slot ^ swz(row)
-  constexpr int kADma = 16 / kRowsPerDma, kBDma = 32 / kRowsPerDma;
+  constexpr int kARows = kTM / kTileWaves, kBRows = kTN / kTileWaves;  // rows filled per wave
+  constexpr int kADma = kARows / kRowsPerDma, kBDma = kBRows / kRowsPerDma;
   const int lr = lane / kChunksPerRow;
-  const int a_row_l = wave * 16 + lr;   // + kRowsPerDma * i
-  const int b_row_l = wave * 32 + lr;
+  const int a_row_l = wave * kARows + lr;   // + kRowsPerDma * i
+  const int b_row_l = wave * kBRows + lr;
   const int chunk = ((lane % kChunksPerRow) ^ tile_swz(lr)) * 8;  // swz(row) == swz(lr)
   const uint16_t* a_src[kADma];
   const uint16_t* b_src[kBDma];
@@ -180,8 +191,8 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
     }
     b_src[i] = p.w + brow * K + chunk;
   }
-  const int a_dst = wave * 16 * kTK;  // element offset of this wave's first A row in a stage
-  const int b_dst = wave * 32 * kTK;
+  const int a_dst = wave * kARows * kTK;  // element offset of this wave's first A row in a stage
+  const int b_dst = wave * kBRows * kTK;
 
   auto issue = [&](int kt, uint16_t* stage) {
     const int k = kt * kTK;
@@ -192,27 +203,29 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
   };
 
   // fragment rows of this wave: A rows wm*64 + 16i + r16; B rows per column tile j
-  int b_frag[4];
+  // GATE_UP: the first kNJ/2 tiles are gate columns wn*kWN/2 .. +kWN/2, the rest the matching
+  // up columns (B rows 128 + ...)
+  int b_frag[kNJ];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < kNJ; ++j) {
     if constexpr (MODE == kGateUp)
-      b_frag[j] = (j < 2 ? 0 : 128) + wn * 32 + (j & 1) * 16 + r16;
+      b_frag[j] = (j < kNJ / 2 ? 0 : 128) + wn * (kWN / 2) + (j % (kNJ / 2)) * 16 + r16;
     else
-      b_frag[j] = wn * 64 + j * 16 + r16;
+      b_frag[j] = wn * kWN + j * 16 + r16;
   }
   const int sw = tile_swz(r16);  // every fragment row r has swz(r) == swz(r16)
 
-  floatx4 acc[4][4];
+  floatx4 acc[4][kNJ];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < kNJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   // all fragment reads of the step are issued before its MFMAs
   auto compute = [&](const uint16_t* stage) {
     const uint16_t* sA = stage;
     const uint16_t* sB = stage + kAStage;
-    u32x4 fa[2][4], fb[2][4];
+    u32x4 fa[2][4], fb[2][kNJ];
 #pragma unroll
     for (int kh = 0; kh < kTK / 32; ++kh) {
       const int slot = ((kh * 4 + kq) ^ sw) * 8;
@@ -220,7 +233,7 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
       for (int i = 0; i < 4; ++i)
         fa[kh][i] = *reinterpret_cast<const u32x4*>(&sA[(wm * 64 + i * 16 + r16) * kTK + slot]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < kNJ; ++j)
         fb[kh][j] = *reinterpret_cast<const u32x4*>(&sB[b_frag[j] * kTK + slot]);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -229,7 +242,7 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < kNJ; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
               __builtin_bit_cast(bf16x8, fa[kh][i]), __builtin_bit_cast(bf16x8, fb[kh][j]),
               acc[i][j], 0, 0, 0);
@@ -238,13 +251,14 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
   // Step k: wait for its stage (the DMA of step k + 1 may still be in flight), barrier (every
   // wave is also done with step k - 1's stage), issue step k + 2 into that stage, MFMAs. Step k
   // uses stage k % 3.
-  static_assert(kDmaPerStep == 6 || kDmaPerStep == 3, "SYM_TILE_SYNC count");
+  static_assert(kDmaPerStep == 3 || kDmaPerStep == 6 || kDmaPerStep == 12, "SYM_TILE_SYNC count");
   const int nk = K / kTK;
   issue(0, smem);
   if (nk > 1) issue(1, smem + kStage);
   int cur = 0;  // stage of step kt (element offset)
   for (int kt = 0; kt < nk; ++kt) {
     if (kt + 1 >= nk) SYM_TILE_SYNC(0);
+    else if constexpr (kDmaPerStep == 12) SYM_TILE_SYNC(12);
     else if constexpr (kDmaPerStep == 6) SYM_TILE_SYNC(6);
     else SYM_TILE_SYNC(3);
     const int nxt = cur == 0 ? 2 * kStage : cur - kStage;  // stage of step kt + 2
@@ -263,16 +277,16 @@ __global__ __launch_bounds__(kTileThreads) void gemm_tile_kernel(TileArgs p) {
       const size_t orow = (size_t)(row0 + r);
       if constexpr (MODE == kGateUp) {
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const int col = ct * 128 + wn * 32 + j * 16 + r16;
+        for (int j = 0; j < kNJ / 2; ++j) {
+          const int col = ct * 128 + wn * (kWN / 2) + j * 16 + r16;
           if (col >= p.N) continue;
-          const float g = acc[i][j][q], u = acc[i][j + 2][q];
+          const float g = acc[i][j][q], u = acc[i][j + kNJ / 2][q];
           p.out_bf16[orow * p.N + col] = f32_to_bf16(g / (1.0f + expf(-g)) * u);
         }
       } else {
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int col = ct * kTN + wn * 64 + j * 16 + r16;
+        for (int j = 0; j < kNJ; ++j) {
+          const int col = ct * kTN + wn * kWN + j * 16 + r16;
           if (col >= p.N) continue;
           float v = acc[i][j][q];
           if constexpr (MODE == kDense) {
