@@ -557,7 +557,9 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
 
 // Merge of the splits of a sequence with more than one split (log-sum-exp rule), one wave per
 // (sequence, query head): lane l owns dims 2l, 2l+1; the split weights 2^(m_s - M) are computed
-// one split per lane and broadcast, and the partial-output loads of 8 splits are issued at once.
+// one split per lane and broadcast. The partial outputs of the first kMergeBatch splits do not
+// depend on the weights: they are loaded together with the (max, sum) pairs, right after the
+// sequence length, so that a merge of up to kMergeBatch splits waits for two round trips.
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ positions, int B, int Hq, int max_context, int max_splits,
@@ -571,19 +573,35 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(
   if (nsplit <= 1) return;  // written directly by the split kernel
   const float2* ml = reinterpret_cast<const float2*>(ws_ml) + (size_t)idx * max_splits;
   const float2* po = reinterpret_cast<const float2*>(ws_o) + (size_t)idx * max_splits * (D / 2) + lane;
-  float M = -INFINITY;
-  for (int s = lane; s < nsplit; s += 64) M = fmaxf(M, ml[s].x);
+  constexpr int kMergeBatch = 32;
+  const float2 ml0 = ml[min(lane, nsplit - 1)];  // split `lane`'s (max, sum) (lane < nsplit)
+  float2 pv0[kMergeBatch];  // splits past nsplit repeat the last one (in bounds, not used)
+#pragma unroll
+  for (int u = 0; u < kMergeBatch; ++u) pv0[u] = po[(size_t)min(u, nsplit - 1) * (D / 2)];
+  float M = lane < nsplit ? ml0.x : -INFINITY;
+  for (int s = lane + 64; s < nsplit; s += 64) M = fmaxf(M, ml[s].x);
   M = wave_max(M);
   float L = 0.f, ox = 0.f, oy = 0.f;
   for (int c = 0; c < nsplit; c += 64) {
     float w = 0.f;
     if (c + lane < nsplit) {
-      const float2 v = ml[c + lane];
+      const float2 v = c == 0 ? ml0 : ml[c + lane];
       w = (v.x == -INFINITY) ? 0.f : fast_exp2(v.x - M);
       L = fmaf(w, v.y, L);
     }
     const int n = min(64, nsplit - c);
     int j = 0;
+    if (c == 0) {
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const float wj = __shfl(w, u);
+        if (u < n) {
+          ox = fmaf(wj, pv0[u].x, ox);
+          oy = fmaf(wj, pv0[u].y, oy);
+        }
+      }
+      j = min(n, kMergeBatch);
+    }
     for (; j + 8 <= n; j += 8) {
       float2 pv[8];
 #pragma unroll
