@@ -14,8 +14,9 @@
 // sorted_tokens) form the A operand; rows past the segment repeat its last row and their outputs are dropped. Both operands use the
 // same lane -> K mapping, so the K order inside a step is free to follow memory order. Up to
 // MT row tiles (16 rows each) are accumulated per pass over the weights.
-// Segments live on the device: workgroups past *n_segments exit at once, so the grid is sized
-// for the worst case (E+1 segments) without a host synchronization.
+// Segments live on the device: a fixed grid (16 workgroups per CU) strides over the live tiles
+// (*n_segments of them times the tiles per segment), so no host synchronization is needed and no
+// workgroup is launched only to find its segment absent.
 #include "common.h"
 
 namespace sym {
@@ -130,41 +131,44 @@ __device__ __forceinline__ void gate_up_epilogue(float (*s_red)[MT][2][4][64],
 // (count, expert, offset, row count) is loaded in one round trip before the exit test; rows are
 // processed in passes of 16 (a routed expert at decode has a few rows; the shared expert's
 // second pass finds its weight rows in L2).
+#ifdef SYM_GATE_UP_WAVES
+#define SYM_GATE_UP_ATTR __attribute__((amdgpu_waves_per_eu(SYM_GATE_UP_WAVES)))
+#else
+#define SYM_GATE_UP_ATTR
+#endif
 template <int U>
-__global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
+__global__ __launch_bounds__(kGemmThreads) SYM_GATE_UP_ATTR void moe_gate_up_kernel(
     const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
     const int32_t* __restrict__ seg_expert, const int32_t* __restrict__ seg_offset,
     const int32_t* __restrict__ seg_count, const int32_t* __restrict__ n_segments,
     const uint16_t* __restrict__ w_gu, uint16_t* __restrict__ h, int tiles_per_seg) {
   __shared__ float s_red[4][1][2][4][64];
-  const int seg = blockIdx.x / tiles_per_seg;
-  const int nseg = n_segments[0];
-  const int e = seg_expert[seg];
-  const int row0 = seg_offset[seg];
-  const int cnt = seg_count[seg];
-  // used here (an empty asm), so the loads, and those of the kernel arguments, issue together
-  // in one round trip instead of being sunk past the exit test
-  asm volatile("" ::"s"(nseg), "s"(e), "s"(row0), "s"(cnt), "s"(x), "s"(sorted_tokens),
-               "s"(w_gu), "s"(h));
-  if (seg >= nseg) return;
-  const int tile = blockIdx.x - seg * tiles_per_seg;
-  const int col0 = tile * 16;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int r16 = lane & 15;
-  const int kq = lane >> 4;
-  const int nsteps = H >> 6;
-  const int s_beg = (wave * nsteps) >> 2;
-  const int s_end = ((wave + 1) * nsteps) >> 2;
-  const uint16_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * kKLane;
-  const uint16_t* wu = wg + (size_t)I * H;
+  // the grid strides over the live tiles (segments * tiles_per_seg)
+  const int ntiles = n_segments[0] * tiles_per_seg;
+  for (int wt = blockIdx.x; wt < ntiles; wt += gridDim.x) {
+    const int seg = wt / tiles_per_seg;
+    const int e = seg_expert[seg];
+    const int row0 = seg_offset[seg];
+    const int cnt = seg_count[seg];
+    const int tile = wt - seg * tiles_per_seg;
+    const int col0 = tile * 16;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const int nsteps = H >> 6;
+    const int s_beg = (wave * nsteps) >> 2;
+    const int s_end = ((wave + 1) * nsteps) >> 2;
+    const uint16_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * kKLane;
+    const uint16_t* wu = wg + (size_t)I * H;
 
-  for (int mb = 0; mb < cnt; mb += 16) {
-    const int rows = min(16, cnt - mb);
-    floatx4 accg[1], accu[1];
-    gate_up_pass<U>(x, H, sorted_tokens + row0 + mb, rows, wg, wu, s_beg, s_end, r16, kq,
-                    accg[0], accu[0]);
-    gate_up_epilogue<1>(s_red, accg, accu, wave, lane, rows, (size_t)row0 + mb, I, col0, h);
+    for (int mb = 0; mb < cnt; mb += 16) {
+      const int rows = min(16, cnt - mb);
+      floatx4 accg[1], accu[1];
+      gate_up_pass<U>(x, H, sorted_tokens + row0 + mb, rows, wg, wu, s_beg, s_end, r16, kq,
+                      accg[0], accu[0]);
+      gate_up_epilogue<1>(s_red, accg, accu, wave, lane, rows, (size_t)row0 + mb, I, col0, h);
+    }
   }
 }
 
@@ -239,38 +243,42 @@ __device__ __forceinline__ void down_store(const floatx4 (&acc0)[MT], const floa
 
 // down projection. One wave per (segment, 16 * kDownNT output columns); segment metadata in one
 // round trip before the exit test; rows in passes of 16.
+#ifdef SYM_DOWN_WAVES
+#define SYM_DOWN_ATTR __attribute__((amdgpu_waves_per_eu(SYM_DOWN_WAVES)))
+#else
+#define SYM_DOWN_ATTR
+#endif
 template <int U>
-__global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
+__global__ __launch_bounds__(kGemmThreads) SYM_DOWN_ATTR void moe_down_kernel(
     const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
     const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
     const int32_t* __restrict__ n_segments, const uint16_t* __restrict__ w_d,
     float* __restrict__ y, int tiles_per_seg) {
-  const int seg = blockIdx.x / tiles_per_seg;
-  const int nseg = n_segments[0];
-  const int e = seg_expert[seg];
-  const int row0 = seg_offset[seg];
-  const int cnt = seg_count[seg];
-  // used here (an empty asm), so the loads, and those of the kernel arguments, issue together
-  // in one round trip instead of being sunk past the exit test
-  asm volatile("" ::"s"(nseg), "s"(e), "s"(row0), "s"(cnt), "s"(hbuf), "s"(w_d), "s"(y),
-               "s"(H), "s"(I));
-  if (seg >= nseg) return;
-  const int tile = blockIdx.x - seg * tiles_per_seg;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int col0 = (tile * 4 + wave) * (16 * kDownNT);
-  if (col0 >= H) return;
-  const int r16 = lane & 15;
-  const int kq = lane >> 4;
-  const uint16_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * kKLane;
-  const uint16_t* wd1 = wd0 + (size_t)16 * I;
+  // the grid strides over the live tiles; waves are independent (no LDS), so a wave whose
+  // columns lie past H just moves on
+  const int ntiles = n_segments[0] * tiles_per_seg;
+  for (int wt = blockIdx.x; wt < ntiles; wt += gridDim.x) {
+    const int seg = wt / tiles_per_seg;
+    const int e = seg_expert[seg];
+    const int row0 = seg_offset[seg];
+    const int cnt = seg_count[seg];
+    const int tile = wt - seg * tiles_per_seg;
+    const int wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
+    const int col0 = (tile * 4 + wave) * (16 * kDownNT);
+    if (col0 >= H) continue;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const uint16_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * kKLane;
+    const uint16_t* wd1 = wd0 + (size_t)16 * I;
 
-  for (int mb = 0; mb < cnt; mb += 16) {
-    const int rows = min(16, cnt - mb);
-    floatx4 acc0[1], acc1[1];
-    down_pass<1, U, kDownNT>(hbuf + (size_t)(row0 + mb) * I, I, rows, wd0, wd1, r16, kq, acc0,
-                             acc1);
-    down_store<1, kDownNT>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
+    for (int mb = 0; mb < cnt; mb += 16) {
+      const int rows = min(16, cnt - mb);
+      floatx4 acc0[1], acc1[1];
+      down_pass<1, U, kDownNT>(hbuf + (size_t)(row0 + mb) * I, I, rows, wd0, wd1, r16, kq, acc0,
+                               acc1);
+      down_store<1, kDownNT>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
+    }
   }
 }
 
@@ -363,35 +371,35 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_fp8_kernel(
     const uint8_t* __restrict__ w_gu, const float* __restrict__ s_gu, uint16_t* __restrict__ h,
     int tiles_per_seg) {
   __shared__ float s_red[4][1][2][4][64];
-  const int seg = blockIdx.x / tiles_per_seg;
-  const int nseg = n_segments[0];
-  const int e = seg_expert[seg];
-  const int row0 = seg_offset[seg];
-  const int cnt = seg_count[seg];
-  asm volatile("" ::"s"(nseg), "s"(e), "s"(row0), "s"(cnt), "s"(x), "s"(sorted_tokens),
-               "s"(w_gu), "s"(s_gu), "s"(h));
-  if (seg >= nseg) return;
-  const int tile = blockIdx.x - seg * tiles_per_seg;
-  const int col0 = tile * 16;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int r16 = lane & 15;
-  const int kq = lane >> 4;
-  const int nsteps = H >> 7;
-  const int s_beg = (wave * nsteps) >> 2;
-  const int s_end = ((wave + 1) * nsteps) >> 2;
-  const uint8_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * 32;
-  const uint8_t* wu = wg + (size_t)I * H;
-  const int rb = (2 * I) >> 7;  // row blocks per expert
-  const float* sg = s_gu + ((size_t)e * rb + (col0 >> 7)) * nsteps;
-  const float* su = s_gu + ((size_t)e * rb + ((I + col0) >> 7)) * nsteps;
+  // the grid strides over the live tiles (as moe_gate_up_kernel)
+  const int ntiles = n_segments[0] * tiles_per_seg;
+  for (int wt = blockIdx.x; wt < ntiles; wt += gridDim.x) {
+    const int seg = wt / tiles_per_seg;
+    const int e = seg_expert[seg];
+    const int row0 = seg_offset[seg];
+    const int cnt = seg_count[seg];
+    const int tile = wt - seg * tiles_per_seg;
+    const int col0 = tile * 16;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const int nsteps = H >> 7;
+    const int s_beg = (wave * nsteps) >> 2;
+    const int s_end = ((wave + 1) * nsteps) >> 2;
+    const uint8_t* wg = w_gu + ((size_t)e * 2 * I + col0 + r16) * (size_t)H + kq * 32;
+    const uint8_t* wu = wg + (size_t)I * H;
+    const int rb = (2 * I) >> 7;  // row blocks per expert
+    const float* sg = s_gu + ((size_t)e * rb + (col0 >> 7)) * nsteps;
+    const float* su = s_gu + ((size_t)e * rb + ((I + col0) >> 7)) * nsteps;
 
-  for (int mb = 0; mb < cnt; mb += 16) {
-    const int rows = min(16, cnt - mb);
-    floatx4 accg[1], accu[1];
-    gate_up_pass_fp8<U>(x, H, sorted_tokens + row0 + mb, rows, wg, wu, sg, su, s_beg, s_end, r16,
-                        kq, accg[0], accu[0]);
-    gate_up_epilogue<1>(s_red, accg, accu, wave, lane, rows, (size_t)row0 + mb, I, col0, h);
+    for (int mb = 0; mb < cnt; mb += 16) {
+      const int rows = min(16, cnt - mb);
+      floatx4 accg[1], accu[1];
+      gate_up_pass_fp8<U>(x, H, sorted_tokens + row0 + mb, rows, wg, wu, sg, su, s_beg, s_end, r16,
+                          kq, accg[0], accu[0]);
+      gate_up_epilogue<1>(s_red, accg, accu, wave, lane, rows, (size_t)row0 + mb, I, col0, h);
+    }
   }
 }
 
@@ -403,58 +411,58 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_fp8_kernel(
     const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
     const int32_t* __restrict__ n_segments, const uint8_t* __restrict__ w_d,
     const float* __restrict__ s_d, float* __restrict__ y, int tiles_per_seg) {
-  const int seg = blockIdx.x / tiles_per_seg;
-  const int nseg = n_segments[0];
-  const int e = seg_expert[seg];
-  const int row0 = seg_offset[seg];
-  const int cnt = seg_count[seg];
-  asm volatile("" ::"s"(nseg), "s"(e), "s"(row0), "s"(cnt), "s"(hbuf), "s"(w_d), "s"(s_d),
-               "s"(y), "s"(H), "s"(I));
-  if (seg >= nseg) return;
-  const int tile = blockIdx.x - seg * tiles_per_seg;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  const int col0 = (tile * 4 + wave) * 32;
-  if (col0 >= H) return;
-  const int r16 = lane & 15;
-  const int kq = lane >> 4;
-  const int nsteps = I >> 7;
-  const uint8_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 32;
-  const uint8_t* wd1 = wd0 + (size_t)16 * I;
-  const float* sd = s_d + ((size_t)e * (H >> 7) + (col0 >> 7)) * nsteps;
+  // the grid strides over the live tiles (as moe_down_kernel)
+  const int ntiles = n_segments[0] * tiles_per_seg;
+  for (int wt = blockIdx.x; wt < ntiles; wt += gridDim.x) {
+    const int seg = wt / tiles_per_seg;
+    const int e = seg_expert[seg];
+    const int row0 = seg_offset[seg];
+    const int cnt = seg_count[seg];
+    const int tile = wt - seg * tiles_per_seg;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int col0 = (tile * 4 + wave) * 32;
+    if (col0 >= H) continue;
+    const int r16 = lane & 15;
+    const int kq = lane >> 4;
+    const int nsteps = I >> 7;
+    const uint8_t* wd0 = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 32;
+    const uint8_t* wd1 = wd0 + (size_t)16 * I;
+    const float* sd = s_d + ((size_t)e * (H >> 7) + (col0 >> 7)) * nsteps;
 
-  for (int mb = 0; mb < cnt; mb += 16) {
-    const int rows = min(16, cnt - mb);
-    const uint16_t* hr = hbuf + (size_t)(row0 + mb + min(r16, rows - 1)) * I + kq * 32;
-    floatx4 acc0[1] = {{0.f, 0.f, 0.f, 0.f}}, acc1[1] = {{0.f, 0.f, 0.f, 0.f}};
-    for (int st = 0; st < nsteps; st += U) {
-      uint4 b0[U][2], b1[U][2], a[U][4];
-      float c[U];
+    for (int mb = 0; mb < cnt; mb += 16) {
+      const int rows = min(16, cnt - mb);
+      const uint16_t* hr = hbuf + (size_t)(row0 + mb + min(r16, rows - 1)) * I + kq * 32;
+      floatx4 acc0[1] = {{0.f, 0.f, 0.f, 0.f}}, acc1[1] = {{0.f, 0.f, 0.f, 0.f}};
+      for (int st = 0; st < nsteps; st += U) {
+        uint4 b0[U][2], b1[U][2], a[U][4];
+        float c[U];
 #pragma unroll
-      for (int s = 0; s < U; ++s) c[s] = sd[st + s];
+        for (int s = 0; s < U; ++s) c[s] = sd[st + s];
 #pragma unroll
-      for (int s = 0; s < U; ++s) {
-        const int k = (st + s) << 7;
-        b0[s][0] = ld16b(wd0 + k);
-        b0[s][1] = ld16b(wd0 + k + 16);
-        b1[s][0] = ld16b(wd1 + k);
-        b1[s][1] = ld16b(wd1 + k + 16);
+        for (int s = 0; s < U; ++s) {
+          const int k = (st + s) << 7;
+          b0[s][0] = ld16b(wd0 + k);
+          b0[s][1] = ld16b(wd0 + k + 16);
+          b1[s][0] = ld16b(wd1 + k);
+          b1[s][1] = ld16b(wd1 + k + 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          const int k = (st + s) << 7;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a[s][j] = ld16(hr + k + 8 * j);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          acc0[0] = mfma_fp8_step(a[s], b0[s], acc0[0], c[s]);
+          acc1[0] = mfma_fp8_step(a[s], b1[s], acc1[0], c[s]);
+        }
       }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int s = 0; s < U; ++s) {
-        const int k = (st + s) << 7;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a[s][j] = ld16(hr + k + 8 * j);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int s = 0; s < U; ++s) {
-        acc0[0] = mfma_fp8_step(a[s], b0[s], acc0[0], c[s]);
-        acc1[0] = mfma_fp8_step(a[s], b1[s], acc1[0], c[s]);
-      }
+      down_store<1>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
     }
-    down_store<1>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
   }
 }
 
@@ -511,6 +519,27 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
 
 using namespace sym;
 
+// Grid of the decode expert GEMMs: kPersistWGsPerCU workgroups per CU (4 rounds of the 4
+// resident per CU), striding over the live tiles, or fewer when there are fewer tiles at most.
+// Measured at batch 32 (4832 live tiles): 3072 or 4096 workgroups 107 us for gate/up against
+// 113 us for one workgroup per possible tile (8224, most past the live ones exiting at once) or
+// for 5120 / 6144; down 59 against 62 us.
+constexpr int kPersistWGsPerCU = 16;
+
+static int persistent_grid(int max_tiles) {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return max_tiles < kPersistWGsPerCU * cus[dev] ? max_tiles : kPersistWGsPerCU * cus[dev];
+}
+
 static int check_gemm_args(const char* what, int T, int H, int I, int max_segments) {
   SYM_REQUIRE(T >= 0, SYM_ERR_INVALID, "%s: T=%d < 0", what, T);
   SYM_REQUIRE(H > 0 && H % 256 == 0, SYM_ERR_UNSUPPORTED,
@@ -535,7 +564,7 @@ extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t
   (void)hipGetLastError();
   const int tiles = I / 16;
   const int wave_steps = H / 256;  // K-steps of 64 per wave (4 waves split H)
-  const dim3 grid(max_segments * tiles), block(kGemmThreads);
+  const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_GATE_UP(UU)                                                                  \
   hipLaunchKernelGGL((moe_gate_up_kernel<UU>), grid, block, 0, (hipStream_t)stream,              \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
@@ -563,7 +592,7 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
   (void)hipGetLastError();
   const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
   const int steps = I / 64;  // K-steps of 64 per wave (one wave covers all of I)
-  const dim3 grid(max_segments * tiles), block(kGemmThreads);
+  const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_DOWN(UU)                                                                     \
   hipLaunchKernelGGL((moe_down_kernel<UU>), grid, block, 0, (hipStream_t)stream,                 \
                      (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
@@ -642,7 +671,7 @@ extern "C" int sym_moe_gate_up_fp8(const void* x, int T, int H, int I,
   (void)hipGetLastError();
   const int tiles = I / 16;
   const int wave_steps = H / 512;  // K-steps of 128 per wave (4 waves split H)
-  const dim3 grid(max_segments * tiles), block(kGemmThreads);
+  const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_GATE_UP_FP8(UU)                                                              \
   hipLaunchKernelGGL((moe_gate_up_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,          \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
@@ -668,7 +697,7 @@ extern "C" int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_
   (void)hipGetLastError();
   const int tiles = (H + kColsPerWG8 - 1) / kColsPerWG8;
   const int steps = I / 128;  // K-steps of 128 per wave (one wave covers all of I)
-  const dim3 grid(max_segments * tiles), block(kGemmThreads);
+  const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_DOWN_FP8(UU)                                                                 \
   hipLaunchKernelGGL((moe_down_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,             \
                      (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
