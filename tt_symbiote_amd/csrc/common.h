@@ -111,6 +111,8 @@ __device__ __forceinline__ floatx4 mfma16x16x32(const uint4& a, const uint4& b, 
 namespace sym_host {
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
+// compute units of the current device (cached per device; 256 if the query fails)
+int cu_count();
 }  // namespace sym_host
 
 #define SYM_REQUIRE(cond, code, ...)                         \

@@ -527,17 +527,8 @@ using namespace sym;
 constexpr int kPersistWGsPerCU = 16;
 
 static int persistent_grid(int max_tiles) {
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    cus[dev] = n;
-  }
-  return max_tiles < kPersistWGsPerCU * cus[dev] ? max_tiles : kPersistWGsPerCU * cus[dev];
+  const int n = kPersistWGsPerCU * sym_host::cu_count();
+  return max_tiles < n ? max_tiles : n;
 }
 
 static int check_gemm_args(const char* what, int T, int H, int I, int max_segments) {
