@@ -476,36 +476,52 @@ __device__ __forceinline__ void load_y8(const uint16_t* p, float (&f)[8]) {
   unpack8(*reinterpret_cast<const uint4*>(p), f);
 }
 
+// Top-k assignments whose row indices, weights and y rows are loaded in one batch: the row
+// loads depend on the indices, so a batch costs two round trips instead of two per assignment.
+constexpr int kCombineBatch = 8;
+
 template <typename YT>
 __global__ __launch_bounds__(256) void moe_combine_kernel(
     const YT* __restrict__ y, const int32_t* __restrict__ inv_perm,
     const float* __restrict__ topk_w, int K, int H, int shared_row0,
     const float* __restrict__ residual, uint16_t* __restrict__ out) {
   const int t = blockIdx.x;
+  const int32_t* ip = inv_perm + (size_t)t * K;
+  const float* tw = topk_w + (size_t)t * K;
   for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
+    // the shared expert's row and the residual do not depend on the routing: issued first
+    float sh[8], rs[8];
+    if (shared_row0 >= 0) load_y8(y + (size_t)(shared_row0 + t) * H + c, sh);
+    if (residual) load_y8(residual + (size_t)t * H + c, rs);
     float acc[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-    for (int k = 0; k < K; ++k) {
-      const int row = inv_perm[(size_t)t * K + k];
-      const float wk = topk_w[(size_t)t * K + k];
-      float f[8];
-      load_y8(y + (size_t)row * H + c, f);
+    for (int k0 = 0; k0 < K; k0 += kCombineBatch) {
+      // indices past K repeat the last assignment's (in-bounds) row; they are not accumulated
+      int row[kCombineBatch];
+      float wk[kCombineBatch];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += wk * f[i];
-    }
-    if (shared_row0 >= 0) {
-      float f[8];
-      load_y8(y + (size_t)(shared_row0 + t) * H + c, f);
+      for (int j = 0; j < kCombineBatch; ++j) {
+        const int k = min(k0 + j, K - 1);
+        row[j] = ip[k];
+        wk[j] = tw[k];
+      }
+      float f[kCombineBatch][8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += f[i];
+      for (int j = 0; j < kCombineBatch; ++j) load_y8(y + (size_t)row[j] * H + c, f[j]);
+      // assignments added in k order, as one at a time
+#pragma unroll
+      for (int j = 0; j < kCombineBatch; ++j)
+        if (k0 + j < K)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) acc[i] += wk[j] * f[j][i];
     }
-    if (residual) {
-      const float4* rp = reinterpret_cast<const float4*>(residual + (size_t)t * H + c);
-      const float4 r0 = rp[0], r1 = rp[1];
-      acc[0] += r0.x; acc[1] += r0.y; acc[2] += r0.z; acc[3] += r0.w;
-      acc[4] += r1.x; acc[5] += r1.y; acc[6] += r1.z; acc[7] += r1.w;
-    }
+    if (shared_row0 >= 0)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += sh[i];
+    if (residual)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += rs[i];
     uint4 o;
     o.x = pack_bf16x2(acc[0], acc[1]);
     o.y = pack_bf16x2(acc[2], acc[3]);
