@@ -157,16 +157,11 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
     bool done = false;
     if constexpr (NORM) {
       if (nsteps == U * kLinWaves) {
-        // one batch per wave: weights, activations and gamma in flight together; the sums of
-        // squares come from the activation registers, and the same registers feed the MFMAs
+        // one batch per wave: activations, weights and gamma in flight together; the sums of
+        // squares come from the activation registers, and the same registers feed the MFMAs.
+        // The activations are issued first, so the norm statistics (which wait for them only;
+        // loads complete in order) are reduced while the weights are still arriving.
         uint4 b[U][2], a[MT][U][2], gm[U][2];
-#pragma unroll
-        for (int s = 0; s < U; ++s) {
-          const int k = (s_beg + s) << 6;
-          b[s][0] = ldg16(wr + k);
-          b[s][1] = ldg16(wr + k + 8);
-        }
-        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -175,6 +170,13 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
             a[mt][s][0] = ldg16(xr[mt] + k);
             a[mt][s][1] = ldg16(xr[mt] + k + 8);
           }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          const int k = (s_beg + s) << 6;
+          b[s][0] = ldg16(wr + k);
+          b[s][1] = ldg16(wr + k + 8);
+        }
 #pragma unroll
         for (int s = 0; s < U; ++s) {
           const int k = (s_beg + s) << 6;
