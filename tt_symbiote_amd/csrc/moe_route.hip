@@ -486,6 +486,17 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
     // rows past T repeat the last row; their results are dropped
     const int m0 = min(mb + r16, T - 1), m1 = min(mb + 16 + r16, T - 1);
     floatx4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    // NORM: the first 128 partial sums of squares of the pass's rows (16 threads per row, each
+    // every 16th), issued before the weight and activation loads: loads complete in order, so
+    // the rows' r is then reduced while those are still arriving
+    const int ss_row = min(mb + (threadIdx.x >> 4), T - 1);
+    const int ss_c = threadIdx.x & 15;
+    float ss0[8];
+    if constexpr (NORM) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss0[j] = ss_parts[(size_t)min(ss_c + 16 * j, n_ss - 1) * T + ss_row];
+      __builtin_amdgcn_sched_barrier(0);
+    }
     for (int kc = 0; kc < nk; kc += 4) {
       // a group of up to 4 chunks: weights, activations (and gamma) issued first; chunks past
       // the range repeat the last chunk's loads and contribute zero (no branch, which would let
@@ -510,10 +521,12 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
           gv[c] = *reinterpret_cast<const uint2*>(gamma + k_beg + 16 * min(kc + c, nk - 1));
         if (kc == 0) {
           // r of the pass's rows: 16 threads per row, each summing every 16th partial sum
-          const int row = min(mb + (threadIdx.x >> 4), T - 1);
-          const int c = threadIdx.x & 15;
+          const int row = ss_row;
+          const int c = ss_c;
           float t = 0.f;
-          for (int i0 = c; i0 < n_ss; i0 += 128) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) t += c + 16 * j < n_ss ? ss0[j] : 0.f;
+          for (int i0 = c + 128; i0 < n_ss; i0 += 128) {
             float v[8];
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
