@@ -153,10 +153,8 @@ _lib = None
 
 
 def library_path() -> str:
-    """The library this process loads: ``$SYMBIOTE_MI355X_LIB`` when set (e.g. a build with
-    other tuning parameters, see ``python -m tt_symbiote_amd.build --help``), else the in-tree
-    build."""
-    return os.environ.get("SYMBIOTE_MI355X_LIB") or LIB_PATH
+    """The library this process loads: the in-tree build."""
+    return LIB_PATH
 
 
 def load() -> ctypes.CDLL:

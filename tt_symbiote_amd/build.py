@@ -47,22 +47,19 @@ def _hipcc() -> str:
     raise RuntimeError("hipcc not found: the gfx950 kernels cannot be built")
 
 
-def _compile_one(hipcc: str, src: str, obj_dir: str, extra: tuple) -> str:
+def _compile_one(hipcc: str, src: str, obj_dir: str) -> str:
     obj = os.path.join(obj_dir, os.path.basename(src) + ".o")
-    cmd = [hipcc, *HIP_FLAGS, *extra, "-c", src, "-o", obj]
+    cmd = [hipcc, *HIP_FLAGS, "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = False, defines=(), out: str = LIB_PATH) -> str:
-    """Compile every ``csrc/*.hip`` and link the shared library. Returns the library path.
-    ``defines`` (``NAME=VALUE`` strings) set the kernels' tuning macros, e.g. ``SYM_DOWN_U=8``;
-    a build with defines goes to ``out`` (load it with ``SYMBIOTE_MI355X_LIB=<out>``)."""
+def build(verbose: bool = False, out: str = LIB_PATH) -> str:
+    """Compile every ``csrc/*.hip`` and link the shared library. Returns the library path."""
     hipcc = _hipcc()
-    extra = tuple(f"-D{d}" for d in defines)
-    obj_dir = OBJ_DIR if not extra else out + ".objs"
+    obj_dir = OBJ_DIR
     os.makedirs(obj_dir, exist_ok=True)
     os.makedirs(os.path.dirname(os.path.abspath(out)), exist_ok=True)
     sources = sorted(
@@ -72,7 +69,7 @@ def build(verbose: bool = False, defines=(), out: str = LIB_PATH) -> str:
         raise RuntimeError(f"no HIP sources in {CSRC_DIR}")
     jobs = min(len(sources), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
-        objs = list(pool.map(lambda s: _compile_one(hipcc, s, obj_dir, extra), sources))
+        objs = list(pool.map(lambda s: _compile_one(hipcc, s, obj_dir), sources))
     tmp = out + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     proc = subprocess.run(cmd, capture_output=True, text=True)
@@ -85,13 +82,4 @@ def build(verbose: bool = False, defines=(), out: str = LIB_PATH) -> str:
 
 
 if __name__ == "__main__":
-    import argparse
-
-    ap = argparse.ArgumentParser(description="build the gfx950 kernel library")
-    ap.add_argument("--define", "-D", action="append", default=[],
-                    help="tuning macro NAME=VALUE (then --out is required)")
-    ap.add_argument("--out", default=LIB_PATH)
-    a = ap.parse_args()
-    if a.define and a.out == LIB_PATH:
-        ap.error("a build with --define needs its own --out path")
-    build(verbose=True, defines=a.define, out=a.out)
+    build(verbose=True)

@@ -37,9 +37,10 @@ class HIPModule:
         super().__init_subclass__(**kwargs)
         if HIPModule in cls.__bases__ and not cls.__dict__.get("_allow_direct_subclass", False):
             raise TypeError(
-                f"{cls.__module__}.{cls.__qualname__} extends HIPModule directly; extend "
-                "StatelessHIPModule (forward mutates no persistent state) or StatefulHIPModule "
-                "(forward mutates state; implement reset_trace_state) instead.")
+                f"{cls.__qualname__}: pick a graph-capture contract by deriving from "
+                "StatelessHIPModule (the forward leaves no state behind) or StatefulHIPModule "
+                "(the forward writes persistent state, e.g. KV slots, and must define "
+                "reset_trace_state), not from HIPModule itself")
 
     def __init__(self):
         self._device: Optional[torch.device] = None
@@ -48,7 +49,6 @@ class HIPModule:
         self._fallback_torch_layer = None
         self._unique_name: Optional[str] = None
         self._model_config = {}
-        self._bypass_tensor_wrapping = False
         self.training = False
 
     # ---- dispatch ----
@@ -226,8 +226,8 @@ class StatefulHIPModule(HIPModule):
         for klass in cls.__mro__:
             if klass is StatefulHIPModule:
                 raise TypeError(
-                    f"{cls.__module__}.{cls.__qualname__} extends StatefulHIPModule but does not "
-                    "implement reset_trace_state()")
+                    f"{cls.__qualname__} writes persistent state (StatefulHIPModule) and so "
+                    "must define reset_trace_state() for graph capture")
             if "reset_trace_state" in vars(klass):
                 break
 

@@ -30,18 +30,9 @@
 
 namespace sym {
 
-#ifdef SYM_TILE_K
-constexpr int kTK = SYM_TILE_K;  // 32 or 64
-#else
 constexpr int kTK = 32;  // 72 KB of LDS: two workgroups per CU (64: 144 KB, one; 10% slower)
-#endif
 constexpr int kTM = 128, kTN = 256;
-#ifdef SYM_TILE_WN
-constexpr int kWavesN = SYM_TILE_WN;  // waves along N (2 along M, 64 rows each)
-#else
-constexpr int kWavesN = 4;
-#endif
-static_assert(kWavesN == 2 || kWavesN == 4, "waves along N");
+constexpr int kWavesN = 4;  // waves along N (2 along M, 64 rows each)
 constexpr int kTileWaves = 2 * kWavesN;
 constexpr int kTileThreads = 64 * kTileWaves;
 constexpr int kWN = kTN / kWavesN;  // output columns per wave (B rows of its fragments)

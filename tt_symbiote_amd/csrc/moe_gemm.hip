@@ -24,11 +24,7 @@ namespace sym {
 constexpr int kGemmThreads = 256;  // 4 waves; each wave owns 16 output columns
 // 16-column tiles per wave of the down projection: one tile needs 90 + 4 registers (5 waves per
 // SIMD), two need 124 + 8 (3 per SIMD); 62.1 against 65.3 us at batch 32.
-#ifdef SYM_DOWN_NT
-constexpr int kDownNT = SYM_DOWN_NT;
-#else
 constexpr int kDownNT = 1;
-#endif
 constexpr int kColsPerWG = 4 * 16 * kDownNT;  // down projection: 4 waves x 16 * kDownNT columns
 constexpr int kColsPerWG8 = 128;              // fp8 down projection: 4 waves x 32 columns
 
@@ -39,11 +35,7 @@ __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
 // Lane -> k mapping inside a 64-wide K step (the same for both MFMA operands, so any mapping
 // is exact): lane group kq = l / 16 takes k = kKLane * kq + 0..7 for the first MFMA and the same
 // + kKHalf for the second.
-#ifdef SYM_KMAP_CONTIG
-constexpr int kKLane = 8, kKHalf = 32;   // one load instruction covers 64 contiguous bytes/row
-#else
 constexpr int kKLane = 16, kKHalf = 8;   // a lane's two loads are 32 contiguous bytes
-#endif
 
 // One pass of gate/up over 16 rows of a segment, for this wave's K-step range [s_beg, s_end)
 // (a multiple of U steps). Per batch of U K-steps: the weight loads, then the activation loads,
@@ -131,13 +123,8 @@ __device__ __forceinline__ void gate_up_epilogue(float (*s_red)[MT][2][4][64],
 // (count, expert, offset, row count) is loaded in one round trip before the exit test; rows are
 // processed in passes of 16 (a routed expert at decode has a few rows; the shared expert's
 // second pass finds its weight rows in L2).
-#ifdef SYM_GATE_UP_WAVES
-#define SYM_GATE_UP_ATTR __attribute__((amdgpu_waves_per_eu(SYM_GATE_UP_WAVES)))
-#else
-#define SYM_GATE_UP_ATTR
-#endif
 template <int U>
-__global__ __launch_bounds__(kGemmThreads) SYM_GATE_UP_ATTR void moe_gate_up_kernel(
+__global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
     const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
     const int32_t* __restrict__ seg_expert, const int32_t* __restrict__ seg_offset,
     const int32_t* __restrict__ seg_count, const int32_t* __restrict__ n_segments,
@@ -243,13 +230,8 @@ __device__ __forceinline__ void down_store(const floatx4 (&acc0)[MT], const floa
 
 // down projection. One wave per (segment, 16 * kDownNT output columns); segment metadata in one
 // round trip before the exit test; rows in passes of 16.
-#ifdef SYM_DOWN_WAVES
-#define SYM_DOWN_ATTR __attribute__((amdgpu_waves_per_eu(SYM_DOWN_WAVES)))
-#else
-#define SYM_DOWN_ATTR
-#endif
 template <int U>
-__global__ __launch_bounds__(kGemmThreads) SYM_DOWN_ATTR void moe_down_kernel(
+__global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
     const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
     const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
     const int32_t* __restrict__ n_segments, const uint16_t* __restrict__ w_d,
@@ -576,10 +558,6 @@ extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t
   hipLaunchKernelGGL((moe_gate_up_kernel<UU>), grid, block, 0, (hipStream_t)stream,              \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
                      n_segments, (const uint16_t*)w_gate_up, (uint16_t*)h, tiles)
-#ifdef SYM_GATE_UP_U
-  if (wave_steps % SYM_GATE_UP_U == 0) SYM_LAUNCH_GATE_UP(SYM_GATE_UP_U);
-  else
-#endif
   if (wave_steps % 4 == 0) SYM_LAUNCH_GATE_UP(4);
   else if (wave_steps % 2 == 0) SYM_LAUNCH_GATE_UP(2);
   else SYM_LAUNCH_GATE_UP(1);
@@ -604,10 +582,6 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
   hipLaunchKernelGGL((moe_down_kernel<UU>), grid, block, 0, (hipStream_t)stream,                 \
                      (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
                      (const uint16_t*)w_down, y, tiles)
-#ifdef SYM_DOWN_U
-  if (steps % SYM_DOWN_U == 0) SYM_LAUNCH_DOWN(SYM_DOWN_U);
-  else
-#endif
   if (steps % 4 == 0) SYM_LAUNCH_DOWN(4);
   else if (steps % 2 == 0) SYM_LAUNCH_DOWN(2);
   else SYM_LAUNCH_DOWN(1);
@@ -677,16 +651,11 @@ extern "C" int sym_moe_gate_up_fp8(const void* x, int T, int H, int I,
               SYM_ERR_INVALID, "moe_gate_up_fp8: null pointer argument");
   (void)hipGetLastError();
   const int tiles = I / 16;
-  const int wave_steps = H / 512;  // K-steps of 128 per wave (4 waves split H)
   const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_GATE_UP_FP8(UU)                                                              \
   hipLaunchKernelGGL((moe_gate_up_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,          \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
                      n_segments, (const uint8_t*)w_gate_up, s_gate_up, (uint16_t*)h, tiles)
-#ifdef SYM_FP8_GATE_UP_U
-  if (wave_steps % SYM_FP8_GATE_UP_U == 0) SYM_LAUNCH_GATE_UP_FP8(SYM_FP8_GATE_UP_U);
-  else
-#endif
   SYM_LAUNCH_GATE_UP_FP8(1);
 #undef SYM_LAUNCH_GATE_UP_FP8
   return sym_host::check_launch("moe_gate_up_fp8_kernel");
@@ -703,16 +672,11 @@ extern "C" int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_
               SYM_ERR_INVALID, "moe_down_fp8: null pointer argument");
   (void)hipGetLastError();
   const int tiles = (H + kColsPerWG8 - 1) / kColsPerWG8;
-  const int steps = I / 128;  // K-steps of 128 per wave (one wave covers all of I)
   const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_DOWN_FP8(UU)                                                                 \
   hipLaunchKernelGGL((moe_down_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,             \
                      (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
                      (const uint8_t*)w_down, s_down, y, tiles)
-#ifdef SYM_FP8_DOWN_U
-  if (steps % SYM_FP8_DOWN_U == 0) SYM_LAUNCH_DOWN_FP8(SYM_FP8_DOWN_U);
-  else
-#endif
   SYM_LAUNCH_DOWN_FP8(1);
 #undef SYM_LAUNCH_DOWN_FP8
   return sym_host::check_launch("moe_down_fp8_kernel");

@@ -13,9 +13,10 @@
 //
 // Decode kernel design (gfx950): split-K ("flash decoding"). One workgroup
 // (4 waves) owns one (sequence, kv head, 256-token split): it loads the G = Hq/Hkv query heads
-// of that kv head once and streams the split's K and V rows exactly once, all loads issued up
-// front. Scores come from MFMA (query heads as the rows of the A operand), live in LDS
-// (G x 256 fp32) for the workgroup softmax, and P.V accumulates per lane on the VALU. A merge
+// of that kv head once and streams the split's K and V rows exactly once, K issued up front and
+// V after the scores. Scores come from MFMA (query heads as the rows of the A operand), live in
+// LDS (G x 256 fp32) for the workgroup softmax, and P.V runs on the MFMA too (P of the lane's
+// tokens as the A operand, the V elements it loaded as B, with matching k orders). A merge
 // kernel combines the splits of each sequence with the log-sum-exp rule. Splits past a
 // sequence's length exit at once.
 #include "common.h"
@@ -27,32 +28,16 @@ constexpr int kTPW = 64;           // tokens per wave in the split kernel
 constexpr int kSplit = 4 * kTPW;  // tokens per split (one workgroup of 4 waves)
 // The fp8 cache's split kernel: tokens per wave (a wave of 128 tokens fits the bf16 kernel's
 // registers, but measured slower: 225 against 199 us at batch 128 with 1024-8192 contexts).
-#ifdef SYM_FP8_TPW
-constexpr int kTPW8 = SYM_FP8_TPW;
-#else
 constexpr int kTPW8 = 64;
-#endif
 constexpr int kSplit8 = 4 * kTPW8;
+static_assert(kSplit8 == kSplit, "the decode workspace is sized for kSplit-token splits");
 // fp8 split kernel: V is loaded after the scores (into the registers K used) and the kernel is
 // held to 6 workgroups per CU at up to 4 query heads per kv head (80 VGPRs with P.V on MFMA, 2
 // of them spilled: 164 against 170 us at 5 per CU, 82 VGPRs, at batch 128 with 1024-8192
 // contexts); 8 heads per kv head keep the default. (With P.V on the VALU: late V and 5 per CU,
 // 92 VGPRs, 197 us; late V alone at 4 per CU 218 us; V with K 210 us.)
-#ifdef SYM_FP8_LATE_V
-constexpr bool kLateV8 = SYM_FP8_LATE_V != 0;
-#else
-constexpr bool kLateV8 = true;
-#endif
-#ifdef SYM_FP8_MIN_BLOCKS
-constexpr int kFp8MinBlocks = SYM_FP8_MIN_BLOCKS;
-#else
 constexpr int kFp8MinBlocks = 6;
-#endif
-#ifdef SYM_BF16_MIN_BLOCKS
-constexpr int kBf16MinBlocks = SYM_BF16_MIN_BLOCKS;
-#else
 constexpr int kBf16MinBlocks = 1;
-#endif
 constexpr int kAttnThreads = 256;
 
 // ---------------------------------------------------------------------------------------------
@@ -952,7 +937,6 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
       kb[tt][0] = *reinterpret_cast<const uint4*>(kr);
       kb[tt][1] = *reinterpret_cast<const uint4*>(kr + 16);
     }
-    if constexpr (!kLateV8) load_v();
 #pragma unroll
     for (int j = 0; j < TPT; ++j) {
       ks_own[j] = k_scale[my_sidx[j]];
@@ -1013,7 +997,7 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
       if (h < G) s_p[h][tl] = sacc[i];
     }
   }
-  if constexpr (kLateV8) load_v();  // into the registers K used; arrives during the softmax
+  load_v();  // into the registers K used; arrives during the softmax
   __syncthreads();
 
   // ---- softmax statistics (log2 domain); thread tid owns tokens t0 + tid + 256 j ----

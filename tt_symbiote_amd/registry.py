@@ -28,18 +28,20 @@ TT_MODEL_REGISTRY: Dict[str, Any] = {}
 def register_recipe(hf_class_name: str) -> Callable[[type], type]:
     """Class decorator: instantiate the recipe and register it under ``hf_class_name``."""
     if not isinstance(hf_class_name, str) or not hf_class_name:
-        raise ValueError("register_recipe requires a non-empty hf_class_name string")
+        raise ValueError(f"hf_class_name must name an HF model class, got {hf_class_name!r}")
 
     def decorator(cls):
         inst = cls()
         if not hasattr(inst, "build_module_dict"):
-            raise TypeError(f"Recipe {cls.__name__} is missing build_module_dict(model)")
+            raise TypeError(f"{cls.__name__} cannot be a recipe: it defines no "
+                            "build_module_dict(model) returning the module replacements")
         if not hasattr(inst, "post_register"):
             inst.post_register = lambda model: None
         if not hasattr(inst, "make_kv_cache"):
             inst.make_kv_cache = lambda model, device, **kwargs: None
         if hf_class_name in TT_MODEL_REGISTRY:
-            warnings.warn(f"Overriding existing recipe for {hf_class_name!r}", stacklevel=2)
+            warnings.warn(f"{cls.__name__} replaces the recipe already registered for "
+                          f"{hf_class_name!r}", stacklevel=2)
         TT_MODEL_REGISTRY[hf_class_name] = inst
         return cls
 
