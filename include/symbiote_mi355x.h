@@ -169,6 +169,24 @@ int sym_paged_gqa_decode(const void* q, const void* k_pool, const void* v_pool,
                          size_t workspace_bytes, void* out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Allocation-free paged GQA decode. No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). Same arguments, kernels and results as sym_paged_gqa_decode, without
+ * the workspace: the per-split partial results live in a fixed 32 MiB device array inside the
+ * library, one copy per GPU, held until the process ends. Calls whose
+ * sym_paged_gqa_decode_workspace_bytes(B, Hq, head_dim, max_context) exceeds 32 MiB return
+ * SYM_ERR_WORKSPACE (e.g. batch 32 x 16 heads fits up to 32 K tokens of max_context). The first
+ * call on a device locates that device's copy (a runtime query, no allocation). Every call on a
+ * GPU shares its copy: calls that overlap in time on one GPU (two streams, two host threads)
+ * race. Nothing in it needs clearing between calls.
+ */
+int sym_paged_gqa_decode_noalloc(const void* q, const void* k_pool, const void* v_pool,
+                                 const int32_t* block_tables, const int32_t* positions, int B,
+                                 int Hq, int Hkv, int head_dim, int block_size,
+                                 int max_blocks_per_seq, int num_blocks, int max_context,
+                                 float scale, void* out, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Fused attention decode step: sym_attn_decode_prologue followed by sym_paged_gqa_decode in
  * one split kernel (+ the merge kernel). Replaces the QK-norm, RoPE, paged_update_cache and
  * paged SDPA decode of TTNNBailingMoEAttention._forward_decode_paged

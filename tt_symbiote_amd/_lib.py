@@ -45,6 +45,11 @@ _SIGNATURES = {
         [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
          _c_float, _vp, _c_size, _vp, _vp],
     ),
+    "sym_paged_gqa_decode_noalloc": (
+        _c_int,
+        [_vp, _vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
+         _c_float, _vp, _vp],
+    ),
     "sym_attn_decode_step": (
         _c_int,
         [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float,

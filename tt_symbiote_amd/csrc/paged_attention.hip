@@ -19,6 +19,8 @@
 // tokens as the A operand, the V elements it loaded as B, with matching k orders). A merge
 // kernel combines the splits of each sequence with the log-sum-exp rule. Splits past a
 // sequence's length exit at once.
+#include <mutex>
+
 #include "common.h"
 
 namespace sym {
@@ -1316,6 +1318,65 @@ extern "C" int sym_paged_gqa_decode(const void* q, const void* k_pool, const voi
                        Hq, Hkv, head_dim,
                        block_size, max_blocks_per_seq, num_blocks, max_context, scale, workspace,
                        workspace_bytes, out, stream);
+}
+
+// ---------------------------------------------------------------------------------------------
+// Allocation-free decode. The per-split partial results live in this file-scope device array
+// instead of a caller workspace: one copy per GPU, held until the process ends. The host never
+// passes the array's name to a kernel (in host code it is only a stand-in for the symbol); each
+// device's copy is located once with hipGetSymbolAddress and that address is used. Nothing in it
+// needs initial contents: the split kernel writes every (sequence, head, split) entry that the
+// merge kernel reads, and a sequence with a single split never touches it.
+constexpr size_t kNoAllocScratchBytes = (size_t)32 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_addr[kMaxDevices] = {};
+}  // namespace
+
+// Address of the current device's scratch copy (located on the first call on that device).
+static int noalloc_scratch(const char* what, void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  SYM_REQUIRE(e == hipSuccess, SYM_ERR_LAUNCH, "%s: hipGetDevice: %s", what,
+              hipGetErrorString(e));
+  SYM_REQUIRE(dev >= 0 && dev < kMaxDevices, SYM_ERR_UNSUPPORTED, "%s: device %d", what, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    SYM_REQUIRE(e == hipSuccess && p, SYM_ERR_LAUNCH,
+                "%s: hipGetSymbolAddress(scratch) on device %d: %s", what, dev,
+                hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return SYM_OK;
+}
+
+extern "C" int sym_paged_gqa_decode_noalloc(const void* q, const void* k_pool,
+                                            const void* v_pool, const int32_t* block_tables,
+                                            const int32_t* positions, int B, int Hq, int Hkv,
+                                            int head_dim, int block_size,
+                                            int max_blocks_per_seq, int num_blocks,
+                                            int max_context, float scale, void* out,
+                                            void* stream) {
+  const char* what = "paged_gqa_decode_noalloc";
+  SYM_REQUIRE(B <= 0 || q, SYM_ERR_INVALID, "%s: null pointer argument", what);
+  const size_t need = sym_paged_gqa_decode_workspace_bytes(B, Hq, head_dim, max_context);
+  SYM_REQUIRE(need <= kNoAllocScratchBytes, SYM_ERR_WORKSPACE,
+              "%s: B=%d x Hq=%d x %d splits of the context need %zu bytes of scratch, above the "
+              "fixed %zu (use sym_paged_gqa_decode with a caller workspace)",
+              what, B, Hq, (max_context + kSplit - 1) / kSplit, need, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  int rc = noalloc_scratch(what, &ws);
+  if (rc) return rc;
+  return launch_decode(what, q, nullptr, const_cast<void*>(k_pool), const_cast<void*>(v_pool),
+                       nullptr, nullptr, block_tables, positions, B, Hq, Hkv, head_dim,
+                       block_size, max_blocks_per_seq, num_blocks, max_context, scale, ws,
+                       kNoAllocScratchBytes, out, stream);
 }
 
 extern "C" int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const void* k_norm_w,

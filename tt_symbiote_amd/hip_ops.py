@@ -544,6 +544,35 @@ def paged_gqa_decode(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
     return out
 
 
+def paged_gqa_decode_noalloc(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                             block_tables: torch.Tensor, positions: torch.Tensor, scale: float,
+                             out: torch.Tensor, max_context: Optional[int] = None) -> torch.Tensor:
+    """:func:`paged_gqa_decode` (bf16 pools) through the allocation-free entry point: the split
+    partials live in the library's fixed per-GPU scratch array, and ``out`` [B, Hq, D] bf16 is
+    the caller's, so the call allocates no device memory. Calls that overlap in time on one GPU
+    race on that array."""
+    _check(q, "q", torch.bfloat16)
+    if q.dim() != 3 or q.shape[2] != HEAD_DIM:
+        raise ValueError(f"q must be [B, Hq, {HEAD_DIM}], got {tuple(q.shape)}")
+    B, Hq, _ = q.shape
+    lay = _check_pools(k_pool, v_pool, block_tables, B)
+    _check(positions, "positions", torch.int32, q.device)
+    _check_shape(positions, "positions", (B,))
+    cap = lay.max_blocks_per_seq * lay.block_size
+    if max_context is None:
+        max_context = cap
+    if not 0 < max_context <= cap:
+        raise ValueError(f"max_context {max_context} outside (0, {cap}]")
+    _check(out, "out", torch.bfloat16, q.device)
+    _check_shape(out, "out", tuple(q.shape))
+    _timed("paged_gqa_decode", lambda: _lib.call(
+        "sym_paged_gqa_decode_noalloc", _ptr(q), _ptr(k_pool), _ptr(v_pool),
+        _ptr(block_tables), _ptr(positions), B, Hq, lay.num_kv_heads, HEAD_DIM, lay.block_size,
+        lay.max_blocks_per_seq, lay.num_blocks, int(max_context), float(scale), _ptr(out),
+        _stream()))
+    return out
+
+
 def paged_kv_fill_fp8(k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
                       max_seqlen: int, k_pool: torch.Tensor, v_pool: torch.Tensor,
                       k_scale: torch.Tensor, v_scale: torch.Tensor, block_tables: torch.Tensor,
