@@ -217,11 +217,12 @@ int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const void* k_no
  * (TTNNPagedAttentionKVCache, ttnn_attention.py:116-137); the layout and page-table semantics
  * are the same.
  * sym_paged_kv_fill_fp8: appends tokens cu_seqlens[s] + i (i < L_s) of n_seqs sequences at
- *   positions start_pos[s] + i (start_pos null: 0) through page-table row s
+ *   positions start_pos[s] + i (start_pos null: 0) through page-table row seq_rows[s]
+ *   (seq_rows null: row s) of a page table of page_table_rows rows
  *   (paged_fill_on_device / paged_update_on_device, ttnn_attention.py:202-269). The 128 bf16
  *   dims of token t, head g start at element t * tok_stride + g * head_stride of k / v
  *   ([T, Hkv, 128]: Hkv*128, 128; [Hkv, S, 128]: 128, S*128). A sequence whose start is
- *   negative is skipped. max_seqlen >= every L_s.
+ *   negative, or whose row lies outside the page table, is skipped. max_seqlen >= every L_s.
  * sym_paged_gqa_decode_fp8 / sym_attn_decode_step_fp8: sym_paged_gqa_decode /
  *   sym_attn_decode_step over the fp8 pools (paged_sdpa_decode, ttnn_attention.py:288-329);
  *   same workspace. The step appends the new token's k and v by the rule above before the
@@ -229,10 +230,11 @@ int sym_attn_decode_step(const void* qkv, const void* q_norm_w, const void* k_no
  */
 int sym_paged_kv_fill_fp8(const void* k, const void* v, long long tok_stride,
                           long long head_stride, const int32_t* cu_seqlens,
-                          const int32_t* start_pos, int n_seqs, int max_seqlen, int Hkv,
-                          int head_dim, void* k_pool, void* v_pool, float* k_scale,
-                          float* v_scale, const int32_t* block_tables, int max_blocks_per_seq,
-                          int block_size, int num_blocks, void* stream);
+                          const int32_t* start_pos, const int32_t* seq_rows, int n_seqs,
+                          int max_seqlen, int Hkv, int head_dim, void* k_pool, void* v_pool,
+                          float* k_scale, float* v_scale, const int32_t* block_tables,
+                          int page_table_rows, int max_blocks_per_seq, int block_size,
+                          int num_blocks, void* stream);
 int sym_paged_gqa_decode_fp8(const void* q, const void* k_pool, const void* v_pool,
                              const float* k_scale, const float* v_scale,
                              const int32_t* block_tables, const int32_t* positions, int B,

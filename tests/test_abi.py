@@ -148,11 +148,15 @@ def test_fp8_entry_points_reject_bad_shapes():
     dargs = lambda H, I: (FAKE, 4, H, I, FAKE, FAKE, FAKE, FAKE, 65, FAKE, FAKE, FAKE, None)
     assert _call("sym_moe_down_fp8", *dargs(2048, 192))[0] == 2
     # fp8 cache: the block size must divide 256; strides must be multiples of 8
-    fill = lambda bs, ts, hs: (FAKE, FAKE, ts, hs, FAKE, None, 2, 10, 4, 128, FAKE, FAKE, FAKE,
-                               FAKE, FAKE, 8, bs, 64, None)
+    fill = lambda bs, ts, hs, rows=2, seq_rows=None: (
+        FAKE, FAKE, ts, hs, FAKE, None, seq_rows, 2, 10, 4, 128, FAKE, FAKE, FAKE, FAKE, FAKE,
+        rows, 8, bs, 64, None)
     rc, msg = _call("sym_paged_kv_fill_fp8", *fill(48, 512, 128))
     assert rc == 2 and "block_size" in msg
     assert _call("sym_paged_kv_fill_fp8", *fill(32, 500, 128))[0] == 1
+    # two sequences need two page-table rows unless each names its own row
+    rc, msg = _call("sym_paged_kv_fill_fp8", *fill(32, 512, 128, rows=1))
+    assert rc == 1 and "rows" in msg
     rc, msg = _call("sym_paged_gqa_decode_fp8", FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 2, 16, 4,
                     128, 48, 8, 64, 300, 1.0, FAKE, 1 << 20, FAKE, None)
     assert rc == 2 and "block_size" in msg

@@ -2,15 +2,18 @@
 module-replacement API.
 
     import tt_symbiote_amd as ts
-    ts.apply_recipe(model)              # swap the HF trunk, decoder layers, attention, MoE, lm_head
+    model = ts.AutoModelForCausalLM.from_pretrained(path, trust_remote_code=True,
+                                                    kv_cache_kwargs={"max_num_blocks": 512})
+    # (or ts.apply_recipe(model) on an already-loaded HF model)
     ts.set_device(model, "cuda:0")      # bind to the GPU, move weights, allocate the paged cache
-    cache = model._tt_kv_cache          # pass back as past_key_values
+    out = model.generate(input_ids, max_new_tokens=64, past_key_values=model._tt_kv_cache)
 
 The compute runs in hand-written gfx950 HIP kernels behind a C ABI
 (``include/symbiote_mi355x.h``, ``lib/libsymbiote_mi355x.so``); importing this package does
 not touch the GPU or load the library.
 """
 from . import recipe_bailing_moe_v2  # noqa: F401  -- registers the recipe
+from .auto import AutoModelForCausalLM
 from .core.module import (HIPModule, StatefulHIPModule, StatefulTTNNModule, StatelessHIPModule,
                           StatelessTTNNModule, TTNNModule)
 from .modules import (HIPBailingMoE, HIPBailingMoEAttention, HIPBailingMoEDecoderLayer,
@@ -36,7 +39,7 @@ def apply_recipe(model, kv_cache_kwargs=None, exclude_replacement=None):
     return swapped
 
 
-__all__ = ["apply_recipe", "set_device", "register_modules", "register_recipe",
+__all__ = ["AutoModelForCausalLM", "apply_recipe", "set_device", "register_modules", "register_recipe",
            "TT_MODEL_REGISTRY", "compatibility", "HIPModule", "StatelessHIPModule",
            "StatefulHIPModule", "TTNNModule", "StatelessTTNNModule", "StatefulTTNNModule",
            "HIPBailingMoE", "HIPBailingMoEAttention", "HIPBailingMoEDecoderLayer",

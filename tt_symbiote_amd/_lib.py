@@ -58,8 +58,8 @@ _SIGNATURES = {
     ),
     "sym_paged_kv_fill_fp8": (
         _c_int,
-        [_vp, _vp, _c_ll, _c_ll, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp,
-         _vp, _c_int, _c_int, _c_int, _vp],
+        [_vp, _vp, _c_ll, _c_ll, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp,
+         _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp],
     ),
     "sym_paged_gqa_decode_fp8": (
         _c_int,

@@ -663,20 +663,22 @@ __device__ __forceinline__ uint2 byte_mask8(uint32_t m) {
 __global__ __launch_bounds__(256) void paged_kv_fill_fp8_kernel(
     const uint16_t* __restrict__ k, const uint16_t* __restrict__ v, long long tok_stride,
     long long head_stride, const int32_t* __restrict__ cu_seqlens,
-    const int32_t* __restrict__ start_pos, int Hkv, uint8_t* __restrict__ k_pool,
-    uint8_t* __restrict__ v_pool, float* __restrict__ k_scale, float* __restrict__ v_scale,
+    const int32_t* __restrict__ start_pos, const int32_t* __restrict__ seq_rows, int n_rows,
+    int Hkv, uint8_t* __restrict__ k_pool, uint8_t* __restrict__ v_pool,
+    float* __restrict__ k_scale, float* __restrict__ v_scale,
     const int32_t* __restrict__ block_tables, int mbps, int block_size, int num_blocks) {
   __shared__ float s_amax[2][4];
   const int j = blockIdx.x, g = blockIdx.y, sq = blockIdx.z;
   const int c0 = cu_seqlens[sq];
   const int L = cu_seqlens[sq + 1] - c0;
   const int start = start_pos ? start_pos[sq] : 0;
-  if (L <= 0 || start < 0) return;
+  const int row = seq_rows ? seq_rows[sq] : sq;  // page-table row of the sequence
+  if (L <= 0 || start < 0 || row < 0 || row >= n_rows) return;
   const int blk = start / block_size + j;
   const int p0 = max(start, blk * block_size);
   const int p1 = min(start + L, (blk + 1) * block_size);
   if (p0 >= p1 || blk >= mbps) return;
-  const int phys = block_tables[(size_t)sq * mbps + blk];
+  const int phys = block_tables[(size_t)row * mbps + blk];
   if (phys < 0 || phys >= num_blocks) return;
   const int n_old = p0 - blk * block_size;
   const int n_new = p1 - p0;
@@ -1456,9 +1458,10 @@ extern "C" int sym_attn_decode_step_fp8(const void* qkv, const void* q_norm_w,
 
 extern "C" int sym_paged_kv_fill_fp8(const void* k, const void* v, long long tok_stride,
                                      long long head_stride, const int32_t* cu_seqlens,
-                                     const int32_t* start_pos, int n_seqs, int max_seqlen,
-                                     int Hkv, int head_dim, void* k_pool, void* v_pool,
-                                     float* k_scale, float* v_scale, const int32_t* block_tables,
+                                     const int32_t* start_pos, const int32_t* seq_rows,
+                                     int n_seqs, int max_seqlen, int Hkv, int head_dim,
+                                     void* k_pool, void* v_pool, float* k_scale, float* v_scale,
+                                     const int32_t* block_tables, int page_table_rows,
                                      int max_blocks_per_seq, int block_size, int num_blocks,
                                      void* stream) {
   int rc = check_cache_args("paged_kv_fill_fp8", n_seqs, Hkv, head_dim, block_size,
@@ -1472,6 +1475,9 @@ extern "C" int sym_paged_kv_fill_fp8(const void* k, const void* v, long long tok
               "paged_kv_fill_fp8: block_size=%d must be a multiple of 8 dividing %d", block_size,
               kSplit);
   SYM_REQUIRE(n_seqs <= 65535 && Hkv <= 65535, SYM_ERR_INVALID, "paged_kv_fill_fp8: grid");
+  SYM_REQUIRE(page_table_rows >= 1 && (seq_rows || n_seqs <= page_table_rows), SYM_ERR_INVALID,
+              "paged_kv_fill_fp8: %d sequences for a page table of %d rows", n_seqs,
+              page_table_rows);
   SYM_REQUIRE(tok_stride > 0 && head_stride > 0 && tok_stride % 8 == 0 && head_stride % 8 == 0,
               SYM_ERR_INVALID, "paged_kv_fill_fp8: strides %lld, %lld must be positive multiples"
               " of 8", tok_stride, head_stride);
@@ -1479,8 +1485,8 @@ extern "C" int sym_paged_kv_fill_fp8(const void* k, const void* v, long long tok
   (void)hipGetLastError();
   hipLaunchKernelGGL(paged_kv_fill_fp8_kernel, dim3(gx, Hkv, n_seqs), dim3(256), 0,
                      (hipStream_t)stream, (const uint16_t*)k, (const uint16_t*)v, tok_stride,
-                     head_stride, cu_seqlens, start_pos, Hkv, (uint8_t*)k_pool, (uint8_t*)v_pool,
-                     k_scale, v_scale,
-                     block_tables, max_blocks_per_seq, block_size, num_blocks);
+                     head_stride, cu_seqlens, start_pos, seq_rows, page_table_rows, Hkv,
+                     (uint8_t*)k_pool, (uint8_t*)v_pool, k_scale, v_scale, block_tables,
+                     max_blocks_per_seq, block_size, num_blocks);
   return sym_host::check_launch("paged_kv_fill_fp8_kernel");
 }

@@ -17,6 +17,10 @@ without the host in the loop:
 
 Prompts of different lengths are supported (each sequence keeps its own position); there is no
 stopping criterion (exactly ``max_new_tokens`` per sequence, as the fixed-length benchmark).
+The cache's host counters (one per layer, batch-uniform as the reference's) follow sequence 0:
+they are advanced with ``update_seq_length`` after the prefill and after the decode steps,
+outside the captured graph, as the reference's model loop does (modeling_bailing_moe_v2.py
+:244-251).
 """
 from __future__ import annotations
 
@@ -93,10 +97,16 @@ class GreedyGenerator:
             rows = hip_ops.embedding(last, hn)                 # gather each prompt's last row
             self.ids[s:e].copy_(self.lm_head.greedy(rows))
             s = e
+        self._count(lens[0])
         lens_d = torch.tensor(lens, dtype=torch.int32, device=dev)
         self.hist_base.copy_(lens_d)
         self.positions.copy_(lens_d - 1)
         hip_ops.greedy_advance(self.ids, self.positions, self.history, self.hist_base)
+
+    def _count(self, n: int) -> None:
+        self.cache.set_external_seq_tracking(True)
+        for i in range(len(self.model.layers)):
+            self.cache.update_seq_length(i, n)
 
     # ---------------------------------------------------------------- decode
     def _step(self) -> None:
@@ -119,6 +129,7 @@ class GreedyGenerator:
                 self.graph.replay()
             else:
                 self._step()
+        self._count(n_steps)
 
 
 def greedy_generate(model: HIPBailingMoeV2Model, lm_head: HIPLMHead, prompts, cache,

@@ -67,7 +67,8 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
-def _check(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device = None) -> None:
+def _check(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device = None,
+           align: int = 16) -> None:
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name}: expected a torch.Tensor, got {type(t).__name__}")
     if t.device.type != "cuda":
@@ -78,9 +79,9 @@ def _check(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device 
         raise TypeError(f"{name}: dtype {t.dtype}, expected {dtype}")
     if not t.is_contiguous():
         raise ValueError(f"{name}: must be contiguous")
-    if t.data_ptr() % 16:
-        # the kernels use 16-byte vector loads
-        raise ValueError(f"{name}: data pointer must be 16-byte aligned")
+    if t.data_ptr() % align:
+        # the kernels use 16-byte vector loads (``align`` 4: an array read one int at a time)
+        raise ValueError(f"{name}: data pointer must be {align}-byte aligned")
 
 
 def _check_shape(t: torch.Tensor, name: str, shape: tuple) -> None:
@@ -576,11 +577,13 @@ def paged_gqa_decode_noalloc(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torc
 def paged_kv_fill_fp8(k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
                       max_seqlen: int, k_pool: torch.Tensor, v_pool: torch.Tensor,
                       k_scale: torch.Tensor, v_scale: torch.Tensor, block_tables: torch.Tensor,
-                      start_pos: Optional[torch.Tensor] = None, layout: str = "thd") -> None:
+                      start_pos: Optional[torch.Tensor] = None, layout: str = "thd",
+                      seq_rows: Optional[torch.Tensor] = None) -> None:
     """Append tokens to an fp8 KV cache (per-(block, head) power-of-two scales, requantising a
     block's earlier tokens when its scale grows). Sequence s = tokens cu_seqlens[s] ..
     cu_seqlens[s+1]-1 at positions start_pos[s] + i (0 when start_pos is None) in page-table row
-    s. ``layout``: "thd" for k, v [T, Hkv, D]; "htd" for k, v [Hkv, T, D]."""
+    seq_rows[s] (s when seq_rows is None). ``layout``: "thd" for k, v [T, Hkv, D]; "htd" for
+    k, v [Hkv, T, D]."""
     _check(k, "k", torch.bfloat16)
     _check(v, "v", torch.bfloat16, k.device)
     _check_shape(v, "v", tuple(k.shape))
@@ -588,7 +591,8 @@ def paged_kv_fill_fp8(k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor
     n = cu_seqlens.numel() - 1
     if n < 0 or cu_seqlens.dim() != 1:
         raise ValueError("cu_seqlens must be [n_seqs + 1]")
-    lay = _check_pools(k_pool, v_pool, block_tables, n, k_scale, v_scale)
+    lay = _check_pools(k_pool, v_pool, block_tables, 1 if seq_rows is not None else n,
+                       k_scale, v_scale)
     if k_pool.dtype != torch.float8_e4m3fn:
         raise TypeError("paged_kv_fill_fp8 needs float8_e4m3fn pools")
     if k.dim() != 3 or k.shape[2] != HEAD_DIM:
@@ -603,13 +607,15 @@ def paged_kv_fill_fp8(k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor
         raise ValueError(f"layout {layout!r}")
     if hkv != lay.num_kv_heads:
         raise ValueError(f"k has {hkv} kv heads, the pool {lay.num_kv_heads}")
-    if start_pos is not None:
-        _check(start_pos, "start_pos", torch.int32, k.device)
-        _check_shape(start_pos, "start_pos", (n,))
+    for t, name in ((start_pos, "start_pos"), (seq_rows, "seq_rows")):
+        if t is not None:
+            _check(t, name, torch.int32, k.device, align=4)
+            _check_shape(t, name, (n,))
     _lib.call("sym_paged_kv_fill_fp8", _ptr(k), _ptr(v), strides[0], strides[1],
-              _ptr(cu_seqlens), _ptr(start_pos), n, int(max_seqlen), lay.num_kv_heads, HEAD_DIM,
-              _ptr(k_pool), _ptr(v_pool), _ptr(k_scale), _ptr(v_scale), _ptr(block_tables),
-              lay.max_blocks_per_seq, lay.block_size, lay.num_blocks, _stream())
+              _ptr(cu_seqlens), _ptr(start_pos), _ptr(seq_rows), n, int(max_seqlen),
+              lay.num_kv_heads, HEAD_DIM, _ptr(k_pool), _ptr(v_pool), _ptr(k_scale),
+              _ptr(v_scale), _ptr(block_tables), block_tables.shape[0], lay.max_blocks_per_seq,
+              lay.block_size, lay.num_blocks, _stream())
 
 
 # -------------------------------------------------------------------------------------------

@@ -8,13 +8,25 @@ same HF fields (ttnn_attention.py:1954-2042): ``config.num_attention_heads`` /
 ``query_layernorm`` / ``key_layernorm``, ``layer_idx``. The Q/K rows keep HF's split-half RoPE
 layout (no Meta-interleave permutation: that layout exists for TT's rotary kernel).
 
-Decode step (``seq_len == 1`` with a paged cache; ttnn_attention.py:2308-2466):
+``forward`` routes by sequence length, as the reference (ttnn_attention.py:2480-2517):
+
+Decode step (``seq_len == 1``; ttnn_attention.py:2308-2466):
   qkv  = x W_qkv^T (+b)                          skinny-GEMM kernel
   o    = fused decode step (split-K + merge)     QK RMSNorm, partial RoPE, paged KV write and
                                                   paged GQA decode in one pass
   out  = o W_dense^T (+b)                         skinny-GEMM kernel
 Positions are per-sequence device int32 (``cache_position`` / ``position_ids`` per row); when
-absent, the cache's host counter is used for every row, as in the reference.
+absent, the cache's host counter is used for every row, as in the reference
+(ttnn_attention.py:2285-2287).
+
+Prefill (``seq_len > 1``; ttnn_attention.py:2153-2230): batch row b is a prompt at positions
+0 .. S-1 written into page-table row b (the reference fills batch row 0 only, 2205-2210); tiled
+QKV GEMM, prefill prologue (QK-norm, RoPE, paged KV write of every token), causal varlen flash
+attention, tiled dense GEMM.
+
+The cache's host counters advance with each write (decode by 1, prefill by S) unless the caller
+tracks them itself (``update_seq_length``), as the reference's paged_update_on_device /
+paged_fill_on_device do (ttnn_attention.py:224-233, 259-269).
 """
 from __future__ import annotations
 
@@ -191,6 +203,7 @@ class HIPBailingMoEAttention(StatefulHIPModule):
             q_norm_w=d["q_norm"], k_norm_w=d["k_norm"], eps=self.norm_eps,
             max_context=cache.max_context, workspace=cache.decode_workspace(B, self.num_heads),
             k_scale=cache.key_scale(self.layer_idx), v_scale=cache.value_scale(self.layer_idx))
+        cache.advance(self.layer_idx, 1)
         return o.view(B, self.num_heads * self.head_dim)
 
     def dense_residual(self, o: torch.Tensor, residual: torch.Tensor):
@@ -203,11 +216,13 @@ class HIPBailingMoEAttention(StatefulHIPModule):
                        positions: torch.Tensor, seq_ids: torch.Tensor,
                        cache: HIPPagedAttentionKVCache) -> torch.Tensor:
         """Prefill of packed sequences: x [T, H] (bf16, already normalised by the layer), token
-        t of sequence seq_ids[t] at positions[t] (0 .. L-1). Writes the sequences' K/V into the
-        paged cache (page-table row = sequence) and returns the attention output after the
-        dense projection, [T, H] bf16. With an fp8 cache the sequences start at position 0 and
-        sequence s uses page-table row s (the K/V are appended per block after the prologue)."""
+        t of sequence seq_ids[t] at positions[t] (0 .. L-1; page-table row seq_ids[t]). Writes
+        the sequences' K/V into the paged cache and returns the attention output after the
+        dense projection, [T, H] bf16. The host counters are not advanced here (the forward
+        methods do). With an fp8 cache the K/V are appended per block after the prologue, at
+        the page-table row and start position of each sequence's first token."""
         d = self._dev
+        T = x.shape[0]
         qkv = hip_ops.gemm(x, d["qkv_w"], d["qkv_b"])
         q, k, v = hip_ops.attn_prefill_prologue(
             qkv, positions, seq_ids, cache.key_cache(self.layer_idx),
@@ -215,27 +230,70 @@ class HIPBailingMoEAttention(StatefulHIPModule):
             num_heads=self.num_heads, num_kv_heads=self.num_kv_heads,
             rotary_dim=self.rotary_dim, rope_cs=d["rope"], q_norm_w=d["q_norm"],
             k_norm_w=d["k_norm"], eps=self.norm_eps)
-        if cache.is_fp8:
+        if cache.is_fp8 and T > 0:
+            first = cu_seqlens[:-1].long().clamp(max=T - 1)
             hip_ops.paged_kv_fill_fp8(
                 k, v, cu_seqlens, max_seqlen, cache.key_cache(self.layer_idx),
                 cache.value_cache(self.layer_idx), cache.key_scale(self.layer_idx),
-                cache.value_scale(self.layer_idx), cache.page_table_device)
+                cache.value_scale(self.layer_idx), cache.page_table_device,
+                start_pos=positions[first].contiguous(), seq_rows=seq_ids[first].contiguous())
         o = hip_ops.prefill_attention(q, k, v, cu_seqlens, max_seqlen, self.scaling)
         return hip_ops.gemm(o.view(-1, self.num_heads * self.head_dim), d["dense_w"],
                             d["dense_b"])
+
+    def prefill_rows(self, x: torch.Tensor, cache: HIPPagedAttentionKVCache,
+                     cache_position=None, position_ids=None) -> torch.Tensor:
+        """Prefill of B equal-length prompts x [B, S, H] (bf16): row b at positions 0 .. S-1 of
+        page-table row b. Returns [B, S, H] bf16 and advances the counters by S."""
+        B, S, H = x.shape
+        if B > cache.page_table.shape[0]:
+            raise ValueError(f"{B} prompts for a page table of {cache.page_table.shape[0]} rows")
+        pos = cache_position if cache_position is not None else position_ids
+        if isinstance(pos, torch.Tensor) and pos.device.type == "cpu" and pos.numel():
+            if int(pos.reshape(-1)[0]) != 0:
+                raise NotImplementedError(
+                    "prefill starting at a cached position (a prompt continuing earlier tokens); "
+                    "as the reference's prefill, prompts start at position 0")
+        positions, seq_ids, cu = equal_length_packing(B, S, x.device)
+        out = self.prefill_varlen(x.reshape(B * S, H).contiguous(), cu, S, positions, seq_ids,
+                                  cache)
+        cache.advance(self.layer_idx, S)
+        return out.view(B, S, H)
 
     def forward(self, hidden_states: torch.Tensor, position_embeddings=None,
                 attention_mask=None, past_key_values=None, past_key_value=None,
                 cache_position=None, position_ids=None, **kwargs):
         cache = self._cache_of(past_key_values, past_key_value)
         B, S, H = hidden_states.shape
-        if S != 1:
-            raise NotImplementedError("prefill (seq_len > 1) is not implemented on the HIP path")
-        d = self._dev
-        x = hidden_states.reshape(B, H)
+        x = hidden_states
         if x.dtype != torch.bfloat16:
             x = x.to(torch.bfloat16)
-        qkv = self.qkv_projection(x.contiguous())
+        if S != 1:
+            return self.prefill_rows(x, cache, cache_position, position_ids), None, cache
+        d = self._dev
+        qkv = self.qkv_projection(x.reshape(B, H).contiguous())
         o = self.decode_from_qkv(qkv, cache, cache_position, position_ids)
         out = hip_ops.linear(o, d["dense_w"], d["dense_b"])
         return out.view(B, 1, H), None, cache
+
+
+def equal_length_packing(B: int, S: int, device):
+    """(positions [B*S], seq_ids [B*S], cu_seqlens [B+1]) int32 on ``device`` for B prompts of S
+    tokens packed row after row (prompt b = page-table row b, positions 0 .. S-1), built on the
+    device without a host round trip."""
+    i32 = dict(dtype=torch.int32, device=device)
+    positions = torch.arange(S, **i32).repeat(B)
+    seq_ids = torch.arange(B, **i32).repeat_interleave(S)
+    cu = torch.arange(0, B * S + 1, S, **i32)
+    return positions, seq_ids, cu
+
+
+def varlen_packing(cu_seqlens: torch.Tensor, T: int):
+    """(positions [T], seq_ids [T]) int32 of packed sequences (sequence s = rows cu_seqlens[s]
+    .. cu_seqlens[s+1]-1 at positions 0 .. L-1, page-table row s), on cu_seqlens' device
+    without a host round trip."""
+    cu = cu_seqlens.to(torch.int32).contiguous()
+    t = torch.arange(T, dtype=torch.int32, device=cu.device)
+    seq_ids = torch.searchsorted(cu[1:].contiguous(), t, right=True).to(torch.int32)
+    positions = (t - cu[seq_ids.long()]).to(torch.int32)
+    return positions.contiguous(), seq_ids.contiguous()

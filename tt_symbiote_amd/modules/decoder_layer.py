@@ -18,7 +18,7 @@ import torch
 
 from .. import hip_ops
 from ..core.module import StatefulHIPModule
-from .attention import HIPBailingMoEAttention
+from .attention import HIPBailingMoEAttention, equal_length_packing, varlen_packing
 from .moe import HIPBailingMoE, HIPBailingMoeV2MLP
 
 
@@ -83,15 +83,14 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
                        cache, positions: torch.Tensor = None,
                        seq_ids: torch.Tensor = None) -> torch.Tensor:
         """Prefill of packed sequences x [T, H] (bf16), sequence s = rows cu_seqlens[s] ..
-        cu_seqlens[s+1]-1 at positions 0 .. L-1 (page-table row s of the cache). Returns the
-        layer output [T, H] (bf16); the sequences' K/V are written into the paged cache."""
+        cu_seqlens[s+1]-1 at positions 0 .. L-1 (page-table row s of the cache, unless
+        ``positions`` / ``seq_ids`` say otherwise per token). Returns the layer output [T, H]
+        (bf16); the sequences' K/V are written into the paged cache. The host counters are not
+        advanced here (:meth:`forward` does)."""
         x = x.to(torch.bfloat16).contiguous()
         T, H = x.shape
         if positions is None or seq_ids is None:
-            cu = cu_seqlens.cpu().long()
-            lens = (cu[1:] - cu[:-1]).tolist()
-            positions = torch.cat([torch.arange(L) for L in lens]).to(torch.int32)
-            seq_ids = torch.cat([torch.full((L,), s) for s, L in enumerate(lens)]).to(torch.int32)
+            positions, seq_ids = varlen_packing(cu_seqlens.to(x.device), T)
         positions = positions.to(device=x.device, dtype=torch.int32).contiguous()
         seq_ids = seq_ids.to(device=x.device, dtype=torch.int32).contiguous()
         xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
@@ -119,9 +118,12 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
         x = x.contiguous()
         B, S, H = x.shape
         if S != 1:
-            # equal-length prompts, positions 0 .. S-1 of sequences 0 .. B-1
-            cu = torch.arange(0, B * S + 1, S, dtype=torch.int32, device=x.device)
-            out = self.prefill_varlen(x.view(B * S, H), cu, S, attn._cache_of(cache, None))
+            # equal-length prompts, positions 0 .. S-1 of page-table rows 0 .. B-1
+            kv = attn._cache_of(cache, None)
+            positions, seq_ids, cu = equal_length_packing(B, S, x.device)
+            out = self.prefill_varlen(x.view(B * S, H), cu, S, kv, positions=positions,
+                                      seq_ids=seq_ids)
+            kv.advance(attn.layer_idx, S)
             outputs = (out.view(B, S, H),)
             if output_attentions:
                 outputs += (None,)

@@ -179,6 +179,19 @@ class HIPPagedAttentionKVCache(_CacheBase):
             if layer_idx == 0:
                 self._seen_tokens += n
 
+    def advance(self, layer_idx: int, n: int) -> None:
+        """Advance layer ``layer_idx``'s counter by ``n`` tokens after a fill or an update,
+        unless the caller tracks the counters itself (:meth:`update_seq_length`); the paged
+        ops of the attention module call this, as the reference's paged_fill_on_device /
+        paged_update_on_device do (ttnn_attention.py:224-233, 259-269)."""
+        self._advance(layer_idx, n)
+
+    def set_external_seq_tracking(self, enabled: bool = True) -> None:
+        """Hand the counters to the caller (a model loop that calls :meth:`update_seq_length`
+        after each layer, outside any captured region) before its first layer runs, so that no
+        layer's own fill is counted as well."""
+        self._external_seq_tracking = bool(enabled)
+
     def update_seq_length(self, layer_idx: int, seq_len: int = 1) -> None:
         """Advance the host counters (call from the model loop); switches to external tracking."""
         self._external_seq_tracking = True
@@ -230,10 +243,11 @@ class HIPPagedAttentionKVCache(_CacheBase):
             v = v.to(torch.bfloat16).contiguous()
             S = k.shape[1]
             cu = torch.tensor([0, S], dtype=torch.int32, device=self._device)
+            rows = self._cu_arange(self.page_table.shape[0])[batch_idx:batch_idx + 1]
             hip_ops.paged_kv_fill_fp8(
                 k, v, cu, S, self._key_cache[layer_idx], self._value_cache[layer_idx],
-                self._key_scale[layer_idx], self._value_scale[layer_idx],
-                self._page_table_dev[batch_idx:batch_idx + 1], layout="htd")
+                self._key_scale[layer_idx], self._value_scale[layer_idx], self._page_table_dev,
+                layout="htd", seq_rows=rows)
             self._advance(layer_idx, S)
             return
         k = k.to(self.dtype).contiguous()

@@ -8,9 +8,16 @@ HF ``generate`` then reads the logits back and takes the argmax on the host; her
 
 ``HIPBailingMoeV2Model.forward(input_ids, cache_position=..., past_key_values=cache)``:
   * seq_len 1 (decode): embedding gather -> each layer's fused decode step -> final RMSNorm;
+    without ``cache_position`` / ``position_ids`` the tokens go at the cache's counter
+    (``get_seq_length()``), as the reference builds its positions (modeling_bailing_moe_v2.py
+    :154-158);
   * seq_len > 1: the batch rows are equal-length prompts at positions 0 .. S-1 (page-table row
     = batch row), run as packed varlen prefill through every layer.
-Returns the final-normed hidden states [B, S, H] (bf16), as the HF model's last hidden state.
+As the reference's layer loop (modeling_bailing_moe_v2.py:244-251), the cache's host counters
+are advanced by the model after each layer (``update_seq_length``: the cache switches to
+external tracking before the first layer, so no layer is counted twice). Returns the
+final-normed hidden states [B, S, H] (bf16) as ``last_hidden_state`` of a ``ModelOutput`` (a
+tuple with ``return_dict=False``), as the HF model does.
 """
 from __future__ import annotations
 
@@ -20,7 +27,18 @@ import torch
 
 from .. import hip_ops
 from ..core.module import StatefulHIPModule, StatelessHIPModule
+from .attention import equal_length_packing
 from .decoder_layer import HIPBailingMoEDecoderLayer
+
+
+def _model_output(hidden: torch.Tensor, cache):
+    """HF's BaseModelOutputWithPast (last_hidden_state, past_key_values), or a tuple when
+    transformers is absent."""
+    try:
+        from transformers.modeling_outputs import BaseModelOutputWithPast
+    except Exception:  # pragma: no cover - transformers is optional for the kernels
+        return (hidden, cache)
+    return BaseModelOutputWithPast(last_hidden_state=hidden, past_key_values=cache)
 
 
 def _embedding_module(torch_model):
@@ -113,28 +131,52 @@ class HIPBailingMoeV2Model(StatefulHIPModule):
 
     # ------------------------------------------------------------------ HF-shaped forward
     def forward(self, input_ids=None, attention_mask=None, position_ids=None,
-                past_key_values=None, inputs_embeds=None, cache_position=None, **kwargs):
+                past_key_values=None, inputs_embeds=None, cache_position=None,
+                return_dict=None, **kwargs):
         if inputs_embeds is not None:
             raise NotImplementedError("inputs_embeds: pass input_ids")
         cache = past_key_values if past_key_values is not None else kwargs.get("past_key_value")
+        if cache is None:
+            raise NotImplementedError("HIPBailingMoeV2Model needs the paged KV cache "
+                                      "(model._tt_kv_cache) as past_key_values")
         ids = torch.as_tensor(input_ids)
         if ids.dim() == 1:
             ids = ids.view(1, -1)
         B, S = ids.shape
         dev = self.device
         ids = ids.to(device=dev, dtype=torch.int32).contiguous()
+        cache.set_external_seq_tracking(True)
         if S == 1:
             pos = cache_position if cache_position is not None else position_ids
             if pos is None:
-                raise ValueError("decode needs cache_position (or position_ids)")
+                pos = torch.tensor([cache.get_seq_length(0)])
             pos = torch.as_tensor(pos).reshape(-1)
-            if pos.numel() == 1 and B > 1:
-                pos = pos.expand(B)
+            if pos.numel() != B:
+                pos = pos.expand(B) if pos.numel() == 1 else pos.reshape(B, -1)[:, -1]
             pos = pos.to(device=dev, dtype=torch.int32).contiguous()
-            return self.decode_hidden(ids.view(B), pos, cache).view(B, 1, self.hidden_size)
-        cu = torch.arange(0, B * S + 1, S, dtype=torch.int32, device=dev)
-        out = self.prefill_hidden(ids.view(B * S), cu, S, cache)
-        return out.view(B, S, self.hidden_size)
+            h = self.embed(ids.view(B)).view(B, 1, self.hidden_size)
+            for i, layer in enumerate(self.layers):
+                h = layer(h, past_key_values=cache, cache_position=pos)[0]
+                cache.update_seq_length(i, 1)
+            h = self.final_norm(h.view(B, self.hidden_size)).view(B, 1, self.hidden_size)
+        else:
+            pos = cache_position if cache_position is not None else position_ids
+            if isinstance(pos, torch.Tensor) and pos.device.type == "cpu" and pos.numel():
+                if int(pos.reshape(-1)[0]) != 0:
+                    raise NotImplementedError("prefill starting at a cached position; prompts "
+                                              "start at position 0 (as the reference's prefill)")
+            if B > cache.page_table.shape[0]:
+                raise ValueError(f"{B} prompts for a page table of {cache.page_table.shape[0]} "
+                                 "rows")
+            positions, seq_ids, cu = equal_length_packing(B, S, dev)
+            h = self.embed(ids.view(B * S))
+            for i, layer in enumerate(self.layers):
+                h = layer.prefill_varlen(h, cu, S, cache, positions=positions, seq_ids=seq_ids)
+                cache.update_seq_length(i, S)
+            h = self.final_norm(h).view(B, S, self.hidden_size)
+        if return_dict is False:
+            return (h, cache)
+        return _model_output(h, cache)
 
 
 class HIPLMHead(StatelessHIPModule):
@@ -170,6 +212,14 @@ class HIPLMHead(StatelessHIPModule):
     def move_weights_to_device_impl(self):
         self._dev = {k: v.to(self.device) for k, v in self._host.items()}
         self._host = {}
+        # the projection kernels take multiples of 16 output rows: the last vocab % 16 rows get
+        # a zero-padded 16-row copy for the logits path
+        V, H = self._dev["w"].shape
+        tail = V % 16
+        if tail:
+            pad = torch.zeros(16, H, dtype=torch.bfloat16, device=self.device)
+            pad[:tail].copy_(self._dev["w"][V - tail:])
+            self._dev["w_tail"] = pad
         return super().move_weights_to_device_impl()
 
     @property
@@ -192,8 +242,13 @@ class HIPLMHead(StatelessHIPModule):
         """Logits (fp32) [..., V] for HF-style callers."""
         shape = x.shape
         x2 = x.reshape(-1, self.hidden_size).to(torch.bfloat16).contiguous()
-        if x2.shape[0] <= 64:
-            out = hip_ops.linear(x2, self._dev["w"], None, out_dtype=torch.float32)
-        else:
-            out = hip_ops.gemm(x2, self._dev["w"], None, out_dtype=torch.float32)
-        return out.view(*shape[:-1], self.vocab_size)
+        op = hip_ops.linear if x2.shape[0] <= 64 else hip_ops.gemm
+        V = self.vocab_size
+        tail = V % 16
+        parts = []
+        if V - tail:
+            parts.append(op(x2, self._dev["w"][:V - tail], None, out_dtype=torch.float32))
+        if tail:
+            parts.append(op(x2, self._dev["w_tail"], None, out_dtype=torch.float32)[:, :tail])
+        out = parts[0] if len(parts) == 1 else torch.cat(parts, dim=1)
+        return out.view(*shape[:-1], V)

@@ -68,6 +68,11 @@ class BailingMoEV2Recipe:
         return None
 
     def make_kv_cache(self, model, device, batch_size: int = 1, **kwargs):
+        """The paged cache (reference: modeling_bailing_moe_v2.py:724-736). ``dtype``
+        (``torch.bfloat16`` by default, or ``torch.float8_e4m3fn`` for the fp8 cache) is this
+        build's addition."""
+        import torch
+
         config = PagedAttentionConfig(
             block_size=kwargs.get("block_size", 64),
             max_num_blocks=kwargs.get("max_num_blocks", 32),
@@ -76,4 +81,5 @@ class BailingMoEV2Recipe:
         head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
         return HIPPagedAttentionKVCache(
             num_layers=cfg.num_hidden_layers, num_kv_heads=cfg.num_key_value_heads,
-            head_dim=head_dim, config=config, device=None).to_device(device)
+            head_dim=head_dim, config=config, device=None,
+            dtype=kwargs.get("dtype", torch.bfloat16)).to_device(device)
