@@ -106,39 +106,82 @@ def algorithmic_bytes(shape, ctx, n_routed_active: int, B: int) -> dict:
                 experts=(n_routed_active + shape.num_shared_experts) * expert)
 
 
-def cpu_baseline(w_gpu, shape, ctx, x, steps: int) -> dict:
-    """The oracle (HF-shaped CPU module forward, fp32) on the same layer and batch."""
+def _cpu_model() -> str:
+    """The host CPU's model name (lscpu's "Model name", read from /proc/cpuinfo)."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _time_oracle_layer(layer, k_pool, v_pool, page_table, positions, x, steps: int, label: str):
+    """Median seconds of `steps` decode steps (after 2 warm-up steps) of the oracle layer."""
+    import torch
+
+    from oracle.paged_kv import PagedKVCacheRef
+
+    times = []
+    with torch.no_grad():
+        for i in range(steps + 2):
+            cache = PagedKVCacheRef([k_pool], [v_pool], page_table)
+            t0 = time.perf_counter()
+            layer(x, past_key_value=cache, cache_position=positions)
+            dt = time.perf_counter() - t0
+            if i >= 2:
+                times.append(dt)
+            _log(f"cpu baseline {label} step {i}: {dt * 1e3:.1f} ms")
+    return statistics.median(times)
+
+
+def cpu_baseline(w_gpu, shape, ctx, x, steps: int, legs=True) -> dict:
+    """The oracle (HF-shaped CPU module forward) on the host's cores: the reported leg is the
+    same layer and batch as the GPU run in fp32; with ``legs`` the bf16 module and the
+    single-sequence workload (one sequence of 512 cached tokens, 16 + 1 blocks of 32 placed by
+    a random permutation of a 64-block pool) are timed too, fp32 and bf16."""
     import torch
 
     from oracle.bailing_moe_v2 import decoder_layer_from_weights
-    from oracle.paged_kv import PagedKVCacheRef
+    from tt_symbiote_amd.workloads import decode_layer_config, paged_context
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
     w = {k: v.cpu() for k, v in w_gpu.items()}
-    layer = decoder_layer_from_weights(w, shape, dtype=torch.float32)
-    del w
-    kp = ctx.k_pool.float().cpu()
-    vp = ctx.v_pool.float().cpu()
-    pt = ctx.page_table.cpu()
-    pos = ctx.positions.cpu().long()
-    xc = x.float().cpu()
-    times = []
-    with torch.no_grad():
-        for i in range(steps + 2):
-            cache = PagedKVCacheRef([kp], [vp], pt)
-            t0 = time.perf_counter()
-            layer(xc, past_key_value=cache, cache_position=pos)
-            dt = time.perf_counter() - t0
-            if i >= 2:
-                times.append(dt)
-            _log(f"cpu baseline step {i}: {dt * 1e3:.1f} ms")
-    med = statistics.median(times)
     B = x.shape[0]
-    return {"value": B / med, "unit": "tokens/s", "cores": torch.get_num_threads(),
-            "kind": "port",
-            "sample": f"{steps} decode steps (median, after 2 warm-up) of the same layer and "
-                      f"batch of {B} in fp32 on the host CPU; {med * 1e3:.1f} ms/step"}
+    single = decode_layer_config("single")
+    one = paged_context(1, single["ctx_lo"], single["ctx_hi"], block_size=single["block_size"],
+                        num_kv_heads=shape.num_kv_heads, pool_blocks=single["pool_blocks"],
+                        seed=11)
+    x1 = torch.randn(1, 1, shape.hidden_size, generator=torch.Generator().manual_seed(12))
+    cases = [("batch", ctx, x.cpu())]
+    if legs:
+        cases.append(("single", one, x1))
+    results = []
+    for dtype in ((torch.float32, torch.bfloat16) if legs else (torch.float32,)):
+        layer = decoder_layer_from_weights(w, shape, dtype=dtype)
+        for name, c, xc in cases:
+            n = xc.shape[0]
+            label = f"{name}/{str(dtype).split('.')[-1]}"
+            med = _time_oracle_layer(layer, c.k_pool.to(dtype).cpu(), c.v_pool.to(dtype).cpu(),
+                                     c.page_table.cpu(), c.positions.cpu().long(),
+                                     xc.to(dtype), steps, label)
+            results.append({"workload": f"batch {n}, {int(c.context_lens.sum())} cached tokens",
+                            "dtype": str(dtype).split(".")[-1],
+                            "ms_per_step": med * 1e3, "tokens_per_s": n / med})
+        del layer
+    del w
+    head = results[0]
+    out = {"value": head["tokens_per_s"], "unit": "tokens/s", "cores": torch.get_num_threads(),
+           "kind": "port",
+           "sample": f"{steps} decode steps (median, after 2 warm-up) of the same layer and "
+                     f"batch of {B} in fp32 on the host CPU; {head['ms_per_step']:.1f} ms/step",
+           "os_cpu_count": os.cpu_count(), "cpu_model": _cpu_model()}
+    if legs:
+        out["legs"] = results
+    return out
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
@@ -616,7 +659,7 @@ def cpu_baseline_fp8(layer, w_gpu, shape, ctx, cache, x, steps: int) -> dict:
                                 v_pool=pool(hip_ops.fp8_v_rows(cache.value_cache(0)),
                                             cache.value_scale(0)),
                                 page_table=ctx.page_table[:n], positions=ctx.positions[:n])
-    r = cpu_baseline(w, shape, sub, x[:n], steps)
+    r = cpu_baseline(w, shape, sub, x[:n], steps, legs=False)
     r["sample"] = (f"{steps} decode steps (median, after 2 warm-up) of the same layer on the "
                    f"dequantised fp8 weights and cache, first {n} of the {x.shape[0]} sequences, "
                    f"fp32 on the host CPU; " + r["sample"].split("; ")[-1])
