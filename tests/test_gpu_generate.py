@@ -6,9 +6,12 @@
     apply_recipe + set_device and generated greedily for ragged prompts:
       - the HIP-graph decode loop gives exactly the eager loop's tokens;
       - teacher-forced against the oracle (the original HF-shaped modules, fp32 on the CPU) run
-        with the GPU's expert choices: every generated token is the oracle's argmax, except
-        where the oracle's top-2 logit margin is below 2e-2 (a near tie that bf16 activations
-        may flip); the oracle's own routing differs from the GPU's only at router near-ties.
+        with the GPU's expert choices, for the eager and the captured loop: every generated
+        token is the oracle's argmax, except where the oracle's top-2 logit margin is below
+        2e-2 (a near tie that bf16 activations may flip); the oracle's own routing differs from
+        the GPU's only at router near-ties;
+      - free-running: 128 tokens of the captured loop against the oracle's own greedy
+        continuation; the first step where they part must be a logit or router near tie.
 """
 import copy
 
@@ -19,6 +22,7 @@ import torch
 import tt_symbiote_amd as ts
 from oracle.bailing_moe_v2 import BailingMoeV2Config, BailingMoeV2ForCausalLM, init_weights_
 from tt_symbiote_amd import hip_ops
+from oracle.paged_kv import PagedKVCacheRef
 from oracle.route import route_torch, selection_margins
 from tt_symbiote_amd.generate import GreedyGenerator, greedy_generate, model_parts
 
@@ -109,7 +113,37 @@ def test_greedy_generate_graph_equals_eager(device):
     assert torch.equal(out[0], out[1])
 
 
-def test_greedy_generate_matches_oracle(device):
+def _record_routes(gen, trunk, moe, n_new):
+    """Run the decode steps of ``gen`` one at a time and return, per MoE layer, the GPU's
+    expert choice of the prefill (first entry) and of each decode step. With the captured
+    loop, the step that runs eagerly before the capture is recorded by a wrapper of the step
+    (not during the capture itself), and each replay is recorded after it ran: the kept route
+    tensors are the graph's own buffers, which every replay rewrites."""
+    routes = {i: [trunk.layers[i].mlp.last_route.topk_idx.cpu().long()] for i in moe}
+
+    def record():
+        for i in moe:
+            routes[i].append(trunk.layers[i].mlp.last_route.topk_idx.cpu().long())
+
+    eager_step = gen._step
+
+    def step():
+        eager_step()
+        if not torch.cuda.is_current_stream_capturing():
+            record()
+
+    gen._step = step
+    for _ in range(n_new - 1):
+        graph_before = gen.graph is not None
+        gen.decode(1)
+        if graph_before:
+            record()
+    assert all(len(r) == n_new for r in routes.values())
+    return routes
+
+
+@pytest.mark.parametrize("use_graph", [False, True], ids=["eager", "graph"])
+def test_greedy_generate_matches_oracle(device, use_graph):
     """Teacher-forced comparison with the GPU's expert choices replayed in the oracle: a
     near-tie in a router (bf16 activations on the GPU, fp32 in the oracle) legitimately picks a
     different expert and then changes the logits by far more than rounding, so the oracle runs
@@ -126,13 +160,10 @@ def test_greedy_generate_matches_oracle(device):
     moe = [i for i, layer in enumerate(trunk.layers) if not layer.is_dense_layer]
     for i in moe:
         trunk.layers[i].mlp.keep_last_route = True
-    gen = GreedyGenerator(trunk, head, hip._tt_kv_cache, 4, n_new, use_graph=False)
+    gen = GreedyGenerator(trunk, head, hip._tt_kv_cache, 4, n_new, use_graph=use_graph)
     gen.prefill(prompts)
-    routes = {i: [trunk.layers[i].mlp.last_route.topk_idx.cpu().long()] for i in moe}
-    for _ in range(n_new - 1):
-        gen.decode(1)
-        for i in moe:
-            routes[i].append(trunk.layers[i].mlp.last_route.topk_idx.cpu().long())
+    routes = _record_routes(gen, trunk, moe, n_new)
+    assert (gen.graph is not None) == use_graph
     toks = gen.history.cpu().long()
     cu = [0]
     for L in lens:
@@ -170,3 +201,98 @@ def test_greedy_generate_matches_oracle(device):
                         f"margin {float(margin[j]):.3e}"
                     ties += 1
     print(f"tokens: {4 * n_new}, near-tie token flips: {ties}, router near-tie flips: {flips}")
+
+
+def _oracle_greedy(oracle, prompt, n_new, moe, block_size=16):
+    """The oracle's own greedy continuation of one prompt (fp32, its own routing), incremental
+    over a paged reference cache: the tokens, the logits that chose them, and per MoE layer
+    the (router logits, expert choice) of the prefill and of each decode step."""
+    cfg = oracle.config
+    L = prompt.numel()
+    nblk = (L + n_new + block_size - 1) // block_size
+    shape = (nblk, cfg.num_key_value_heads, block_size, cfg.head_dim)
+    n_layers = cfg.num_hidden_layers
+    cache = PagedKVCacheRef([torch.zeros(shape) for _ in range(n_layers)],
+                            [torch.zeros(shape) for _ in range(n_layers)],
+                            torch.arange(nblk)[None])
+    gates = {i: oracle.model.layers[i].mlp.gate for i in moe}
+    toks, logits, routes = [], [], {i: [] for i in moe}
+    ids, pos = prompt.long()[None], torch.arange(L)[None]
+    with torch.no_grad():
+        for s in range(n_new):
+            lg = oracle(input_ids=ids, past_key_values=cache, cache_position=pos)[0, -1]
+            for i in moe:
+                glogits, gidx, _ = gates[i].last_routing
+                routes[i].append((glogits, gidx))
+            t = int(lg.argmax())
+            toks.append(t)
+            logits.append(lg)
+            ids, pos = torch.tensor([[t]]), torch.tensor([L + s])
+    return torch.tensor(toks), torch.stack(logits), routes
+
+
+def test_free_running_128_tokens_vs_oracle(device):
+    """128 greedy tokens from the captured decode loop against the oracle's own greedy
+    continuation (fp32, its own routing, no teacher forcing). bf16 activations on the GPU can
+    make the two part at a near tie, after which the continuations are unrelated; so per
+    prompt the test finds the first step where they part and requires that step to be a near
+    tie: the oracle's top-2 logit margin there below 2e-2, or an earlier router decision of the
+    GPU that differs from the oracle's. The first router difference (in causal order) must be a
+    router near tie (selection margin < 2e-3); the later ones route different hidden states and
+    are only counted. The report gives, per prompt, the parting step (or none), its logit
+    margin and the router differences before it."""
+    model = _tiny_lm(seed=3)
+    oracle = copy.deepcopy(model)
+    lens = [24, 17, 31, 9]
+    n_new = 128
+    prompts = _prompts(4, lens, 1000, 11)
+    hip = _hip_lm(model, device, 4)
+    trunk, head = model_parts(hip)
+    moe = [i for i, layer in enumerate(trunk.layers) if not layer.is_dense_layer]
+    for i in moe:
+        trunk.layers[i].mlp.keep_last_route = True
+    gen = GreedyGenerator(trunk, head, hip._tt_kv_cache, 4, n_new, use_graph=True)
+    gen.prefill(prompts)
+    routes = _record_routes(gen, trunk, moe, n_new)
+    toks = gen.history.cpu().long()
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    report = []
+    for b, p in enumerate(prompts):
+        own_toks, own_logits, own_routes = _oracle_greedy(oracle, p, n_new, moe)
+        parted = (own_toks != toks[b]).nonzero().flatten()
+        j = int(parted[0]) if parted.numel() else n_new
+        # router decisions that produced the logits of tokens 0..j: the prefill (entry 0) and
+        # the decode steps that fed tokens 0..j-1 (entries 1..j), in causal order (step, then
+        # layer). Up to the first difference both sides route the same hidden states up to
+        # rounding, so that difference must be a near tie; later ones follow from it (the
+        # oracle continues on its own choice) and are only reported.
+        diffs = []
+        for s in range(min(j, n_new - 1) + 1):
+            for i in moe:
+                gate = oracle.model.layers[i].mlp.gate
+                kw = dict(n_group=gate.n_group, topk_group=gate.topk_group, top_k=gate.top_k)
+                gpu = routes[i][0][cu[b]:cu[b + 1]] if s == 0 else routes[i][s][b:b + 1]
+                glogits, own = own_routes[i][s]
+                diff = (own.sort(-1).values != gpu.sort(-1).values).any(-1)
+                if bool(diff.any()):
+                    m = selection_margins(glogits, gate.expert_bias, **kw)[diff].tolist()
+                    diffs.append((s, i, m))
+        if diffs:
+            s0, i0, m0 = diffs[0]
+            assert all(m < 2e-3 for m in m0), \
+                f"prompt {b}: first router difference (step {s0}, layer {i0}) at margins {m0}"
+        router_gaps = [m for _, _, ms in diffs for m in ms]
+        if j < n_new:
+            top2 = own_logits[j].topk(2).values
+            margin = float(top2[0] - top2[1])
+            assert margin < MARGIN or router_gaps, \
+                f"prompt {b} step {j}: gpu {int(toks[b, j])} oracle {int(own_toks[j])}, " \
+                f"logit margin {margin:.3e}, no router difference before it"
+            report.append(f"prompt {b}: parts at step {j} (logit margin {margin:.3e}, "
+                          f"{len(router_gaps)} router differences before it"
+                          + (f", the first at step {diffs[0][0]}" if diffs else "") + ")")
+        else:
+            report.append(f"prompt {b}: all {n_new} tokens equal ({len(router_gaps)} router "
+                          f"differences" + (f", the first at step {diffs[0][0]}" if diffs else "")
+                          + ")")
+    print("; ".join(report))

@@ -48,11 +48,14 @@ def _hip_cache(ctx, device, num_layers=1):
     return cache
 
 
-def _oracle_with_gpu_routing(oracle_layer, hip_moe, run_oracle):
-    """Run the oracle with the GPU's expert choice; check that the oracle's own choice (from
-    its own fp32 logits) differs only on near-tie tokens. Returns (oracle output, flips)."""
+def _oracle_with_gpu_routing(oracle_layer, hip_moe, run_oracle, rows=None):
+    """Run the oracle with the GPU's expert choice (of token rows ``rows`` when the oracle runs
+    on a subset); check that the oracle's own choice (from its own fp32 logits) differs only on
+    near-tie tokens. Returns (oracle output, flips)."""
     gate = oracle_layer.mlp.gate
     gpu_idx = hip_moe.last_route.topk_idx.cpu().long()
+    if rows is not None:
+        gpu_idx = gpu_idx[rows]
     gate.route_override = gpu_idx
     try:
         with torch.no_grad():
@@ -167,8 +170,9 @@ def test_recipe_path_two_layer_model(device):
 
 def test_decode_step_graph_replay_matches_eager(device, ling_layer):
     """A HIP-graph capture of the decode step replays to the eager result on every replay,
-    with eager work and synchronisations between replays."""
-    _, layer = ling_layer
+    with eager work and synchronisations between replays; the replayed output against the
+    oracle at the layer tolerance."""
+    oracle, layer = ling_layer
     ctx = paged_context(32, 128, 4096, block_size=32, num_kv_heads=4, seed=3, device=device)
     cache = _hip_cache(ctx, device)
     x = torch.randn(32, 1, 2048, generator=torch.Generator().manual_seed(4)).bfloat16().to(device)
@@ -191,6 +195,15 @@ def test_decode_step_graph_replay_matches_eager(device, ling_layer):
         assert torch.equal(out, eager), f"replay {i} differs"
         _ = (x.float() * 2).sum()          # unrelated eager work between replays
         torch.cuda.synchronize()
+    ref_cache = PagedKVCacheRef([ctx.k_pool.float().cpu()], [ctx.v_pool.float().cpu()],
+                                ctx.page_table.cpu())
+    ref, flips = _oracle_with_gpu_routing(
+        oracle, layer.mlp,
+        lambda: oracle(x.float().cpu(), past_key_value=ref_cache,
+                       cache_position=ctx.positions.long().cpu())[0])
+    err = (out.float().cpu() - ref).abs().max().item()
+    print(f"graph replay: max|gpu-oracle| = {err:.3e}, routing flips on tokens {flips}")
+    assert err <= TOL
 
 
 def test_decoder_layer_prefill_varlen(device, ling_layer):
