@@ -168,7 +168,9 @@ def cpu_baseline(w_gpu, shape, ctx, x, steps: int, legs=True) -> dict:
             med = _time_oracle_layer(layer, c.k_pool.to(dtype).cpu(), c.v_pool.to(dtype).cpu(),
                                      c.page_table.cpu(), c.positions.cpu().long(),
                                      xc.to(dtype), steps, label)
-            results.append({"workload": f"batch {n}, {int(c.context_lens.sum())} cached tokens",
+            # a sequence's position is its number of cached tokens
+            cached = int(c.positions.cpu().long().sum())
+            results.append({"workload": f"batch {n}, {cached} cached tokens",
                             "dtype": str(dtype).split(".")[-1],
                             "ms_per_step": med * 1e3, "tokens_per_s": n / med})
         del layer

@@ -32,7 +32,7 @@ constexpr int kSplit = 4 * kTPW;  // tokens per split (one workgroup of 4 waves)
 // registers, but measured slower: 225 against 199 us at batch 128 with 1024-8192 contexts).
 constexpr int kTPW8 = 64;
 constexpr int kSplit8 = 4 * kTPW8;
-static_assert(kSplit8 == kSplit, "the decode workspace is sized for kSplit-token splits");
+static_assert(kSplit <= kSplit8, "the decode workspace (kSplit-token splits) must hold the fp8 kernel's");
 // fp8 split kernel: V is loaded after the scores (into the registers K used) and the kernel is
 // held to 6 workgroups per CU at up to 4 query heads per kv head (80 VGPRs with P.V on MFMA, 2
 // of them spilled: 164 against 170 us at 5 per CU, 82 VGPRs, at batch 128 with 1024-8192
@@ -255,6 +255,25 @@ struct FusedQKV {
   float eps;
 };
 
+// Max / sum over the 16 lanes of each row of the wave (DPP: xor 1, xor 2, half-mirror, mirror;
+// every lane of the row ends with the row's value).
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, dpp_row<0xB1>(v));
+  v = fmaxf(v, dpp_row<0x4E>(v));
+  v = fmaxf(v, dpp_row<0x141>(v));
+  return fmaxf(v, dpp_row<0x140>(v));
+}
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_row<0xB1>(v);
+  v += dpp_row<0x4E>(v);
+  v += dpp_row<0x141>(v);
+  return v + dpp_row<0x140>(v);
+}
+
 template <int G, int TPW, bool FUSED>
 __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_kernel(
     const uint16_t* __restrict__ q, FusedQKV fq, uint16_t* __restrict__ k_pool,
@@ -270,8 +289,7 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
   __shared__ __align__(16) uint16_t s_new[FUSED ? 2 : 1][D];   // new token's k and v
   __shared__ float s_p[G][SPLIT];
   __shared__ float s_red[4][G][D];
-  __shared__ float s_stat[G][4];
-  __shared__ float s_fin[2][G];
+  __shared__ float s_stat[2][G][4];  // each wave's max and sum of its tokens, per head
   __shared__ unsigned s_row[SPLIT];  // K/V pool row of each token (always an in-bounds row)
   __shared__ int s_ok[SPLIT];        // token is inside the split and its page-table entry is valid
 
@@ -369,8 +387,8 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
 #pragma unroll
     for (int j = 0; j < 4; ++j) kb[tt][j] = *reinterpret_cast<const uint4*>(kr + 32 * j);
   }
-  // V is loaded after the scores, into the registers K used: holding K and V together takes 164
-  // VGPRs (3 workgroups per CU), V late 124 VGPRs (4 per CU; 2 us faster at batch 32)
+  // V for P.V, in flight together with K: step it covers tokens it*4 + kg (4 per step), lane r16
+  // owns dims r16*8 .. +8 (the new token's row, on the writer, is substituted where V is used)
   uint4 vreg[VS];
   if constexpr (FUSED) {
     // QK-norm + RoPE of this wave's heads (K loads in flight), into LDS; the writer also
@@ -419,56 +437,65 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
           kb[tt][j] = *reinterpret_cast<const uint4*>(&s_new[0][8 * kg + 32 * j]);
   }
 
-  // ---- scores on MFMA ----
+  // ---- scores on MFMA: lane (kg, r16) holds heads 4 kg + i of token wt0 + 16 tt + r16 ----
+  float sc[KT][4];
 #pragma unroll
   for (int tt = 0; tt < KT; ++tt) {
     floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 4; ++j) sacc = mfma16x16x32(qa[j], kb[tt][j], sacc);
-    const int tl = wt0 + tt * 16 + r16;
-    const bool valid = s_ok[tl] != 0;
+    const bool valid = s_ok[wt0 + tt * 16 + r16] != 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = 4 * kg + i;
-      if (h < G) s_p[h][tl] = valid ? sacc[i] * scale_log2 : -INFINITY;
-    }
+    for (int i = 0; i < 4; ++i) sc[tt][i] = valid ? sacc[i] * scale_log2 : -INFINITY;
   }
-  // V for P.V: step it covers tokens it*4 + kg (4 per step), lane r16 owns dims r16*8 .. +8;
-  // it arrives while the softmax statistics are reduced
 #pragma unroll
   for (int it = 0; it < VS; ++it)
     vreg[it] = *reinterpret_cast<const uint4*>(v_pool + row_offset(wt0 + it * 4 + kg) + r16 * 8);
-  if (patch_new) {
-    const int tn = pos - t0;
-#pragma unroll
-    for (int it = 0; it < VS; ++it)
-      if (wt0 + it * 4 + kg == tn) vreg[it] = *reinterpret_cast<const uint4*>(&s_new[1][r16 * 8]);
-  }
-  __syncthreads();
+  const int tn = patch_new ? pos - t0 : -1;
+  const uint4 v_new = patch_new ? *reinterpret_cast<const uint4*>(&s_new[1][r16 * 8])
+                                : make_uint4(0u, 0u, 0u, 0u);
 
-  // ---- softmax statistics over the split (log2 domain); lane l < TPW owns token wt0 + l ----
-  const bool mine = lane < TPW;
-  const int tm = wt0 + (lane & (TPW - 1));
-  float mx[G];
+  // ---- softmax of this wave's tokens (log2 domain, relative to the wave's own maximum), in
+  // the score layout: each row of 16 lanes reduces its heads over its tokens with DPP. The
+  // probabilities go to s_p for the P.V operand; s_p is written and read by this wave only (LDS
+  // operations of a wave complete in order), so no workgroup barrier: the four waves' (max, sum)
+  // pairs are combined once, after P.V. ----
+  float mrow[4], lrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float m = sc[0][i];
+#pragma unroll
+    for (int tt = 1; tt < KT; ++tt) m = fmaxf(m, sc[tt][i]);
+    mrow[i] = row16_max(m);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float l = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+      const float v = sc[tt][i];
+      const float pr = (mrow[i] == -INFINITY || v == -INFINITY) ? 0.f : fast_exp2(v - mrow[i]);
+      sc[tt][i] = pr;
+      l += pr;
+    }
+    lrow[i] = row16_sum(l);
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int h = 4 * kg + i;
+      if (h < G) s_p[h][wt0 + tt * 16 + r16] = sc[tt][i];
+    }
+  asm volatile("" ::: "memory");
+  // head h's statistics live in lane 16 * (h / 4) (row h / 4, slot h % 4)
+  float mw[G], lw[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    const float m = wave_max(mine ? s_p[h][tm] : -INFINITY);
-    if (lane == 0) s_stat[h][wave] = m;
+    mw[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mrow[h % 4]), 16 * (h / 4)));
+    lw[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lrow[h % 4]), 16 * (h / 4)));
   }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-    mx[h] = fmaxf(fmaxf(s_stat[h][0], s_stat[h][1]), fmaxf(s_stat[h][2], s_stat[h][3]));
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    const float v = s_p[h][tm];
-    const float pr = (mx[h] == -INFINITY || v == -INFINITY) ? 0.f : fast_exp2(v - mx[h]);
-    if (mine) s_p[h][tm] = pr;
-    const float l = wave_sum(mine ? pr : 0.f);
-    if (lane == 0) s_stat[h][wave] = l;
-  }
-  __syncthreads();
 
   // ---- P.V on MFMA ----
   // k-step ks covers steps it = 8 ks .. 8 ks + 7: lane group kg holds tokens wt0 + 4 it + kg, lane
@@ -494,7 +521,7 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
       const uint32_t sel = (c & 1) ? 0x07060302u : 0x05040100u;
       const uint4* v0 = &vreg[8 * ks];
       auto word = [&](int m) -> uint32_t {
-        const uint4 x = v0[m];
+        const uint4 x = wt0 + 4 * (8 * ks + m) + kg == tn ? v_new : v0[m];
         return (c >> 1) == 0 ? x.x : (c >> 1) == 1 ? x.y : (c >> 1) == 2 ? x.z : x.w;
       };
       const uint4 vb = make_uint4(__builtin_amdgcn_perm(word(1), word(0), sel),
@@ -513,17 +540,38 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
       const int h = 4 * kg + i;
       if (h < G) s_red[wave][h][r16 * 8 + c] = pacc[c][i];
     }
-  if (tid < G) {
-    s_fin[0][tid] = mx[tid];
-    s_fin[1][tid] = (s_stat[tid][0] + s_stat[tid][1]) + (s_stat[tid][2] + s_stat[tid][3]);
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      s_stat[0][h][wave] = mw[h];
+      s_stat[1][h][wave] = lw[h];
+    }
   }
   __syncthreads();
+
+  // the split's maximum M over the waves' maxima and each wave's weight 2^(m_w - M) (0 for a
+  // wave without a valid token), the split's sum, and its output for head h, dim d
+  auto split_stats = [&](int h, float (&f)[4], float& M, float& L) {
+    M = fmaxf(fmaxf(s_stat[0][h][0], s_stat[0][h][1]), fmaxf(s_stat[0][h][2], s_stat[0][h][3]));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float m = s_stat[0][h][w];
+      f[w] = m == -INFINITY ? 0.f : fast_exp2(m - M);
+    }
+    L = (f[0] * s_stat[1][h][0] + f[1] * s_stat[1][h][1]) +
+        (f[2] * s_stat[1][h][2] + f[3] * s_stat[1][h][3]);
+  };
+  auto split_out = [&](int h, int d, const float (&f)[4]) {
+    return (f[0] * s_red[0][h][d] + f[1] * s_red[1][h][d]) +
+           (f[2] * s_red[2][h][d] + f[3] * s_red[3][h][d]);
+  };
 
   if (nsplit == 1) {
     for (int i = tid; i < G * D; i += kAttnThreads) {
       const int h = i / D, d = i - h * D;
-      const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
-      const float L = s_fin[1][h];
+      float f[4], M, L;
+      split_stats(h, f, M, L);
+      const float o = split_out(h, d, f);
       out[((size_t)b * Hq + g * G + h) * D + d] = f32_to_bf16(L > 0.f ? o / L : 0.f);
     }
     return;
@@ -532,13 +580,16 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
   // this split's unnormalised output and (max, sum); the merge kernel combines the splits
   for (int i = tid; i < G * D; i += kAttnThreads) {
     const int h = i / D, d = i - h * D;
-    const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
-    ws_o[(((size_t)b * Hq + g * G + h) * max_splits + split) * D + d] = o;
+    float f[4], M, L;
+    split_stats(h, f, M, L);
+    ws_o[(((size_t)b * Hq + g * G + h) * max_splits + split) * D + d] = split_out(h, d, f);
   }
   if (tid < G) {
+    float f[4], M, L;
+    split_stats(tid, f, M, L);
     float* ml = ws_ml + (((size_t)b * Hq + g * G + tid) * max_splits + split) * 2;
-    ml[0] = s_fin[0][tid];
-    ml[1] = s_fin[1][tid];
+    ml[0] = M;
+    ml[1] = L;
   }
 }
 
@@ -834,8 +885,7 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
   __shared__ __align__(16) uint16_t s_q[G][D];
   __shared__ __align__(16) float s_p[G][SPLIT];
   __shared__ float s_red[4][G][D];
-  __shared__ float s_stat[G][4];
-  __shared__ float s_fin[2][G];
+  __shared__ float s_stat[2][G][4];  // each wave's max and sum of its tokens, per head
   __shared__ unsigned s_row[SPLIT];
 
   const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
@@ -890,10 +940,8 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
           q + ((size_t)b * Hq + g * G + h) * D + c * 8);
     }
   }
-  // tokens t0 + tid + 256 j of the split: their pool rows (always in bounds), validity and
-  // scale indices
+  // tokens t0 + tid + 256 j of the split: their pool rows (always in bounds) and validity
   bool my_ok[TPT];
-  size_t my_sidx[TPT];
 #pragma unroll
   for (int j = 0; j < TPT; ++j) {
     const int tl = tid + kAttnThreads * j;
@@ -904,8 +952,8 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
     my_ok[j] = t < t1 && pb >= 0 && pb < num_blocks;
     if (pb < 0 || pb >= num_blocks) pb = 0;
     s_row[tl] = (unsigned)(((size_t)pb * Hkv + g) * block_size + (tc - blk * block_size));
-    my_sidx[j] = (size_t)pb * Hkv + g;
   }
+  const unsigned long long okw = __ballot(my_ok[0]);  // validity of this wave's 64 tokens
   if constexpr (FUSED) {
 #pragma unroll
     for (int jj = 0; jj < JPW; ++jj) asm volatile("" ::"v"(hx[jj][0]), "v"(hx[jj][1]));
@@ -922,7 +970,10 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
   static_assert(TPW == 64 && TPT == 1, "P.V MFMA tiling assumes 64 tokens per wave");
   constexpr int KS = TPW / 32;
   uint2 vreg[KS][D / 16];
-  float ks_own[TPT], vs_own[TPT];
+  // K and V scales of the tokens wt0 + 16 tt + r16 this lane holds scores of: the scale index
+  // (block, head) is the pool row / block_size (a power of two)
+  const int bs_log2 = 31 - __clz(block_size);
+  float ksc[KT], vsc[KT];
   auto load_v = [&]() {
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
@@ -937,14 +988,12 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
   auto issue_loads = [&]() {
 #pragma unroll
     for (int tt = 0; tt < KT; ++tt) {
-      const uint8_t* kr = k_pool + (size_t)s_row[wt0 + tt * 16 + r16] * D + 32 * kg;
+      const unsigned row = s_row[wt0 + tt * 16 + r16];
+      const uint8_t* kr = k_pool + (size_t)row * D + 32 * kg;
       kb[tt][0] = *reinterpret_cast<const uint4*>(kr);
       kb[tt][1] = *reinterpret_cast<const uint4*>(kr + 16);
-    }
-#pragma unroll
-    for (int j = 0; j < TPT; ++j) {
-      ks_own[j] = k_scale[my_sidx[j]];
-      vs_own[j] = v_scale[my_sidx[j]];
+      ksc[tt] = k_scale[row >> bs_log2];
+      vsc[tt] = v_scale[row >> bs_log2];
     }
   };
   if (!writer) issue_loads();
@@ -986,7 +1035,8 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
     }
   }
 
-  // ---- raw scores (before the K scale) on MFMA ----
+  // ---- scores on MFMA: lane (kg, r16) holds heads 4 kg + i of token wt0 + 16 tt + r16 ----
+  float sc[KT][4];
 #pragma unroll
   for (int tt = 0; tt < KT; ++tt) {
     floatx4 sacc = {0.f, 0.f, 0.f, 0.f};
@@ -994,53 +1044,56 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
     sacc = mfma16x16x32(qa[1], fp8x8_to_bf16x8(kb[tt][0].z, kb[tt][0].w), sacc);
     sacc = mfma16x16x32(qa[2], fp8x8_to_bf16x8(kb[tt][1].x, kb[tt][1].y), sacc);
     sacc = mfma16x16x32(qa[3], fp8x8_to_bf16x8(kb[tt][1].z, kb[tt][1].w), sacc);
-    const int tl = wt0 + tt * 16 + r16;
+    const bool valid = (okw >> (tt * 16 + r16)) & 1ull;
+    const float f = ksc[tt] * scale_log2;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sc[tt][i] = valid ? sacc[i] * f : -INFINITY;
+  }
+  load_v();  // into the registers K used; arrives during the softmax
+
+  // ---- softmax of this wave's tokens (log2 domain, relative to the wave's own maximum), in
+  // the score layout: each row of 16 lanes reduces its heads over its tokens with DPP. P (times
+  // the token's V scale) goes to s_p for the P.V operand; s_p is written and read by this wave
+  // only (LDS operations of a wave complete in order), so no workgroup barrier: the four waves'
+  // (max, sum) pairs are combined once, after P.V. ----
+  float mrow[4], lrow[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float m = sc[0][i];
+#pragma unroll
+    for (int tt = 1; tt < KT; ++tt) m = fmaxf(m, sc[tt][i]);
+    mrow[i] = row16_max(m);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float l = 0.f;
+#pragma unroll
+    for (int tt = 0; tt < KT; ++tt) {
+      const float v = sc[tt][i];
+      const float pr = (mrow[i] == -INFINITY || v == -INFINITY) ? 0.f : fast_exp2(v - mrow[i]);
+      sc[tt][i] = pr * vsc[tt];
+      l += pr;
+    }
+    lrow[i] = row16_sum(l);
+  }
+  asm volatile("" ::: "memory");
+#pragma unroll
+  for (int tt = 0; tt < KT; ++tt)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int h = 4 * kg + i;
-      if (h < G) s_p[h][tl] = sacc[i];
+      if (h < G) s_p[h][wt0 + tt * 16 + r16] = sc[tt][i];
     }
-  }
-  load_v();  // into the registers K used; arrives during the softmax
-  __syncthreads();
-
-  // ---- softmax statistics (log2 domain); thread tid owns tokens t0 + tid + 256 j ----
-  float mx[G];
-  float sc[G][TPT];
+  asm volatile("" ::: "memory");
+  // head h's statistics live in lane 16 * (h / 4) (row h / 4, slot h % 4)
+  float mw[G], lw[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) {
-    float m = -INFINITY;
-#pragma unroll
-    for (int j = 0; j < TPT; ++j) {
-      sc[h][j] = my_ok[j] ? s_p[h][tid + kAttnThreads * j] * (ks_own[j] * scale_log2)
-                          : -INFINITY;
-      m = fmaxf(m, sc[h][j]);
-    }
-    m = wave_max(m);
-    if (lane == 0) s_stat[h][wave] = m;
+    mw[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(mrow[h % 4]), 16 * (h / 4)));
+    lw[h] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(lrow[h % 4]), 16 * (h / 4)));
   }
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < G; ++h)
-    mx[h] = fmaxf(fmaxf(s_stat[h][0], s_stat[h][1]), fmaxf(s_stat[h][2], s_stat[h][3]));
-  __syncthreads();
-#pragma unroll
-  for (int h = 0; h < G; ++h) {
-    float l = 0.f;
-#pragma unroll
-    for (int j = 0; j < TPT; ++j) {
-      const float pr =
-          (mx[h] == -INFINITY || sc[h][j] == -INFINITY) ? 0.f : fast_exp2(sc[h][j] - mx[h]);
-      s_p[h][tid + kAttnThreads * j] = pr * vs_own[j];
-      l += pr;
-    }
-    l = wave_sum(l);
-    if (lane == 0) s_stat[h][wave] = l;
-  }
-  __syncthreads();
 
   // ---- P.V on MFMA: O[head][dim] += P[head][token] . V[token][dim] per 32-token k-step ----
-  const unsigned long long okw = __ballot(my_ok[0]);  // validity of this wave's 64 tokens
   floatx4 oacc[D / 16];
 #pragma unroll
   for (int j = 0; j < D / 16; ++j) oacc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -1070,30 +1123,54 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
       const int h = 4 * kg + i;
       if (h < G) s_red[wave][h][16 * j + r16] = oacc[j][i];
     }
-  if (tid < G) {
-    s_fin[0][tid] = mx[tid];
-    s_fin[1][tid] = (s_stat[tid][0] + s_stat[tid][1]) + (s_stat[tid][2] + s_stat[tid][3]);
+  if (lane == 0) {
+#pragma unroll
+    for (int h = 0; h < G; ++h) {
+      s_stat[0][h][wave] = mw[h];
+      s_stat[1][h][wave] = lw[h];
+    }
   }
   __syncthreads();
+
+  // the split's maximum M over the waves' maxima and each wave's weight 2^(m_w - M) (0 for a
+  // wave without a valid token), the split's sum, and its output for head h, dim d
+  auto split_stats = [&](int h, float (&f)[4], float& M, float& L) {
+    M = fmaxf(fmaxf(s_stat[0][h][0], s_stat[0][h][1]), fmaxf(s_stat[0][h][2], s_stat[0][h][3]));
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float m = s_stat[0][h][w];
+      f[w] = m == -INFINITY ? 0.f : fast_exp2(m - M);
+    }
+    L = (f[0] * s_stat[1][h][0] + f[1] * s_stat[1][h][1]) +
+        (f[2] * s_stat[1][h][2] + f[3] * s_stat[1][h][3]);
+  };
+  auto split_out = [&](int h, int d, const float (&f)[4]) {
+    return (f[0] * s_red[0][h][d] + f[1] * s_red[1][h][d]) +
+           (f[2] * s_red[2][h][d] + f[3] * s_red[3][h][d]);
+  };
 
   if (nsplit == 1) {
     for (int i = tid; i < G * D; i += kAttnThreads) {
       const int h = i / D, d = i - h * D;
-      const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
-      const float L = s_fin[1][h];
+      float f[4], M, L;
+      split_stats(h, f, M, L);
+      const float o = split_out(h, d, f);
       out[((size_t)b * Hq + g * G + h) * D + d] = f32_to_bf16(L > 0.f ? o / L : 0.f);
     }
     return;
   }
   for (int i = tid; i < G * D; i += kAttnThreads) {
     const int h = i / D, d = i - h * D;
-    const float o = (s_red[0][h][d] + s_red[1][h][d]) + (s_red[2][h][d] + s_red[3][h][d]);
-    ws_o[(((size_t)b * Hq + g * G + h) * max_splits + split) * D + d] = o;
+    float f[4], M, L;
+    split_stats(h, f, M, L);
+    ws_o[(((size_t)b * Hq + g * G + h) * max_splits + split) * D + d] = split_out(h, d, f);
   }
   if (tid < G) {
+    float f[4], M, L;
+    split_stats(tid, f, M, L);
     float* ml = ws_ml + (((size_t)b * Hq + g * G + tid) * max_splits + split) * 2;
-    ml[0] = s_fin[0][tid];
-    ml[1] = s_fin[1][tid];
+    ml[0] = M;
+    ml[1] = L;
   }
 }
 
@@ -1245,8 +1322,8 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
               SYM_ERR_INVALID, "%s: null pointer argument", what);
   const bool fp8 = k_scale != nullptr;
   SYM_REQUIRE(fp8 == (v_scale != nullptr), SYM_ERR_INVALID, "%s: k_scale and v_scale", what);
-  SYM_REQUIRE(!fp8 || (kSplit % block_size == 0 && block_size % 8 == 0), SYM_ERR_UNSUPPORTED,
-              "%s: fp8 cache needs block_size a multiple of 8 dividing %d (got %d)", what, kSplit,
+  SYM_REQUIRE(!fp8 || (kSplit8 % block_size == 0 && block_size % 8 == 0), SYM_ERR_UNSUPPORTED,
+              "%s: fp8 cache needs block_size a multiple of 8 dividing %d (got %d)", what, kSplit8,
               block_size);
   SYM_REQUIRE(Hq >= Hkv && Hq % Hkv == 0, SYM_ERR_INVALID, "%s: Hq=%d not a multiple of Hkv=%d",
               what, Hq, Hkv);
@@ -1267,7 +1344,13 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
   const float scale_log2 = scale * 1.4426950408889634f;
   hipStream_t s = (hipStream_t)stream;
   (void)hipGetLastError();
-  const dim3 grid(max_splits, Hkv, B), block(kAttnThreads);
+  // Workgroups are spread over the XCDs and their shader engines in linear-id order, so a split
+  // dimension that is a multiple of 32 puts split s of every (kv head, sequence) row on the same
+  // XCD / engine slot: the low splits (present in every sequence) pile onto a quarter of the
+  // CUs while the high ones (mostly past the end) leave others idle. An odd width rotates the
+  // mapping from row to row; the extra split starts at or past max_context and exits at once.
+  // (fp8 batch 128, 1024-8192 tokens: 32 -> 33 splits, 153 -> 123 us.)
+  const dim3 grid(max_splits | 1, Hkv, B), block(kAttnThreads);
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* kp = (uint16_t*)k_pool;
   uint16_t* vp = (uint16_t*)v_pool;
@@ -1471,9 +1554,9 @@ extern "C" int sym_paged_kv_fill_fp8(const void* k, const void* v, long long tok
   if (n_seqs == 0 || max_seqlen == 0) return SYM_OK;
   SYM_REQUIRE(k && v && cu_seqlens && k_pool && v_pool && k_scale && v_scale && block_tables,
               SYM_ERR_INVALID, "paged_kv_fill_fp8: null pointer argument");
-  SYM_REQUIRE(kSplit % block_size == 0 && block_size % 8 == 0, SYM_ERR_UNSUPPORTED,
+  SYM_REQUIRE(kSplit8 % block_size == 0 && block_size % 8 == 0, SYM_ERR_UNSUPPORTED,
               "paged_kv_fill_fp8: block_size=%d must be a multiple of 8 dividing %d", block_size,
-              kSplit);
+              kSplit8);
   SYM_REQUIRE(n_seqs <= 65535 && Hkv <= 65535, SYM_ERR_INVALID, "paged_kv_fill_fp8: grid");
   SYM_REQUIRE(page_table_rows >= 1 && (seq_rows || n_seqs <= page_table_rows), SYM_ERR_INVALID,
               "paged_kv_fill_fp8: %d sequences for a page table of %d rows", n_seqs,
