@@ -55,8 +55,8 @@ ROUTE_CASES = [
     (32, 256, 8, 4, 8, "randn"),
     (64, 256, 8, 4, 8, "randn"),
     (65, 256, 8, 4, 8, "randn"),
-    (128, 256, 8, 4, 8, "zipf"),        # largest batch of the one-workgroup route + permute
-    (129, 256, 8, 4, 8, "ties"),        # smallest batch of the two-launch route + permute
+    (128, 256, 8, 4, 8, "zipf"),        # the fp8 decode batch
+    (129, 256, 8, 4, 8, "ties"),
     (1000, 256, 8, 4, 8, "randn"),
     (9000, 256, 8, 4, 8, "zipf"),
     (300, 64, 8, 4, 4, "randn"),
