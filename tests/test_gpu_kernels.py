@@ -201,8 +201,10 @@ def test_router_logits_split(device, T, H, E):
     (32, 2048, 2048, True, torch.bfloat16),
     (1, 256, 512, False, torch.float32),
     (70, 128, 192, True, torch.float32),
-    (64, 2048, 2048, False, torch.float32),      # one 64-row pass
+    (64, 2048, 2048, False, torch.float32),      # 32-row passes, weights held in registers
     (100, 512, 1024, True, torch.bfloat16),
+    (128, 3072, 2048, True, torch.bfloat16),     # the batch-128 QKV shape
+    (77, 2048, 2048, False, torch.float32),      # a partial last pass
 ])
 def test_linear(device, M, N, K, bias, out_dtype):
     g = torch.Generator().manual_seed(M + N + K)
@@ -227,7 +229,8 @@ def _rmsnorm_bf16(x, gamma, eps):
 
 @pytest.mark.parametrize("M,N,K,bias", [(32, 3072, 2048, False), (64, 3072, 2048, False),
                                         (48, 512, 1024, True), (1, 256, 2048, True),
-                                        (70, 128, 192, True)])
+                                        (70, 128, 192, True), (128, 3072, 2048, False),
+                                        (97, 2048, 2048, True)])
 def test_rmsnorm_linear(device, M, N, K, bias):
     g = torch.Generator().manual_seed(M * 3 + N + K)
     x = (torch.randn(M, K, generator=g) * 1.5).bfloat16()
@@ -247,7 +250,7 @@ def test_rmsnorm_linear(device, M, N, K, bias):
 
 
 @pytest.mark.parametrize("M,N,K", [(32, 2048, 2048), (64, 2048, 2048), (5, 256, 512),
-                                   (40, 128, 192)])
+                                   (40, 128, 192), (128, 2048, 2048), (33, 2048, 2048)])
 def test_linear_residual(device, M, N, K):
     g = torch.Generator().manual_seed(M + 7 * N + K)
     x = torch.randn(M, K, generator=g).bfloat16()

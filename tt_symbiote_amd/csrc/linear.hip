@@ -287,6 +287,142 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
   }
 }
 
+// Rows in 32-row passes for M > 32 with K = 64 * 4 * kLinWaves: each wave's weights for its 4
+// K-steps are loaded once and stay in registers for every pass. The next pass's activations
+// are requested into the same registers as soon as the current pass's MFMAs have read them, so
+// they arrive during the cross-wave reduction and the stores; the epilogue's bias and residual
+// are requested when the pass starts. (The general kernel above re-streams the weights and
+// waits for every load in every pass.)
+template <bool NORM, bool RES>
+__global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
+    const uint16_t* __restrict__ bias, int M, int N, int K, const uint16_t* __restrict__ gamma,
+    float eps, const uint16_t* __restrict__ residual, float* __restrict__ sumsq_parts,
+    uint16_t* __restrict__ out_bf16, float* __restrict__ out_f32) {
+  constexpr int MT = 2, U = 4;
+  static_assert(256 * MT == kLinThreads, "one output element per thread and pass");
+  __shared__ float s_red[kLinWaves][MT][4][64];
+  __shared__ float s_ss[NORM ? kLinWaves : 1][16 * MT];
+  __shared__ float s_r[16 * MT];
+  const int col0 = blockIdx.x * 16;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const int k0 = wave * U * 64 + kq * 16;  // this lane's first element of the wave's K range
+  const uint16_t* wr = w + (size_t)(col0 + r16) * K + k0;
+  // this thread's output element of each pass: element i of lane l's fragment of tile mt
+  const int e_mt = threadIdx.x >> 8, e_l = threadIdx.x & 63, e_i = (threadIdx.x >> 6) & 3;
+  const int e_row = e_mt * 16 + 4 * (e_l >> 4) + e_i;  // + mb
+  const int e_col = col0 + (e_l & 15);
+
+  uint4 b[U][2];
+#pragma unroll
+  for (int s = 0; s < U; ++s) {
+    b[s][0] = ldg16(wr + s * 64);
+    b[s][1] = ldg16(wr + s * 64 + 8);
+  }
+  // rows past M read row M - 1 (in bounds); their outputs are dropped
+  uint4 a[MT][U][2];
+  auto load_rows = [&](int mb) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const uint16_t* xr = x + (size_t)min(mb + mt * 16 + r16, M - 1) * K + k0;
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        a[mt][s][0] = ldg16(xr + s * 64);
+        a[mt][s][1] = ldg16(xr + s * 64 + 8);
+      }
+    }
+  };
+  load_rows(0);
+  const float bias_v = bias ? bf16_to_f32(bias[e_col]) : 0.f;
+
+  for (int mb = 0; mb < M; mb += 16 * MT) {
+    const int row = mb + e_row;
+    const bool ok = row < M;
+    float res_v = 0.f;
+    if constexpr (RES) res_v = ok ? bf16_to_f32(residual[(size_t)row * N + e_col]) : 0.f;
+    floatx4 acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (NORM) {
+      // gamma is reloaded per pass (cache hits) rather than held: the registers go to the
+      // weights
+      uint4 gm[U][2];
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        gm[s][0] = ldg16(gamma + k0 + s * 64);
+        gm[s][1] = ldg16(gamma + k0 + s * 64 + 8);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        float v = 0.f;
+#pragma unroll
+        for (int s = 0; s < U; ++s) v += sumsq8(a[mt][s][0]) + sumsq8(a[mt][s][1]);
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        if (kq == 0) s_ss[wave][mt * 16 + r16] = v;
+      }
+      __syncthreads();
+      if (threadIdx.x < 16 * MT) {
+        float t = 0.f;
+#pragma unroll
+        for (int i = 0; i < kLinWaves; ++i) t += s_ss[i][threadIdx.x];
+        s_r[threadIdx.x] = rsqrtf(t / (float)K + eps);
+      }
+      __syncthreads();
+      // normalised rows in place, one K-step at a time (a scheduling barrier after each keeps
+      // the compiler from converting all of them ahead of the MFMAs)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const float r = s_r[mt * 16 + r16];
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          a[mt][s][0] = scale8(a[mt][s][0], gm[s][0], r);
+          a[mt][s][1] = scale8(a[mt][s][1], gm[s][1], r);
+          acc[mt] = mfma16x16x32(a[mt][s][0], b[s][0], acc[mt]);
+          acc[mt] = mfma16x16x32(a[mt][s][1], b[s][1], acc[mt]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          acc[mt] = mfma16x16x32(a[mt][s][0], b[s][0], acc[mt]);
+          acc[mt] = mfma16x16x32(a[mt][s][1], b[s][1], acc[mt]);
+        }
+    }
+    // the MFMAs have read the rows: the next pass's rows go into the same registers now
+    if (mb + 16 * MT < M) load_rows(mb + 16 * MT);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) s_red[wave][mt][i][lane] = acc[mt][i];
+    __syncthreads();
+    float v = bias_v;
+#pragma unroll
+    for (int wv = 0; wv < kLinWaves; ++wv) v += s_red[wv][e_mt][e_i][e_l];
+    if constexpr (RES) {
+      v += res_v;
+      if (ok) out_f32[(size_t)row * N + e_col] = v;
+      // sum of squares over the 16 columns of this row (16 consecutive lanes)
+      float q = ok ? v * v : 0.f;
+      q += __shfl_xor(q, 1);
+      q += __shfl_xor(q, 2);
+      q += __shfl_xor(q, 4);
+      q += __shfl_xor(q, 8);
+      if (ok && (e_l & 15) == 0) sumsq_parts[(size_t)blockIdx.x * M + row] = q;
+    } else if (ok) {
+      if (out_f32) out_f32[(size_t)row * N + e_col] = v;
+      else out_bf16[(size_t)row * N + e_col] = f32_to_bf16(v);
+    }
+    __syncthreads();
+  }
+}
+
 }  // namespace sym
 
 using namespace sym;
@@ -308,7 +444,12 @@ static void launch_proj(const void* x, const void* w, const void* bias, int M, i
   // rows in passes of 16 * MT, each pass streaming the weights: one pass up to 64 rows. With
   // the norm fused, 32-row passes keep the single-batch path (a 64-row pass needs two batches
   // of K-steps and measured slower at 64 rows: 24.4 against 18.7 us for 3072 x 2048)
-  if (M > 32 && !NORM)
+  if (M > 32 && K == 64 * 4 * kLinWaves)
+    hipLaunchKernelGGL((proj_rows_kernel<NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
+                       (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
+                       (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
+                       (uint16_t*)out_bf16, out_f32);
+  else if (M > 32 && !NORM)
     hipLaunchKernelGGL((proj_kernel<4, 4, NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
                        (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
                        (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
