@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
   const uint16_t* wr = w + (size_t)(col0 + r16) * K + kq * 16;
   const uint16_t* gr = NORM ? gamma + kq * 16 : nullptr;
 
-  for (int mb = 0; mb < M; mb += 16 * MT) {
+  for (int mb = blockIdx.y * 16 * MT; mb < M; mb += gridDim.y * 16 * MT) {
     const int nmt = min(MT, (M - mb + 15) >> 4);
     floatx4 acc[MT];
     const uint16_t* xr[MT];
@@ -201,13 +201,18 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
           s_r[threadIdx.x] = rsqrtf(t / (float)K + eps);
         }
         __syncthreads();
+        // normalised rows in place, one K-step at a time (a scheduling barrier after each
+        // keeps the compiler from converting all of them ahead of the MFMAs)
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const float r = s_r[mt * 16 + r16];
 #pragma unroll
           for (int s = 0; s < U; ++s) {
-            acc[mt] = mfma16x16x32(scale8(a[mt][s][0], gm[s][0], r), b[s][0], acc[mt]);
-            acc[mt] = mfma16x16x32(scale8(a[mt][s][1], gm[s][1], r), b[s][1], acc[mt]);
+            a[mt][s][0] = scale8(a[mt][s][0], gm[s][0], r);
+            a[mt][s][1] = scale8(a[mt][s][1], gm[s][1], r);
+            acc[mt] = mfma16x16x32(a[mt][s][0], b[s][0], acc[mt]);
+            acc[mt] = mfma16x16x32(a[mt][s][1], b[s][1], acc[mt]);
+            __builtin_amdgcn_sched_barrier(0);
           }
         }
         done = true;
@@ -441,9 +446,9 @@ template <bool NORM, bool RES>
 static void launch_proj(const void* x, const void* w, const void* bias, int M, int N, int K,
                         const void* gamma, float eps, const void* residual, float* sumsq_parts,
                         void* out_bf16, float* out_f32, hipStream_t s) {
-  // rows in passes of 16 * MT, each pass streaming the weights: one pass up to 64 rows. With
-  // the norm fused, 32-row passes keep the single-batch path (a 64-row pass needs two batches
-  // of K-steps and measured slower at 64 rows: 24.4 against 18.7 us for 3072 x 2048)
+  // Above 32 rows with K = 2048: 32-row passes over weights held in registers. Other K above
+  // 32 rows: passes of 64 rows (32 with the norm fused, whose single-batch path a 64-row pass
+  // would leave: 24.4 against 18.7 us for 3072 x 2048 at 64 rows), each streaming the weights.
   if (M > 32 && K == 64 * 4 * kLinWaves)
     hipLaunchKernelGGL((proj_rows_kernel<NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
                        (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
@@ -454,6 +459,14 @@ static void launch_proj(const void* x, const void* w, const void* bias, int M, i
                        (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
                        (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
                        (uint16_t*)out_bf16, out_f32);
+  else if (!NORM)
+    // 16-row blocks as a second grid dimension: each workgroup reads half the activations of a
+    // 32-row batch and the grid doubles (dense 2048 x 2048 at 32 rows: 8.3 -> 6.7 us). With the
+    // norm fused the 16-row kernel needs 172 VGPRs (2 rounds of workgroups), so it keeps 32.
+    hipLaunchKernelGGL((proj_kernel<1, 4, NORM, RES>), dim3(N / 16, (M + 15) / 16),
+                       dim3(kLinThreads), 0, s, (const uint16_t*)x, (const uint16_t*)w,
+                       (const uint16_t*)bias, M, N, K, (const uint16_t*)gamma, eps,
+                       (const uint16_t*)residual, sumsq_parts, (uint16_t*)out_bf16, out_f32);
   else
     hipLaunchKernelGGL((proj_kernel<2, 4, NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
                        (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,

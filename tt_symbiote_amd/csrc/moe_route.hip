@@ -457,15 +457,18 @@ __global__ __launch_bounds__(256) void moe_permute_scatter_kernel(
 // a separate RMSNorm pass), upcast. The workgroups of the first expert tile also store that
 // normalised row (bf16) for the expert GEMMs.
 constexpr int kLogitWaves = 8;
-constexpr int kLogitRows = 32;  // token rows per pass (two 16-row tiles)
+constexpr int kLogitRows = 32;  // token rows per pass at most (two 16-row tiles)
 
-template <bool NORM>
+// NT 16-row tiles per workgroup (grid z = passes of 16 * NT rows): a decode batch of up to 32
+// tokens takes one tile per workgroup, so its 256 experts x 4 quarters of H spread over 128
+// workgroups instead of 64.
+template <bool NORM, int NT>
 __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
     const uint16_t* __restrict__ x, const float* __restrict__ hres,
     const float* __restrict__ ss_parts, int n_ss, const uint16_t* __restrict__ gamma, float eps,
     const float* __restrict__ w, int T, int H, int E, float* __restrict__ parts,
     uint16_t* __restrict__ xn_out) {
-  __shared__ float s_red[kLogitWaves][2][4][64];
+  __shared__ float s_red[kLogitWaves][NT][4][64];
   __shared__ float s_r[kLogitRows];
   const int ntile = blockIdx.x;
   const int q = blockIdx.y;
@@ -481,11 +484,13 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
   // one pass of kLogitRows tokens per workgroup (grid z), so long prompts spread over many
   // workgroups
   {
-    const int mb = blockIdx.z * kLogitRows;
+    const int mb = blockIdx.z * 16 * NT;
     float rm[2] = {1.f, 1.f};
     // rows past T repeat the last row; their results are dropped
     const int m0 = min(mb + r16, T - 1), m1 = min(mb + 16 + r16, T - 1);
-    floatx4 acc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+    floatx4 acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = floatx4{0.f, 0.f, 0.f, 0.f};
     // NORM: the first 128 partial sums of squares of the pass's rows (16 threads per row, each
     // every 16th), issued before the weight and activation loads: loads complete in order, so
     // the rows' r is then reduced while those are still arriving
@@ -502,13 +507,13 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
       // the range repeat the last chunk's loads and contribute zero (no branch, which would let
       // the compiler sink their loads behind the first MFMAs)
       float4 b[4];
-      float4 hv[2][4];
-      uint2 xv[2][4], gv[4];
+      float4 hv[NT][4];
+      uint2 xv[NT][4], gv[4];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
         b[c] = *reinterpret_cast<const float4*>(wr + 16 * min(kc + c, nk - 1));
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const size_t off = (size_t)(t ? m1 : m0) * H + k_beg + 16 * min(kc + c, nk - 1);
@@ -544,13 +549,13 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
           if (c == 0) s_r[threadIdx.x >> 4] = rsqrtf(t / (float)H + eps);
           __syncthreads();
           rm[0] = s_r[r16];
-          rm[1] = s_r[16 + r16];
+          rm[1] = s_r[(NT - 1) * 16 + r16];
         }
       }
       __builtin_amdgcn_sched_barrier(0);
-      float a[2][4][4];
+      float a[NT][4][4];
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           if constexpr (NORM) {
@@ -567,7 +572,7 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
           }
         }
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int t = 0; t < NT; ++t)
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           const float z = kc + c < nk ? 1.f : 0.f;
@@ -580,7 +585,7 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
         if (xn_out && ntile == 0) {
           // the normalised rows, for the expert GEMMs
 #pragma unroll
-          for (int t = 0; t < 2; ++t)
+          for (int t = 0; t < NT; ++t)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
               if (kc + c < nk && mb + t * 16 + r16 < T) {
@@ -595,12 +600,12 @@ __global__ __launch_bounds__(kLogitWaves * 64) void moe_router_logits_kernel(
       }
     }
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+    for (int t = 0; t < NT; ++t)
 #pragma unroll
       for (int i = 0; i < 4; ++i) s_red[wave][t][i][lane] = acc[t][i];
     __syncthreads();
-    {
-      // 512 threads: tile t = tid / 256, element i of lane l's fragment
+    if (threadIdx.x < 256 * NT) {
+      // tile t = tid / 256, element i of lane l's fragment
       const int t = threadIdx.x >> 8;
       const int l = threadIdx.x & 63;
       const int i = (threadIdx.x >> 6) & 3;
@@ -641,11 +646,18 @@ extern "C" int sym_moe_router_logits(const void* x, const float* w, int T, int H
   (void)hipGetLastError();
   SYM_REQUIRE((T + kLogitRows - 1) / kLogitRows <= 65535, SYM_ERR_UNSUPPORTED,
               "moe_router_logits: T=%d too large", T);
-  hipLaunchKernelGGL((moe_router_logits_kernel<false>),
-                     dim3(E / 16, kLogitParts, (T + kLogitRows - 1) / kLogitRows),
-                     dim3(kLogitWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)x,
-                     (const float*)nullptr, (const float*)nullptr, 0, (const uint16_t*)nullptr,
-                     0.f, w, T, H, E, parts, (uint16_t*)nullptr);
+  if (T <= 32)
+    hipLaunchKernelGGL((moe_router_logits_kernel<false, 1>),
+                       dim3(E / 16, kLogitParts, (T + 15) / 16), dim3(kLogitWaves * 64), 0,
+                       (hipStream_t)stream, (const uint16_t*)x, (const float*)nullptr,
+                       (const float*)nullptr, 0, (const uint16_t*)nullptr, 0.f, w, T, H, E,
+                       parts, (uint16_t*)nullptr);
+  else
+    hipLaunchKernelGGL((moe_router_logits_kernel<false, 2>),
+                       dim3(E / 16, kLogitParts, (T + kLogitRows - 1) / kLogitRows),
+                       dim3(kLogitWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)x,
+                       (const float*)nullptr, (const float*)nullptr, 0,
+                       (const uint16_t*)nullptr, 0.f, w, T, H, E, parts, (uint16_t*)nullptr);
   return sym_host::check_launch("moe_router_logits_kernel");
 }
 
@@ -661,11 +673,17 @@ extern "C" int sym_moe_router_logits_norm(const float* h, const float* ss_parts,
   (void)hipGetLastError();
   SYM_REQUIRE((T + kLogitRows - 1) / kLogitRows <= 65535, SYM_ERR_UNSUPPORTED,
               "moe_router_logits_norm: T=%d too large", T);
-  hipLaunchKernelGGL((moe_router_logits_kernel<true>),
-                     dim3(E / 16, kLogitParts, (T + kLogitRows - 1) / kLogitRows),
-                     dim3(kLogitWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)nullptr, h,
-                     ss_parts, n_ss, (const uint16_t*)gamma, eps, w, T, H, E, parts,
-                     (uint16_t*)xn_out);
+  if (T <= 32)
+    hipLaunchKernelGGL((moe_router_logits_kernel<true, 1>),
+                       dim3(E / 16, kLogitParts, (T + 15) / 16), dim3(kLogitWaves * 64), 0,
+                       (hipStream_t)stream, (const uint16_t*)nullptr, h, ss_parts, n_ss,
+                       (const uint16_t*)gamma, eps, w, T, H, E, parts, (uint16_t*)xn_out);
+  else
+    hipLaunchKernelGGL((moe_router_logits_kernel<true, 2>),
+                       dim3(E / 16, kLogitParts, (T + kLogitRows - 1) / kLogitRows),
+                       dim3(kLogitWaves * 64), 0, (hipStream_t)stream, (const uint16_t*)nullptr,
+                       h, ss_parts, n_ss, (const uint16_t*)gamma, eps, w, T, H, E, parts,
+                       (uint16_t*)xn_out);
   return sym_host::check_launch("moe_router_logits_kernel");
 }
 
