@@ -470,7 +470,8 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   const int t = blockIdx.x;
   const int32_t* ip = inv_perm + (size_t)t * K;
   const float* tw = topk_w + (size_t)t * K;
-  for (int c = threadIdx.x * 8; c < H; c += blockDim.x * 8) {
+  const int stride = gridDim.y * blockDim.x * 8;
+  for (int c = (blockIdx.y * blockDim.x + threadIdx.x) * 8; c < H; c += stride) {
     // the shared expert's row and the residual do not depend on the routing: issued first
     float sh[8], rs[8];
     if (shared_row0 >= 0) load_y8(y + (size_t)(shared_row0 + t) * H + c, sh);
@@ -615,12 +616,19 @@ extern "C" int sym_moe_unpermute_combine(const void* y, int y_bf16, const int32_
   SYM_REQUIRE(top_k >= 1 && top_k <= 64, SYM_ERR_INVALID, "moe_unpermute_combine: top_k=%d",
               top_k);
   (void)hipGetLastError();
+  // a decode batch spreads each token's row over several 64-thread workgroups (more CUs
+  // loading the assignments' rows at once); prefill sizes keep one 256-thread workgroup per
+  // token
+  const int threads = T >= 128 ? 256 : 64;
+  const int chunks = (H + threads * 8 - 1) / (threads * 8);
+  SYM_REQUIRE(chunks <= 65535, SYM_ERR_UNSUPPORTED, "moe_unpermute_combine: H=%d too large", H);
+  const dim3 grid(T, chunks), block(threads);
   if (y_bf16)
-    hipLaunchKernelGGL(moe_combine_kernel<uint16_t>, dim3(T), dim3(256), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(moe_combine_kernel<uint16_t>, grid, block, 0, (hipStream_t)stream,
                        (const uint16_t*)y, inv_perm, topk_w, top_k, H, shared_row0, residual,
                        (uint16_t*)out);
   else
-    hipLaunchKernelGGL(moe_combine_kernel<float>, dim3(T), dim3(256), 0, (hipStream_t)stream,
+    hipLaunchKernelGGL(moe_combine_kernel<float>, grid, block, 0, (hipStream_t)stream,
                        (const float*)y, inv_perm, topk_w, top_k, H, shared_row0, residual,
                        (uint16_t*)out);
   return sym_host::check_launch("moe_combine_kernel");

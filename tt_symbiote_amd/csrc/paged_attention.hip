@@ -598,13 +598,13 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
 // one split per lane and broadcast. The partial outputs of the first kMergeBatch splits do not
 // depend on the weights: they are loaded together with the (max, sum) pairs, right after the
 // sequence length, so that a merge of up to kMergeBatch splits waits for two round trips.
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(
+__global__ __launch_bounds__(64) void paged_decode_merge_kernel(
     const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
     const int32_t* __restrict__ positions, int B, int Hq, int max_context, int max_splits,
     int split_tokens, uint16_t* __restrict__ out) {
   constexpr int D = kHeadDim;
   const int lane = threadIdx.x & 63;
-  const int idx = blockIdx.x * 4 + (threadIdx.x >> 6);  // b * Hq + head
+  const int idx = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // b * Hq + head
   if (idx >= B * Hq) return;
   const int ctx = min(positions[idx / Hq] + 1, max_context);
   const int nsplit = ctx <= 0 ? 0 : (ctx + split_tokens - 1) / split_tokens;
@@ -1384,9 +1384,9 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
 #undef SYM_LAUNCH_DECODE
   rc = sym_host::check_launch(fp8 ? "paged_decode_fp8_kernel" : "paged_decode_kernel");
   if (rc || max_splits == 1) return rc;
-  hipLaunchKernelGGL(paged_decode_merge_kernel, dim3((B * Hq + 3) / 4), dim3(256), 0, s, ws_o,
-                     ws_ml, positions, B, Hq, max_context, max_splits, split_tokens,
-                     (uint16_t*)out);
+  // one wave per workgroup: the (sequence, head) merges spread over as many CUs as possible
+  hipLaunchKernelGGL(paged_decode_merge_kernel, dim3(B * Hq), dim3(64), 0, s, ws_o, ws_ml,
+                     positions, B, Hq, max_context, max_splits, split_tokens, (uint16_t*)out);
   return sym_host::check_launch("paged_decode_merge_kernel");
 }
 
