@@ -269,7 +269,8 @@ int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E, fl
  *   w - hi, lo = w - hi - mid); x [T, H] bf16;
  *   parts [3, T, E] fp32: parts[z] = x . plane_z^T (each product exact in fp32), summed
  *   (parts[0] + parts[1]) + parts[2] by sym_moe_route_permute (n_logit_parts = 3).
- * H % 32 == 0, E % 16 == 0.
+ * H % 64 == 0, E % 16 == 0; x, w_planes and parts 16-byte aligned, x [T, H] and one plane
+ * under 4 GB.
  */
 int sym_moe_router_logits_split(const void* x, const void* w_planes, int T, int H, int E,
                                 float* parts, void* stream);
@@ -365,15 +366,18 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
                      const float* s_down, float* y, void* stream);
 
 /* ---------------------------------------------------------------------------------------
- * Tiled GEMMs for prefill-size batches (MFMA-bound; 128 x 256 output tiles).
+ * Tiled GEMMs for prefill-size batches (MFMA-bound; 256 x 256 output tiles, 128 x 256 for the
+ * grouped down projection).
  * sym_gemm_bf16: out[M, N] = a[M, K] . w[N, K]^T (+ bias[N] bf16) (+ residual[M, N] fp32),
  *   bf16 out, or fp32 when out_fp32 != 0. Replaces the QKV / dense projections at sequence length
- *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 16 == 0, K % 32 == 0.
+ *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 16 == 0, K % 64 == 0; a, w, out and
+ *   residual 16-byte aligned, bias 8-byte aligned; a and w each under 4 GB.
  * sym_moe_gate_up_tiled / sym_moe_down_tiled: the grouped expert GEMMs of sym_moe_gate_up /
  *   sym_moe_down (same arguments and results; TTNNExperts.forward, ttnn_moe.py:1250-1289) for
  *   segments of many rows; rows = total rows of the segment list (T*top_k + T with the shared
  *   expert). y is fp32, or bf16 when y_bf16 != 0 (half the bytes written here and read back by
- *   sym_moe_unpermute_combine). H % 32 == 0, I % 32 == 0.
+ *   sym_moe_unpermute_combine). H % 64 == 0, I % 64 == 0; x / h, the weights and h / y
+ *   16-byte aligned; x, h and one expert's weights each under 4 GB.
  */
 int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
                   int N, int K, void* out, int out_fp32, void* stream);

@@ -5,52 +5,43 @@
 // sequence length > 1, and the expert sparse_matmuls of TTNNExperts.forward
 // (ttnn_moe.py:1250-1289) with the shared expert (ttnn_moe.py:656-675), for prefill batches.
 //
-// Design (gfx950): a workgroup of 8 waves computes a 128 x 256 output tile; wave w owns the
-// 64 x 64 block (rows 64*(w/4), columns 64*(w%4)) as 4 x 4 v_mfma_f32_16x16x32_bf16 tiles. The
-// K loop moves 32 columns per step through a 3-stage LDS ring (24 KB per stage, 72 KB, so two
-// workgroups share a CU and one's barrier waits are covered by the other's MFMAs): the operand
-// tiles go from global memory straight into LDS (global_load_lds_dwordx4, no register staging),
-// two steps ahead of the MFMAs, with one barrier per step; a step's fragment reads are all
-// issued before its MFMAs. A wave-wide LDS-DMA instruction writes 1 KB = 16 rows of 32 bf16
-// contiguously (lane l -> row l/4, 16-byte slot l%4), so each lane fetches the global chunk
-// (l%4) ^ swz(row) with swz(r) = (r/2) % 4: chunk c of row r sits in slot c ^ swz(r), and the 16
-// rows of an MFMA fragment read (one chunk each) fall in distinct banks. (A 64-wide step with
-// 144 KB of LDS, one workgroup per CU, measured 10% slower on the dense projections.)
+// Design (gfx950). What bounds these kernels was measured, not assumed: a wave-wide load of
+// 16 rows x 64 bytes (a 32-column step of K-major rows) reaches ~30 B/clk per CU from L2, one of
+// 8 rows x 128 bytes ~50 B/clk, while LDS reads (~190 B/clk) and back-to-back MFMAs (94% of
+// peak) have room; and the chip clocks down to 1.5-2.1 GHz under these kernels. Two tile shapes:
+//   gemm_tile_kernel (dense projections, router logits, grouped gate/up): 256 x 256 tiles, one
+//     workgroup of 8 waves per CU, each wave a 64 x 128 block (4 x 8 v_mfma_f32_16x16x32_bf16
+//     tiles). The K loop moves 64 columns per step (128-byte rows: whole cache lines) through two
+//     64 KB LDS stages; each step is computed in two 32-column halves whose fragment reads
+//     overlap the other half's MFMAs, with one barrier per step.
+//   gemm_tile128_kernel (grouped down projection, K = I = 512: few steps per tile): 128 x 256
+//     tiles, two workgroups of 8 waves per CU, each wave a 64 x 64 block; 32 columns per step
+//     through a 3-stage 72 KB ring. The second workgroup covers a tile's prologue (segment
+//     lookup, first loads) and epilogue, which a one-workgroup shape leaves bare at 16 steps.
+// Operand tiles go from global memory straight into LDS (global_load_lds_dwordx4, no register
+// staging). A wave-wide LDS-DMA instruction writes 1 KB contiguously: lane l takes row l / c,
+// 16-byte slot l % c (c = chunks per row), fetching global chunk (l % c) ^ swz(row), so that
+// chunk j of row r sits in slot j ^ swz(r) and the rows of an MFMA fragment read fall in
+// distinct banks. Workgroups are ordered so that each XCD's L2 sees a contiguous run of tiles.
+// The MFMAs compute transposed 16 x 16 tiles, so a lane ends with 4 consecutive columns of one
+// row and the epilogue writes 8 (bf16) or 16 (fp32) bytes per lane.
 //   DENSE:   out[M, N] = A[M, K] . W[N, K]^T (+ bias) (+ residual fp32), bf16 or fp32 out.
 //   GATE_UP: rows of a segment gather x[sorted_tokens[row]]; the B tile holds 128 gate rows and
-//            the matching 128 up rows of the expert, so each wave's block pairs 32 gate with 32
+//            the matching 128 up rows of the expert, so each wave's block pairs 64 gate with 64
 //            up columns and the epilogue writes h = silu(gate) * up (bf16).
 //   DOWN:    rows of a segment are h rows (contiguous); y = h . W_down^T (fp32 or bf16).
 // Rows past a tile's valid rows and columns past N repeat the last row / column in the loads
-// (always in bounds) and are not stored.
+// (always in bounds) and are not stored; in the 256-row tiles, 64-row bands wholly past the
+// valid rows skip their MFMAs (and their A loads).
 // Grouped modes: the workgroup's row tile is found from the device-side segment list (each
-// segment owns ceil(count / 128) consecutive tiles of the grid's y range); workgroups past the
-// last tile exit.
+// segment owns ceil(count / tile rows) consecutive row tiles); workgroups past the last tile
+// exit.
+#include <type_traits>
+
 #include "common.h"
 
 namespace sym {
 
-constexpr int kTK = 32;  // 72 KB of LDS: two workgroups per CU (64: 144 KB, one; 10% slower)
-constexpr int kTM = 128, kTN = 256;
-constexpr int kWavesN = 4;  // waves along N (2 along M, 64 rows each)
-constexpr int kTileWaves = 2 * kWavesN;
-constexpr int kTileThreads = 64 * kTileWaves;
-constexpr int kWN = kTN / kWavesN;  // output columns per wave (B rows of its fragments)
-constexpr int kNJ = kWN / 16;       // 16-column MFMA tiles per wave
-constexpr int kAStage = kTM * kTK;  // bf16 elements of one A stage (16 KB at kTK = 64)
-constexpr int kBStage = kTN * kTK;  // bf16 elements of one B stage (32 KB)
-constexpr int kStage = kAStage + kBStage;
-constexpr int kDmaPerStep = (kAStage + kBStage) * 2 / 1024 / kTileWaves;  // per wave
-constexpr int kChunksPerRow = kTK / 8;          // 16-byte chunks per LDS row
-constexpr int kRowsPerDma = 64 / kChunksPerRow;  // rows one wave-wide LDS-DMA instruction fills
-static_assert(kTK == 32 || kTK == 64, "tile K");
-
-// LDS slot of chunk c in row r: c ^ swz(r), chosen so that the 16 rows of a fragment read (one
-// chunk each) fall in distinct banks: 8 chunks per 128-byte row -> r % 8; 4 chunks per 64-byte
-// row (two rows per 128 bytes) -> (r / 2) % 4.
-__device__ __forceinline__ int tile_swz(int r) {
-  return kChunksPerRow == 8 ? (r & 7) : ((r >> 1) & 3);
-}
 constexpr int kMaxGemmSegments = 4096;  // grid bound on segments (y range)
 
 enum TileMode { kDense = 0, kGateUp = 1, kDown = 2 };
@@ -74,31 +65,405 @@ struct TileArgs {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// 16 bytes per lane from global memory into LDS at base + 16 * lane (base wave-uniform, in M0).
-// Written as asm so that the compiler does not add its own (conservative) waits for these LDS
-// writes: the kernel waits for them explicitly (SYM_TILE_SYNC) before the barrier that
-// publishes a stage.
+// 16 bytes per lane from global memory (base + 32-bit byte offset) into LDS at lds_base + 16 *
+// lane (lds_base wave-uniform, in M0). Written as asm so that the compiler does not add its own
+// (conservative) waits for these LDS writes: the kernels wait for them explicitly
+// (SYM_TILE_SYNC) before the barrier that publishes a stage.
 // (M0 is written here only; no other instruction of these kernels reads it.)
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const uint16_t* g, const uint16_t* lds_base) {
-  const uint32_t lds = (uint32_t)(uintptr_t)lds_base;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(lds), "v"(g)
+// base and lds_base are wave-uniform by construction; readfirstlane states it where the
+// compiler cannot prove it (values derived from lane shuffles), at no cost where it can.
+__device__ __forceinline__ void dma16(const uint16_t* base, uint32_t off,
+                                      const uint16_t* lds_base) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_base);
+  // (readfirstlane returns int: each half goes through uint32_t, so that the low half is not
+  // sign-extended into the high one)
+  const uint64_t g = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32));
+  const uint64_t gu = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
+               "s"((const uint16_t*)(uintptr_t)gu)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
-// Wait until at most N of this wave's vector-memory loads are outstanding (the LDS-DMA of the
-// later steps), then the workgroup barrier. The asm is a compiler memory barrier, so no LDS
-// access moves across it; a plain __syncthreads would also wait for every DMA in flight.
+// Wait until at most N of this wave's vector-memory loads are outstanding (the LDS-DMA of later
+// steps) and for this wave's LDS reads, then the workgroup barrier. The asm is a compiler memory
+// barrier, so no LDS access moves across it; a plain __syncthreads would also wait for every DMA
+// in flight.
 #define SYM_TILE_SYNC(N) \
   asm volatile("s_waitcnt vmcnt(" #N ")\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
+// Tile t of n for the workgroup with linear id lin, or -1. Workgroups are dispatched to the 8
+// XCDs round-robin by linear id (lin % 8), and each XCD has its own L2: XCD x takes the
+// contiguous range of tiles [x n / 8, (x + 1) n / 8) in dispatch order, so the column tiles of a
+// row tile (same A rows) and the row tiles of an expert (same weights) meet in one L2.
+__device__ __forceinline__ int xcd_tile(int lin, int n) {
+  const int x = lin & 7, j = lin >> 3;
+  const int q = n >> 3, r = n & 7;
+  if (j >= q + (x < r ? 1 : 0)) return -1;
+  return x * q + min(x, r) + j;
+}
+
+// The tile of workgroup lin (nx column tiles per row tile). DENSE: row tiles of TM rows of
+// p.M; grouped modes: each segment owns ceil(seg_count / TM) consecutive row tiles, found by
+// every wave scanning the segment list (prefix sums by lane shuffles; no LDS, no barrier, all
+// waves agree): once for the number of row tiles, then up to the segment holding the row tile.
+// The counts are loaded 512 segments at a time (8 loads in flight per lane) and kept in
+// registers for the second pass when there are at most 512 segments. Returns false past the
+// last tile (the grouped grids are sized for the worst case). Results are wave-uniform.
+struct TileLoc {
+  int row0, rows, e, ct, z;  // first row, valid rows, expert, column tile, weight plane
+};
+template <int MODE, int TM>
+__device__ __forceinline__ bool locate_tile(const TileArgs& p, int lane, TileLoc& loc) {
+  const int nx = gridDim.x;
+  const int lin = (blockIdx.z * gridDim.y + blockIdx.y) * nx + blockIdx.x;
+  loc.e = 0;
+  loc.z = 0;
+  if constexpr (MODE == kDense) {
+    const int nxy = nx * gridDim.y;
+    const int t = xcd_tile(lin, nxy * gridDim.z);  // the grid holds exactly the tiles
+    loc.z = t / nxy;
+    const int gy = (t - loc.z * nxy) / nx;
+    loc.ct = t - loc.z * nxy - gy * nx;
+    loc.row0 = gy * TM;
+    loc.rows = min(TM, p.M - loc.row0);
+    return true;
+  } else {
+    constexpr int kBatch = 8;  // 64-segment chunks per batch
+    const int nseg = p.n_segments[0];
+    const int nbatch = (nseg + 64 * kBatch - 1) / (64 * kBatch);
+    int nt[kBatch];
+    auto load = [&](int b) {
+#pragma unroll
+      for (int c = 0; c < kBatch; ++c) {
+        const int s = (b * kBatch + c) * 64 + lane;
+        nt[c] = s < nseg ? (p.seg_count[s] + TM - 1) / TM : 0;
+      }
+    };
+    int ntile = 0;
+    for (int b = 0; b < nbatch; ++b) {
+      load(b);
+#pragma unroll
+      for (int c = 0; c < kBatch; ++c) ntile += nt[c];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ntile += __shfl_xor(ntile, off);
+    const int t = xcd_tile(lin, ntile * nx);
+    if (t < 0) return false;
+    const int g = t / nx;
+    loc.ct = t - g * nx;
+    int seg = -1, start = 0, run = 0;
+    for (int b = 0; b < nbatch && seg < 0; ++b) {
+      if (nbatch > 1) load(b);  // one batch: the counts are still in registers
+#pragma unroll
+      for (int c = 0; c < kBatch; ++c) {
+        int x = nt[c];
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+          const int y = __shfl_up(x, off);
+          if (lane >= off) x += y;
+        }
+        const int s0 = run + x - nt[c];
+        const unsigned long long hit = __ballot(nt[c] > 0 && s0 <= g && g < s0 + nt[c]);
+        if (seg < 0 && hit) {
+          const int l = __ffsll((long long)hit) - 1;
+          seg = (b * kBatch + c) * 64 + l;
+          start = __shfl(s0, l);
+        }
+        run += __shfl(x, 63);
+      }
+    }
+    if (seg < 0) return false;  // not reached: g < ntile
+    // wave-uniform (the compiler cannot see it through the lane shuffles)
+    seg = __builtin_amdgcn_readfirstlane(seg);
+    const int rt = g - __builtin_amdgcn_readfirstlane(start);
+    loc.e = __builtin_amdgcn_readfirstlane(p.seg_expert[seg]);
+    loc.row0 = __builtin_amdgcn_readfirstlane(p.seg_offset[seg] + rt * TM);
+    loc.rows = __builtin_amdgcn_readfirstlane(min(TM, p.seg_count[seg] - rt * TM));
+    loc.ct = __builtin_amdgcn_readfirstlane(loc.ct);
+    return true;
+  }
+}
+
+// Output-plane and weight-matrix bases of a tile: DENSE plane z; GATE_UP / DOWN expert e.
 template <int MODE>
-__global__ __launch_bounds__(kTileThreads) __attribute__((amdgpu_waves_per_eu(kTileWaves / 4 * 2)))
+__device__ __forceinline__ const uint16_t* tile_weights(TileArgs& p, const TileLoc& loc) {
+  if constexpr (MODE == kDense) {
+    if (p.out_f32) p.out_f32 += loc.z * p.out_zstride;
+    else p.out_bf16 += loc.z * p.out_zstride;
+    return p.w + loc.z * p.w_zstride;
+  } else if constexpr (MODE == kGateUp) {
+    return p.w + (size_t)loc.e * 2 * p.N * p.K;
+  } else {
+    return p.w + (size_t)loc.e * p.N * p.K;
+  }
+}
+
+// Byte offset of B row br (0 .. TN - 1) of column tile ct within the tile's weight matrix.
+// GATE_UP: TN / 2 gate rows then the matching TN / 2 up rows. Rows past N repeat the last one.
+template <int MODE, int TN>
+__device__ __forceinline__ uint32_t b_row_offset(const TileArgs& p, int ct, int br) {
+  uint32_t brow;
+  if constexpr (MODE == kGateUp) {
+    const int col = min(ct * (TN / 2) + (br % (TN / 2)), p.N - 1);
+    brow = (uint32_t)(br < TN / 2 ? col : p.N + col);
+  } else {
+    brow = (uint32_t)min(ct * TN + br, p.N - 1);
+  }
+  return brow * (uint32_t)p.K * 2u;
+}
+
+// Byte offset of A row r (< rows) of the tile: GATE_UP gathers x[sorted_tokens[row]].
+template <int MODE>
+__device__ __forceinline__ uint32_t a_row_offset(const TileArgs& p, const TileLoc& loc, int r) {
+  uint32_t arow;
+  if constexpr (MODE == kGateUp) arow = (uint32_t)p.sorted_tokens[loc.row0 + r];
+  else arow = (uint32_t)(loc.row0 + r);
+  return arow * (uint32_t)p.K * 2u;
+}
+
+// Epilogue of one wave's 64 x (16 NJ) block. The MFMAs take the B fragment as their first
+// operand and A as their second, i.e. compute transposed 16 x 16 tiles: lane l holds row l%16,
+// columns 4*(l/16) .. +3 of each, stored as one 8-byte (bf16) or 16-byte (fp32) write.
+// GATE_UP: tiles j < NJ/2 are gate columns col0 + 16 j .., tiles j + NJ/2 the matching up
+// columns; h = silu(gate) * up. Otherwise tile j is columns col0 + 16 j ..
+template <int MODE, int NJ>
+__device__ __forceinline__ void store_block(const TileArgs& p, const floatx4 (&acc)[4][NJ],
+                                            const TileLoc& loc, int rbase, int col0, int lane) {
+  const int r16 = lane & 15, kq = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = rbase + i * 16 + r16;
+    if (r >= loc.rows) continue;
+    const size_t orow = (size_t)(loc.row0 + r);
+    if constexpr (MODE == kGateUp) {
+#pragma unroll
+      for (int j = 0; j < NJ / 2; ++j) {
+        const int col = col0 + j * 16 + kq * 4;
+        if (col >= p.N) continue;  // N % 16 == 0: the 4 columns are all valid or all not
+        float h[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float g = acc[i][j][q], u = acc[i][j + NJ / 2][q];
+          h[q] = g / (1.0f + expf(-g)) * u;
+        }
+        *reinterpret_cast<uint2*>(p.out_bf16 + orow * p.N + col) =
+            make_uint2(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]));
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const int col = col0 + j * 16 + kq * 4;
+        if (col >= p.N) continue;
+        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
+        if constexpr (MODE == kDense) {
+          if (p.bias) {
+            const uint2 b = *reinterpret_cast<const uint2*>(p.bias + col);
+            v[0] += bf16_lo(b.x); v[1] += bf16_hi(b.x); v[2] += bf16_lo(b.y); v[3] += bf16_hi(b.y);
+          }
+          if (p.residual) {
+            const float4 rr = *reinterpret_cast<const float4*>(p.residual + orow * p.N + col);
+            v[0] += rr.x; v[1] += rr.y; v[2] += rr.z; v[3] += rr.w;
+          }
+        }
+        if (p.out_f32)
+          *reinterpret_cast<float4*>(p.out_f32 + orow * p.N + col) =
+              make_float4(v[0], v[1], v[2], v[3]);
+        else
+          *reinterpret_cast<uint2*>(p.out_bf16 + orow * p.N + col) =
+              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+      }
+    }
+  }
+}
+
+// ================================================================================================
+// 256 x 256 tiles (dense projections, router logits, grouped gate/up): 8 waves of 64 x 128, one
+// workgroup per CU, 64-column steps through two 64 KB LDS stages. Per step a CU moves 64 KB from
+// L2 in whole 128-byte lines for 4 M MACs.
+// ================================================================================================
+namespace big {
+constexpr int kTM = 256, kTN = 256, kTK = 64;
+constexpr int kWavesN = 2, kWaves = 8, kThreads = 512;
+constexpr int kWC = kTN / kWavesN, kNJ = kWC / 16;  // 128 columns (8 MFMA tiles) per wave
+constexpr int kAStage = kTM * kTK, kBStage = kTN * kTK, kStage = kAStage + kBStage;  // bf16
+constexpr int kRowsPerDma = 8;  // one wave-wide LDS-DMA instruction: 8 rows x 128 bytes
+constexpr int kARows = kTM / kWaves, kBRows = kTN / kWaves;  // rows DMA'd per wave and step
+constexpr int kADma = kARows / kRowsPerDma, kBDma = kBRows / kRowsPerDma;  // 4 + 4
+static_assert(kADma == 4 && kBDma == 4, "the prologue wait counts");
+// LDS slot of 16-byte chunk c (of 8) in row r: c ^ (r % 8), so that the 8 rows of a fragment
+// read that share a chunk index fall in distinct banks.
+__device__ __forceinline__ int swz(int r) { return r & 7; }
+}  // namespace big
+
+template <int MODE>
+__global__ __launch_bounds__(big::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_tile_kernel(TileArgs p) {
-  // stage s = [A (16 KB) | B (32 KB)] at smem + s * kStage: one base address per stage keeps every
-  // fragment read of the stage within the 64 KB immediate offset of an LDS instruction
+  using namespace big;
+  // stage s = [A | B] at smem + s * kStage (64 KB each): every fragment read of a stage is
+  // within the 64 KB immediate offset of an LDS instruction from the stage base
+  __shared__ __align__(1024) uint16_t smem[2 * kStage];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int r16 = lane & 15, kq = lane >> 4;
+  const int K = p.K;
+
+  TileLoc loc;
+  if (!locate_tile<MODE, kTM>(p, lane, loc)) return;
+  const uint16_t* wbase = tile_weights<MODE>(p, loc);
+
+  // ---- LDS-DMA sources: this wave fills A rows kARows w .. and B rows kBRows w .. of every
+  // stage; lane l takes row + l / 8, slot l % 8, i.e. global chunk slot ^ swz(row). A rows at
+  // or past `rows` in groups of kARows are not loaded (their wave skips those instructions and
+  // waits for fewer loads; no wave reads those LDS rows for a stored output). Sources are byte
+  // offsets from p.a (the host checks that A fits in 4 GB) and from the tile's weight matrix
+  // (one expert's, in the grouped modes; the host checks that one fits in 4 GB).
+  const int lr = lane >> 3;
+  const uint32_t chunk_b = ((lane & 7) ^ swz(lr)) * 16;  // swz(row) == swz(lr)
+  const bool a_on = wave * kARows < loc.rows;
+  uint32_t a_off[kADma], b_off[kBDma];
+#pragma unroll
+  for (int i = 0; i < kADma; ++i)
+    a_off[i] = a_row_offset<MODE>(p, loc, min(wave * kARows + lr + kRowsPerDma * i, loc.rows - 1)) +
+               chunk_b;
+#pragma unroll
+  for (int i = 0; i < kBDma; ++i)
+    b_off[i] = b_row_offset<MODE, kTN>(p, loc.ct, wave * kBRows + lr + kRowsPerDma * i) + chunk_b;
+  const int a_dst = wave * kARows * kTK;  // element offset of this wave's first A row
+  const int b_dst = kAStage + wave * kBRows * kTK;
+
+  auto issue = [&](int kt, uint16_t* stage) {
+    const uint32_t k = (uint32_t)kt * (kTK * 2);
+    if (a_on) {
+#pragma unroll
+      for (int i = 0; i < kADma; ++i) dma16(p.a, a_off[i] + k, stage + a_dst + i * 512);
+    }
+#pragma unroll
+    for (int i = 0; i < kBDma; ++i) dma16(wbase, b_off[i] + k, stage + b_dst + i * 512);
+  };
+
+  // fragment rows of this wave: A rows wm*64 + 16i + r16; B rows b_row(j) + r16 per column
+  // tile j. GATE_UP: the first kNJ/2 tiles are gate columns wn*kWC/2 .., the rest the matching
+  // up columns (B rows 128 + ...). Lane l reads chunk h*4 + l/16 of its row for the 32-column
+  // half h of a step. One per-lane base per operand and half; tile offsets are constants.
+  const int a_frag0 = (wm * 64 + r16) * kTK;
+  const int b_frag0 = kAStage + ((MODE == kGateUp ? wn * (kWC / 2) : wn * kWC) + r16) * kTK;
+  const int slot0 = (kq ^ swz(r16)) * 8, slot1 = ((4 + kq) ^ swz(r16)) * 8;
+  auto b_row = [](int j) {
+    return MODE == kGateUp ? (j < kNJ / 2 ? 0 : kTN / 2) + (j % (kNJ / 2)) * 16 : j * 16;
+  };
+  // a wave whose 64 rows are all past `rows` computes nothing (it still loads and syncs)
+  const bool m_on = wm * 64 < loc.rows;
+
+  floatx4 acc[4][kNJ];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  // fragments of one 32-column half: [0..3] A rows, [4..] B columns
+  constexpr int kNF = 4 + kNJ;
+  auto read_frags = [&](const uint16_t* stage, int slot, u32x4 (&f)[kNF]) {
+    const uint16_t* sA = stage + a_frag0 + slot;
+    const uint16_t* sB = stage + b_frag0 + slot;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = *reinterpret_cast<const u32x4*>(sA + i * 16 * kTK);
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) f[4 + j] = *reinterpret_cast<const u32x4*>(sB + b_row(j) * kTK);
+  };
+  auto mfmas = [&](const u32x4 (&f)[kNF]) {  // transposed tiles (B first), see store_block
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, f[4 + j]), __builtin_bit_cast(bf16x8, f[i]), acc[i][j],
+            0, 0, 0);
+  };
+  // one LDS read between every two MFMAs (the reads feed the other half's MFMAs)
+  auto interleave = [&]() {
+#pragma unroll
+    for (int i = 0; i < kNF; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+  };
+
+  // Step kt (64 columns) uses stage kt % 2 and is computed in two halves: the MFMAs of half 0
+  // run while half 1's fragments are read; then wait for step kt + 1's stage and barrier (every
+  // wave has read all of step kt, so its stage is free), issue step kt + 2 into it, and run the
+  // MFMAs of half 1 while half 0 of step kt + 1 is read.
+  const int nk = K / kTK;
+  auto stage_of = [&](int kt) { return smem + (kt & 1) * kStage; };
+  auto loop = [&](auto with_mfma) {
+    constexpr bool kMfma = decltype(with_mfma)::value;
+    u32x4 fa[kNF], fb[kNF];
+    issue(0, smem);
+    if (nk > 1) {
+      issue(1, smem + kStage);
+      if (a_on) SYM_TILE_SYNC(8);  // step 0 in; step 1 (this wave's 8 or 4 loads) may fly
+      else SYM_TILE_SYNC(4);
+    } else {
+      SYM_TILE_SYNC(0);
+    }
+    if constexpr (kMfma) read_frags(smem, slot0, fa);
+    for (int kt = 0; kt < nk - 1; ++kt) {
+      if constexpr (kMfma) {
+        read_frags(stage_of(kt), slot1, fb);
+        mfmas(fa);
+        interleave();
+      }
+      SYM_TILE_SYNC(0);
+      if (kt + 2 < nk) issue(kt + 2, smem + (kt & 1) * kStage);
+      if constexpr (kMfma) {
+        read_frags(stage_of(kt + 1), slot0, fa);
+        mfmas(fb);
+        interleave();
+      }
+    }
+    if constexpr (kMfma) {  // the last step
+      read_frags(stage_of(nk - 1), slot1, fb);
+      mfmas(fa);
+      mfmas(fb);
+    }
+  };
+  if (m_on) loop(std::true_type{});
+  else loop(std::false_type{});
+  if (!m_on) return;
+
+  const int col0 = MODE == kGateUp ? loc.ct * (kTN / 2) + wn * (kWC / 2) : loc.ct * kTN + wn * kWC;
+  store_block<MODE, kNJ>(p, acc, loc, wm * 64, col0, lane);
+}
+
+// ================================================================================================
+// 128 x 256 tiles (grouped down projection, K = I is short): 8 waves of 64 x 64, two workgroups
+// per CU (while one waits at a barrier or on its prologue, the other computes), 32-column steps
+// through a 3-stage 72 KB LDS ring; a step's fragment reads are all issued before its MFMAs.
+// ================================================================================================
+namespace mid {
+constexpr int kTM = 128, kTN = 256, kTK = 32;
+constexpr int kWavesN = 4, kWaves = 8, kThreads = 512;
+constexpr int kWC = kTN / kWavesN, kNJ = kWC / 16;  // 64 columns (4 MFMA tiles) per wave
+constexpr int kAStage = kTM * kTK, kBStage = kTN * kTK, kStage = kAStage + kBStage;  // bf16
+constexpr int kRowsPerDma = 16;  // one wave-wide LDS-DMA instruction: 16 rows x 64 bytes
+constexpr int kARows = kTM / kWaves, kBRows = kTN / kWaves;
+constexpr int kADma = kARows / kRowsPerDma, kBDma = kBRows / kRowsPerDma;  // 1 + 2
+static_assert(kADma == 1 && kBDma == 2, "the wait counts");
+// LDS slot of 16-byte chunk c (of 4) in row r: c ^ ((r / 2) % 4): the 16 rows of a fragment
+// read (one chunk each, two rows per 128 bytes) fall in distinct banks.
+__device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
+}  // namespace mid
+
+template <int MODE>
+__global__ __launch_bounds__(mid::kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void gemm_tile128_kernel(TileArgs p) {
+  using namespace mid;
   __shared__ __align__(1024) uint16_t smem[3 * kStage];
 
   const int tid = threadIdx.x;
@@ -107,104 +472,34 @@ void gemm_tile_kernel(TileArgs p) {
   const int r16 = lane & 15, kq = lane >> 4;
   const int K = p.K;
 
-  // ---- locate the tile ----
-  int row0, rows, e = 0;  // first output row, valid rows in the tile, expert
-  const int ct = blockIdx.x, gy = blockIdx.y;
-  if constexpr (MODE == kDense) {
-    row0 = gy * kTM;
-    rows = min(kTM, p.M - row0);
-    p.w += blockIdx.z * p.w_zstride;
-    if (p.out_f32) p.out_f32 += blockIdx.z * p.out_zstride;
-    else p.out_bf16 += blockIdx.z * p.out_zstride;
-  } else {
-    // Every wave scans the segment list 64 segments at a time (prefix sum by lane shuffles)
-    // and stops at the one holding tile g: no LDS and no barrier, and all waves agree.
-    const int nseg = p.n_segments[0];
-    const int g = gy;
-    int seg = -1, start = 0, run = 0;
-    for (int s0 = 0; s0 < nseg; s0 += 64) {
-      const int s = s0 + lane;
-      const int nt = s < nseg ? (p.seg_count[s] + kTM - 1) / kTM : 0;
-      int x = nt;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const int y = __shfl_up(x, off);
-        if (lane >= off) x += y;
-      }
-      const int st = run + x - nt;
-      const unsigned long long hit = __ballot(nt > 0 && st <= g && g < st + nt);
-      if (hit) {
-        const int l = __ffsll((long long)hit) - 1;
-        seg = s0 + l;
-        start = __shfl(st, l);
-        break;
-      }
-      run += __shfl(x, 63);
-    }
-    if (seg < 0) return;  // past the last tile (the grid is sized for the worst case)
-    const int rt = g - start;
-    e = p.seg_expert[seg];
-    row0 = p.seg_offset[seg] + rt * kTM;
-    rows = min(kTM, p.seg_count[seg] - rt * kTM);
-  }
+  TileLoc loc;
+  if (!locate_tile<MODE, kTM>(p, lane, loc)) return;
+  const uint16_t* wbase = tile_weights<MODE>(p, loc);
 
-  // ---- LDS-DMA sources: this wave fills A rows 16w .. 16w+15 and B rows 32w .. 32w+31 of
-  // every stage; lane l takes row + l / kChunksPerRow, slot l % kChunksPerRow, i.e. global chunk
-  // slot ^ swz(row)
-  constexpr int kARows = kTM / kTileWaves, kBRows = kTN / kTileWaves;  // rows filled per wave
-  constexpr int kADma = kARows / kRowsPerDma, kBDma = kBRows / kRowsPerDma;
-  const int lr = lane / kChunksPerRow;
-  const int a_row_l = wave * kARows + lr;   // + kRowsPerDma * i
-  const int b_row_l = wave * kBRows + lr;
-  const int chunk = ((lane % kChunksPerRow) ^ tile_swz(lr)) * 8;  // swz(row) == swz(lr)
-  const uint16_t* a_src[kADma];
-  const uint16_t* b_src[kBDma];
+  // LDS-DMA sources as in gemm_tile_kernel, 16 rows x 64 bytes per instruction (every wave
+  // loads its rows: the wait counts are fixed)
+  const int lr = lane >> 2;
+  const uint32_t chunk_b = ((lane & 3) ^ swz(lr)) * 16;
+  const uint32_t a_off = a_row_offset<MODE>(p, loc, min(wave * kARows + lr, loc.rows - 1)) + chunk_b;
+  uint32_t b_off[kBDma];
 #pragma unroll
-  for (int i = 0; i < kADma; ++i) {
-    const int r = min(a_row_l + kRowsPerDma * i, rows - 1);
-    size_t arow;
-    if constexpr (MODE == kGateUp) arow = (size_t)p.sorted_tokens[row0 + r];
-    else arow = (size_t)(row0 + r);
-    a_src[i] = p.a + arow * K + chunk;
-  }
-#pragma unroll
-  for (int i = 0; i < kBDma; ++i) {
-    const int br = b_row_l + kRowsPerDma * i;  // B tile row 0..255
-    size_t brow;
-    if constexpr (MODE == kGateUp) {
-      // 128 gate rows then the matching 128 up rows of expert e
-      const int col = min(ct * 128 + (br & 127), p.N - 1);
-      brow = (size_t)e * 2 * p.N + (br < 128 ? col : p.N + col);
-    } else if constexpr (MODE == kDown) {
-      brow = (size_t)e * p.N + min(ct * kTN + br, p.N - 1);
-    } else {
-      brow = (size_t)min(ct * kTN + br, p.N - 1);
-    }
-    b_src[i] = p.w + brow * K + chunk;
-  }
-  const int a_dst = wave * kARows * kTK;  // element offset of this wave's first A row in a stage
-  const int b_dst = wave * kBRows * kTK;
-
+  for (int i = 0; i < kBDma; ++i)
+    b_off[i] = b_row_offset<MODE, kTN>(p, loc.ct, wave * kBRows + lr + kRowsPerDma * i) + chunk_b;
+  const int a_dst = wave * kARows * kTK;
+  const int b_dst = kAStage + wave * kBRows * kTK;
   auto issue = [&](int kt, uint16_t* stage) {
-    const int k = kt * kTK;
+    const uint32_t k = (uint32_t)kt * (kTK * 2);
+    dma16(p.a, a_off + k, stage + a_dst);
 #pragma unroll
-    for (int i = 0; i < kADma; ++i) dma16(a_src[i] + k, stage + a_dst + i * 512);
-#pragma unroll
-    for (int i = 0; i < kBDma; ++i) dma16(b_src[i] + k, stage + kAStage + b_dst + i * 512);
+    for (int i = 0; i < kBDma; ++i) dma16(wbase, b_off[i] + k, stage + b_dst + i * 512);
   };
 
-  // fragment rows of this wave: A rows wm*64 + 16i + r16; B rows per column tile j
-  // GATE_UP: the first kNJ/2 tiles are gate columns wn*kWN/2 .. +kWN/2, the rest the matching
-  // up columns (B rows 128 + ...)
-  int b_frag[kNJ];
-#pragma unroll
-  for (int j = 0; j < kNJ; ++j) {
-    if constexpr (MODE == kGateUp)
-      b_frag[j] = (j < kNJ / 2 ? 0 : 128) + wn * (kWN / 2) + (j % (kNJ / 2)) * 16 + r16;
-    else
-      b_frag[j] = wn * kWN + j * 16 + r16;
-  }
-  const int sw = tile_swz(r16);  // every fragment row r has swz(r) == swz(r16)
+  const int a_frag0 = (wm * 64 + r16) * kTK + (kq ^ swz(r16)) * 8;
+  const int b_frag0 = kAStage + ((MODE == kGateUp ? wn * (kWC / 2) : wn * kWC) + r16) * kTK +
+                      (kq ^ swz(r16)) * 8;
+  auto b_row = [](int j) {
+    return MODE == kGateUp ? (j < kNJ / 2 ? 0 : kTN / 2) + (j % (kNJ / 2)) * 16 : j * 16;
+  };
 
   floatx4 acc[4][kNJ];
 #pragma unroll
@@ -212,89 +507,53 @@ void gemm_tile_kernel(TileArgs p) {
 #pragma unroll
     for (int j = 0; j < kNJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  // all fragment reads of the step are issued before its MFMAs
   auto compute = [&](const uint16_t* stage) {
-    const uint16_t* sA = stage;
-    const uint16_t* sB = stage + kAStage;
-    u32x4 fa[2][4], fb[2][kNJ];
+    u32x4 fa[4], fb[kNJ];
 #pragma unroll
-    for (int kh = 0; kh < kTK / 32; ++kh) {
-      const int slot = ((kh * 4 + kq) ^ sw) * 8;
+    for (int i = 0; i < 4; ++i)
+      fa[i] = *reinterpret_cast<const u32x4*>(stage + a_frag0 + i * 16 * kTK);
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        fa[kh][i] = *reinterpret_cast<const u32x4*>(&sA[(wm * 64 + i * 16 + r16) * kTK + slot]);
-#pragma unroll
-      for (int j = 0; j < kNJ; ++j)
-        fb[kh][j] = *reinterpret_cast<const u32x4*>(&sB[b_frag[j] * kTK + slot]);
-    }
+    for (int j = 0; j < kNJ; ++j)
+      fb[j] = *reinterpret_cast<const u32x4*>(stage + b_frag0 + b_row(j) * kTK);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int kh = 0; kh < kTK / 32; ++kh)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < kNJ; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, fa[kh][i]), __builtin_bit_cast(bf16x8, fb[kh][j]),
-              acc[i][j], 0, 0, 0);
+      for (int j = 0; j < kNJ; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, fb[j]), __builtin_bit_cast(bf16x8, fa[i]), acc[i][j],
+            0, 0, 0);
   };
 
   // Step k: wait for its stage (the DMA of step k + 1 may still be in flight), barrier (every
   // wave is also done with step k - 1's stage), issue step k + 2 into that stage, MFMAs. Step k
   // uses stage k % 3.
-  static_assert(kDmaPerStep == 3 || kDmaPerStep == 6 || kDmaPerStep == 12, "SYM_TILE_SYNC count");
   const int nk = K / kTK;
   issue(0, smem);
   if (nk > 1) issue(1, smem + kStage);
   int cur = 0;  // stage of step kt (element offset)
   for (int kt = 0; kt < nk; ++kt) {
     if (kt + 1 >= nk) SYM_TILE_SYNC(0);
-    else if constexpr (kDmaPerStep == 12) SYM_TILE_SYNC(12);
-    else if constexpr (kDmaPerStep == 6) SYM_TILE_SYNC(6);
-    else SYM_TILE_SYNC(3);
+    else SYM_TILE_SYNC(3);  // step kt + 1's three loads may still fly
     const int nxt = cur == 0 ? 2 * kStage : cur - kStage;  // stage of step kt + 2
     if (kt + 2 < nk) issue(kt + 2, smem + nxt);
     compute(smem + cur);
     cur = cur == 2 * kStage ? 0 : cur + kStage;
   }
 
-  // ---- epilogue: lane holds rows 4*(l/16)+q, column l%16 of each 16 x 16 tile ----
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int r = wm * 64 + i * 16 + kq * 4 + q;
-      if (r >= rows) continue;
-      const size_t orow = (size_t)(row0 + r);
-      if constexpr (MODE == kGateUp) {
-#pragma unroll
-        for (int j = 0; j < kNJ / 2; ++j) {
-          const int col = ct * 128 + wn * (kWN / 2) + j * 16 + r16;
-          if (col >= p.N) continue;
-          const float g = acc[i][j][q], u = acc[i][j + kNJ / 2][q];
-          p.out_bf16[orow * p.N + col] = f32_to_bf16(g / (1.0f + expf(-g)) * u);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < kNJ; ++j) {
-          const int col = ct * kTN + wn * kWN + j * 16 + r16;
-          if (col >= p.N) continue;
-          float v = acc[i][j][q];
-          if constexpr (MODE == kDense) {
-            if (p.bias) v += bf16_to_f32(p.bias[col]);
-            if (p.residual) v += p.residual[orow * p.N + col];
-          }
-          if (p.out_f32) p.out_f32[orow * p.N + col] = v;
-          else p.out_bf16[orow * p.N + col] = f32_to_bf16(v);
-        }
-      }
-    }
-  }
+  const int col0 = MODE == kGateUp ? loc.ct * (kTN / 2) + wn * (kWC / 2) : loc.ct * kTN + wn * kWC;
+  store_block<MODE, kNJ>(p, acc, loc, wm * 64, col0, lane);
 }
 
 }  // namespace sym
 
 using namespace sym;
+
+// The kernel addresses A and one weight matrix with 32-bit byte offsets.
+static bool fits_4g(long long rows, long long cols) { return rows * cols * 2 < (1ll << 32); }
+// Operands move in 16-byte pieces (A, W, fp32 outputs and residuals) and 8-byte pieces (bf16
+// outputs, bias).
+static bool aligned(const void* ptr, uintptr_t n) { return ((uintptr_t)ptr & (n - 1)) == 0; }
 
 extern "C" int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual,
                              int M, int N, int K, void* out, int out_fp32, void* stream) {
@@ -303,9 +562,17 @@ extern "C" int sym_gemm_bf16(const void* a, const void* w, const void* bias, con
   SYM_REQUIRE(a && w && out, SYM_ERR_INVALID, "gemm_bf16: null pointer argument");
   SYM_REQUIRE(N > 0 && N % 16 == 0, SYM_ERR_UNSUPPORTED,
               "gemm_bf16: N=%d must be a positive multiple of 16", N);
-  SYM_REQUIRE(K > 0 && K % kTK == 0, SYM_ERR_UNSUPPORTED,
-              "gemm_bf16: K=%d must be a positive multiple of %d", K, kTK);
-  SYM_REQUIRE((M + kTM - 1) / kTM <= 65535, SYM_ERR_UNSUPPORTED, "gemm_bf16: M=%d too large", M);
+  SYM_REQUIRE(K > 0 && K % big::kTK == 0, SYM_ERR_UNSUPPORTED,
+              "gemm_bf16: K=%d must be a positive multiple of %d", K, big::kTK);
+  namespace C = big;
+  SYM_REQUIRE((M + C::kTM - 1) / C::kTM <= 65535, SYM_ERR_UNSUPPORTED, "gemm_bf16: M=%d too large",
+              M);
+  SYM_REQUIRE(fits_4g(M, K) && fits_4g(N, K), SYM_ERR_UNSUPPORTED,
+              "gemm_bf16: a [%d, %d] or w [%d, %d] is 4 GB or more", M, K, N, K);
+  SYM_REQUIRE(aligned(a, 16) && aligned(w, 16) && aligned(out, 16) && aligned(residual, 16) &&
+                  aligned(bias, 8),
+              SYM_ERR_INVALID, "gemm_bf16: a, w, out and residual must be 16-byte aligned, bias "
+              "8-byte aligned");
   TileArgs p{};
   p.a = (const uint16_t*)a;
   p.w = (const uint16_t*)w;
@@ -317,8 +584,9 @@ extern "C" int sym_gemm_bf16(const void* a, const void* w, const void* bias, con
   p.out_bf16 = out_fp32 ? nullptr : (uint16_t*)out;
   p.out_f32 = out_fp32 ? (float*)out : nullptr;
   (void)hipGetLastError();
-  hipLaunchKernelGGL((gemm_tile_kernel<kDense>), dim3((N + kTN - 1) / kTN, (M + kTM - 1) / kTM),
-                     dim3(kTileThreads), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL((gemm_tile_kernel<kDense>),
+                     dim3((N + C::kTN - 1) / C::kTN, (M + C::kTM - 1) / C::kTM), dim3(C::kThreads),
+                     0, (hipStream_t)stream, p);
   return sym_host::check_launch("gemm_tile_kernel");
 }
 
@@ -334,10 +602,15 @@ extern "C" int sym_moe_router_logits_split(const void* x, const void* w_planes, 
               "moe_router_logits_split: null pointer argument");
   SYM_REQUIRE(E > 0 && E % 16 == 0, SYM_ERR_UNSUPPORTED,
               "moe_router_logits_split: E=%d must be a positive multiple of 16", E);
-  SYM_REQUIRE(H > 0 && H % kTK == 0, SYM_ERR_UNSUPPORTED,
-              "moe_router_logits_split: H=%d must be a positive multiple of %d", H, kTK);
-  SYM_REQUIRE((T + kTM - 1) / kTM <= 65535, SYM_ERR_UNSUPPORTED,
+  SYM_REQUIRE(H > 0 && H % big::kTK == 0, SYM_ERR_UNSUPPORTED,
+              "moe_router_logits_split: H=%d must be a positive multiple of %d", H, big::kTK);
+  namespace C = big;
+  SYM_REQUIRE((T + C::kTM - 1) / C::kTM <= 65535, SYM_ERR_UNSUPPORTED,
               "moe_router_logits_split: T=%d too large", T);
+  SYM_REQUIRE(fits_4g(T, H) && fits_4g(E, H), SYM_ERR_UNSUPPORTED,
+              "moe_router_logits_split: x [%d, %d] is 4 GB or more", T, H);
+  SYM_REQUIRE(aligned(x, 16) && aligned(w_planes, 16) && aligned(parts, 16), SYM_ERR_INVALID,
+              "moe_router_logits_split: x, w_planes and parts must be 16-byte aligned");
   TileArgs p{};
   p.a = (const uint16_t*)x;
   p.w = (const uint16_t*)w_planes;
@@ -348,20 +621,26 @@ extern "C" int sym_moe_router_logits_split(const void* x, const void* w_planes, 
   p.w_zstride = (long long)E * H;
   p.out_zstride = (long long)T * E;
   (void)hipGetLastError();
-  hipLaunchKernelGGL((gemm_tile_kernel<kDense>), dim3((E + kTN - 1) / kTN, (T + kTM - 1) / kTM, 3),
-                     dim3(kTileThreads), 0, (hipStream_t)stream, p);
+  hipLaunchKernelGGL((gemm_tile_kernel<kDense>),
+                     dim3((E + C::kTN - 1) / C::kTN, (T + C::kTM - 1) / C::kTM, 3), dim3(C::kThreads),
+                     0, (hipStream_t)stream, p);
   return sym_host::check_launch("gemm_tile_kernel");
 }
 
 static int check_grouped(const char* what, int T, int H, int I, int rows, int max_segments) {
+  SYM_REQUIRE(fits_4g(T, H) && fits_4g(rows, I) && fits_4g(2 * (long long)I, H), SYM_ERR_UNSUPPORTED,
+              "%s: an operand (x [%d, %d], h [%d, %d] or one expert's weights) is 4 GB or more",
+              what, T, H, rows, I);
   SYM_REQUIRE(T >= 0 && rows >= 0, SYM_ERR_INVALID, "%s: T=%d rows=%d", what, T, rows);
-  SYM_REQUIRE(H > 0 && H % kTK == 0, SYM_ERR_UNSUPPORTED, "%s: H=%d must be a multiple of %d",
-              what, H, kTK);
-  SYM_REQUIRE(I > 0 && I % kTK == 0, SYM_ERR_UNSUPPORTED, "%s: I=%d must be a multiple of %d",
-              what, I, kTK);
+  // gate/up steps through H 64 columns at a time, down through I 32 at a time; h rows are
+  // written in 128-byte pieces
+  SYM_REQUIRE(H > 0 && H % big::kTK == 0, SYM_ERR_UNSUPPORTED, "%s: H=%d must be a multiple of %d",
+              what, H, big::kTK);
+  SYM_REQUIRE(I > 0 && I % big::kTK == 0, SYM_ERR_UNSUPPORTED, "%s: I=%d must be a multiple of %d",
+              what, I, big::kTK);
   SYM_REQUIRE(max_segments >= 1 && max_segments <= kMaxGemmSegments, SYM_ERR_INVALID,
               "%s: max_segments=%d out of range", what, max_segments);
-  SYM_REQUIRE((long long)rows / kTM + max_segments <= 65535, SYM_ERR_UNSUPPORTED,
+  SYM_REQUIRE((long long)rows / mid::kTM + max_segments <= 65535, SYM_ERR_UNSUPPORTED,
               "%s: %d rows too many", what, rows);
   return SYM_OK;
 }
@@ -376,6 +655,8 @@ extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int row
   SYM_REQUIRE(x && sorted_tokens && seg_expert && seg_offset && seg_count && n_segments &&
                   w_gate_up && h,
               SYM_ERR_INVALID, "moe_gate_up_tiled: null pointer argument");
+  SYM_REQUIRE(aligned(x, 16) && aligned(w_gate_up, 16) && aligned(h, 16), SYM_ERR_INVALID,
+              "moe_gate_up_tiled: x, w_gate_up and h must be 16-byte aligned");
   TileArgs p{};
   p.a = (const uint16_t*)x;
   p.w = (const uint16_t*)w_gate_up;
@@ -389,9 +670,10 @@ extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int row
   p.K = H;
   p.out_bf16 = (uint16_t*)h;
   (void)hipGetLastError();
+  namespace C = big;
   hipLaunchKernelGGL((gemm_tile_kernel<kGateUp>),
-                     dim3((I + 127) / 128, rows / kTM + max_segments), dim3(kTileThreads), 0,
-                     (hipStream_t)stream, p);
+                     dim3((I + C::kTN / 2 - 1) / (C::kTN / 2), rows / C::kTM + max_segments),
+                     dim3(C::kThreads), 0, (hipStream_t)stream, p);
   return sym_host::check_launch("gemm_tile_kernel");
 }
 
@@ -404,6 +686,8 @@ extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
   if (rc || rows == 0 || T == 0) return rc;
   SYM_REQUIRE(h && seg_expert && seg_offset && seg_count && n_segments && w_down && y,
               SYM_ERR_INVALID, "moe_down_tiled: null pointer argument");
+  SYM_REQUIRE(aligned(h, 16) && aligned(w_down, 16) && aligned(y, 16), SYM_ERR_INVALID,
+              "moe_down_tiled: h, w_down and y must be 16-byte aligned");
   TileArgs p{};
   p.a = (const uint16_t*)h;
   p.w = (const uint16_t*)w_down;
@@ -417,8 +701,9 @@ extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
   if (y_bf16) p.out_bf16 = (uint16_t*)y;
   else p.out_f32 = (float*)y;
   (void)hipGetLastError();
-  hipLaunchKernelGGL((gemm_tile_kernel<kDown>),
-                     dim3((H + kTN - 1) / kTN, rows / kTM + max_segments), dim3(kTileThreads), 0,
-                     (hipStream_t)stream, p);
-  return sym_host::check_launch("gemm_tile_kernel");
+  namespace C = mid;
+  hipLaunchKernelGGL((gemm_tile128_kernel<kDown>),
+                     dim3((H + C::kTN - 1) / C::kTN, rows / C::kTM + max_segments),
+                     dim3(C::kThreads), 0, (hipStream_t)stream, p);
+  return sym_host::check_launch("gemm_tile128_kernel");
 }

@@ -892,8 +892,8 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
     """h = silu(x Wg^T) * (x Wu^T), y = h Wd^T per segment; returns (h [rows, I], y [rows, H]).
     The weights are bf16 tensors, or BlockFp8 (fp8 e4m3fn + 128 x 128 block scales, dequantized
     in the kernel). ``kernel``: "stream" (weight-streaming kernels for decode-size segments),
-    "tiled" (128 x 256 MFMA tiles for prefill-size segments, bf16 only) or "auto" (tiled from
-    TILED_MIN_TOKENS tokens with bf16 weights). ``y_dtype``: fp32, or bf16 with the tiled kernels
+    "tiled" (256 x 256 / 128 x 256 MFMA tiles for prefill-size segments, bf16 only) or "auto"
+    (tiled from TILED_MIN_TOKENS tokens with bf16 weights). ``y_dtype``: fp32, or bf16 with the tiled kernels
     (half the bytes of y written and read back by the combine)."""
     _check(x, "x", torch.bfloat16)
     if x.dim() != 2:
