@@ -56,6 +56,7 @@ struct TileArgs {
   const int32_t* seg_offset;
   const int32_t* seg_count;
   const int32_t* n_segments;
+  int max_segments;         // grouped modes: entries of the seg_* arrays (>= *n_segments)
   int M, N, K;              // GATE_UP: N = I (h columns); DOWN: N = H
   uint16_t* out_bf16;
   float* out_f32;
@@ -111,9 +112,10 @@ __device__ __forceinline__ int xcd_tile(int lin, int n) {
 // p.M; grouped modes: each segment owns ceil(seg_count / TM) consecutive row tiles, found by
 // every wave scanning the segment list (prefix sums by lane shuffles; no LDS, no barrier, all
 // waves agree): once for the number of row tiles, then up to the segment holding the row tile.
-// The counts are loaded 512 segments at a time (8 loads in flight per lane) and kept in
-// registers for the second pass when there are at most 512 segments. Returns false past the
-// last tile (the grouped grids are sized for the worst case). Results are wave-uniform.
+// The counts, offsets and experts of 512 segments at a time load together with n_segments (the
+// first 512 speculatively, bounded by max_segments), so that a tile with at most 512 segments
+// in the list waits for one round trip. Returns false past the last tile (the grouped grids
+// are sized for the worst case). Results are wave-uniform.
 struct TileLoc {
   int row0, rows, e, ct, z;  // first row, valid rows, expert, column tile, weight plane
 };
@@ -134,58 +136,62 @@ __device__ __forceinline__ bool locate_tile(const TileArgs& p, int lane, TileLoc
     return true;
   } else {
     constexpr int kBatch = 8;  // 64-segment chunks per batch
-    const int nseg = p.n_segments[0];
-    const int nbatch = (nseg + 64 * kBatch - 1) / (64 * kBatch);
-    int nt[kBatch];
+    int cnt[kBatch], off[kBatch], exp[kBatch];
     auto load = [&](int b) {
 #pragma unroll
       for (int c = 0; c < kBatch; ++c) {
         const int s = (b * kBatch + c) * 64 + lane;
-        nt[c] = s < nseg ? (p.seg_count[s] + TM - 1) / TM : 0;
+        const bool in = s < p.max_segments;
+        cnt[c] = in ? p.seg_count[s] : 0;
+        off[c] = in ? p.seg_offset[s] : 0;
+        exp[c] = in ? p.seg_expert[s] : 0;
       }
+    };
+    load(0);
+    const int nseg = p.n_segments[0];
+    const int nbatch = (nseg + 64 * kBatch - 1) / (64 * kBatch);
+    auto tiles = [&](int b, int c) {
+      return (b * kBatch + c) * 64 + lane < nseg ? (cnt[c] + TM - 1) / TM : 0;
     };
     int ntile = 0;
     for (int b = 0; b < nbatch; ++b) {
-      load(b);
+      if (b > 0) load(b);
 #pragma unroll
-      for (int c = 0; c < kBatch; ++c) ntile += nt[c];
+      for (int c = 0; c < kBatch; ++c) ntile += tiles(b, c);
     }
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ntile += __shfl_xor(ntile, off);
+    for (int off2 = 32; off2 > 0; off2 >>= 1) ntile += __shfl_xor(ntile, off2);
     const int t = xcd_tile(lin, ntile * nx);
     if (t < 0) return false;
     const int g = t / nx;
-    loc.ct = t - g * nx;
-    int seg = -1, start = 0, run = 0;
-    for (int b = 0; b < nbatch && seg < 0; ++b) {
-      if (nbatch > 1) load(b);  // one batch: the counts are still in registers
+    loc.ct = __builtin_amdgcn_readfirstlane(t - g * nx);
+    int found = 0, run = 0;
+    for (int b = 0; b < nbatch && !found; ++b) {
+      if (nbatch > 1) load(b);  // one batch: the values are still in registers
 #pragma unroll
       for (int c = 0; c < kBatch; ++c) {
-        int x = nt[c];
+        const int nt = tiles(b, c);
+        int x = nt;
 #pragma unroll
-        for (int off = 1; off < 64; off <<= 1) {
-          const int y = __shfl_up(x, off);
-          if (lane >= off) x += y;
+        for (int o = 1; o < 64; o <<= 1) {
+          const int y = __shfl_up(x, o);
+          if (lane >= o) x += y;
         }
-        const int s0 = run + x - nt[c];
-        const unsigned long long hit = __ballot(nt[c] > 0 && s0 <= g && g < s0 + nt[c]);
-        if (seg < 0 && hit) {
+        const int s0 = run + x - nt;
+        const unsigned long long hit = __ballot(nt > 0 && s0 <= g && g < s0 + nt);
+        if (!found && hit) {
           const int l = __ffsll((long long)hit) - 1;
-          seg = (b * kBatch + c) * 64 + l;
-          start = __shfl(s0, l);
+          const int rt = g - __shfl(s0, l);
+          // wave-uniform (the compiler cannot see it through the lane shuffles)
+          loc.e = __builtin_amdgcn_readfirstlane(__shfl(exp[c], l));
+          loc.row0 = __builtin_amdgcn_readfirstlane(__shfl(off[c], l) + rt * TM);
+          loc.rows = __builtin_amdgcn_readfirstlane(min(TM, __shfl(cnt[c], l) - rt * TM));
+          found = 1;
         }
         run += __shfl(x, 63);
       }
     }
-    if (seg < 0) return false;  // not reached: g < ntile
-    // wave-uniform (the compiler cannot see it through the lane shuffles)
-    seg = __builtin_amdgcn_readfirstlane(seg);
-    const int rt = g - __builtin_amdgcn_readfirstlane(start);
-    loc.e = __builtin_amdgcn_readfirstlane(p.seg_expert[seg]);
-    loc.row0 = __builtin_amdgcn_readfirstlane(p.seg_offset[seg] + rt * TM);
-    loc.rows = __builtin_amdgcn_readfirstlane(min(TM, p.seg_count[seg] - rt * TM));
-    loc.ct = __builtin_amdgcn_readfirstlane(loc.ct);
-    return true;
+    return found;  // (always true: g < ntile)
   }
 }
 
@@ -329,23 +335,26 @@ void gemm_tile_kernel(TileArgs p) {
   const bool a_on = wave * kARows < loc.rows;
   uint32_t a_off[kADma], b_off[kBDma];
 #pragma unroll
-  for (int i = 0; i < kADma; ++i)
-    a_off[i] = a_row_offset<MODE>(p, loc, min(wave * kARows + lr + kRowsPerDma * i, loc.rows - 1)) +
-               chunk_b;
-#pragma unroll
   for (int i = 0; i < kBDma; ++i)
     b_off[i] = b_row_offset<MODE, kTN>(p, loc.ct, wave * kBRows + lr + kRowsPerDma * i) + chunk_b;
   const int a_dst = wave * kARows * kTK;  // element offset of this wave's first A row
   const int b_dst = kAStage + wave * kBRows * kTK;
 
-  auto issue = [&](int kt, uint16_t* stage) {
+  auto issue_a = [&](int kt, uint16_t* stage) {
     const uint32_t k = (uint32_t)kt * (kTK * 2);
     if (a_on) {
 #pragma unroll
       for (int i = 0; i < kADma; ++i) dma16(p.a, a_off[i] + k, stage + a_dst + i * 512);
     }
+  };
+  auto issue_b = [&](int kt, uint16_t* stage) {
+    const uint32_t k = (uint32_t)kt * (kTK * 2);
 #pragma unroll
     for (int i = 0; i < kBDma; ++i) dma16(wbase, b_off[i] + k, stage + b_dst + i * 512);
+  };
+  auto issue = [&](int kt, uint16_t* stage) {
+    issue_a(kt, stage);
+    issue_b(kt, stage);
   };
 
   // fragment rows of this wave: A rows wm*64 + 16i + r16; B rows b_row(j) + r16 per column
@@ -404,11 +413,19 @@ void gemm_tile_kernel(TileArgs p) {
   auto loop = [&](auto with_mfma) {
     constexpr bool kMfma = decltype(with_mfma)::value;
     u32x4 fa[kNF], fb[kNF];
-    issue(0, smem);
+    // the weight rows of steps 0 and 1 go first: the A rows may wait for their row indices
+    // (GATE_UP gathers them). Step 0 in, step 1's A loads (or, for a wave without A rows, its
+    // B loads) may still fly: 4 either way.
+    issue_b(0, smem);
+    if (nk > 1) issue_b(1, smem + kStage);
+#pragma unroll
+    for (int i = 0; i < kADma; ++i)
+      a_off[i] = a_row_offset<MODE>(p, loc, min(wave * kARows + lr + kRowsPerDma * i, loc.rows - 1)) +
+                 chunk_b;
+    issue_a(0, smem);
     if (nk > 1) {
-      issue(1, smem + kStage);
-      if (a_on) SYM_TILE_SYNC(8);  // step 0 in; step 1 (this wave's 8 or 4 loads) may fly
-      else SYM_TILE_SYNC(4);
+      issue_a(1, smem + kStage);
+      SYM_TILE_SYNC(4);
     } else {
       SYM_TILE_SYNC(0);
     }
@@ -665,6 +682,7 @@ extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int row
   p.seg_offset = seg_offset;
   p.seg_count = seg_count;
   p.n_segments = n_segments;
+  p.max_segments = max_segments;
   p.M = rows;
   p.N = I;
   p.K = H;
@@ -695,6 +713,7 @@ extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
   p.seg_offset = seg_offset;
   p.seg_count = seg_count;
   p.n_segments = n_segments;
+  p.max_segments = max_segments;
   p.M = rows;
   p.N = H;
   p.K = I;
