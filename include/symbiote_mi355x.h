@@ -263,7 +263,8 @@ int sym_attn_decode_step_fp8(const void* qkv, const void* q_norm_w, const void* 
 int sym_moe_router_logits(const void* x, const float* w, int T, int H, int E, float* parts,
                           void* stream);
 
-/* The same router logits for prefill-size T, on bf16 MFMA tiles (sym_gemm_bf16's kernel):
+/* The same router logits for prefill-size T, on bf16 MFMA tiles (128 x 256, the grouped down
+ * projection's kernel):
  *   w_planes [3, E, H] bf16 with w = hi + mid + lo exactly (the fp32 gate weight split into
  *   three 8-bit-mantissa planes, e.g. hi = w with its low 16 bits cleared, mid likewise of
  *   w - hi, lo = w - hi - mid); x [T, H] bf16;

@@ -9,15 +9,16 @@
 // 16 rows x 64 bytes (a 32-column step of K-major rows) reaches ~30 B/clk per CU from L2, one of
 // 8 rows x 128 bytes ~50 B/clk, while LDS reads (~190 B/clk) and back-to-back MFMAs (94% of
 // peak) have room; and the chip clocks down to 1.5-2.1 GHz under these kernels. Two tile shapes:
-//   gemm_tile_kernel (dense projections, router logits, grouped gate/up): 256 x 256 tiles, one
+//   gemm_tile_kernel (dense projections, grouped gate/up): 256 x 256 tiles, one
 //     workgroup of 8 waves per CU, each wave a 64 x 128 block (4 x 8 v_mfma_f32_16x16x32_bf16
 //     tiles). The K loop moves 64 columns per step (128-byte rows: whole cache lines) through two
 //     64 KB LDS stages; each step is computed in two 32-column halves whose fragment reads
 //     overlap the other half's MFMAs, with one barrier per step.
-//   gemm_tile128_kernel (grouped down projection, K = I = 512: few steps per tile): 128 x 256
-//     tiles, two workgroups of 8 waves per CU, each wave a 64 x 64 block; 32 columns per step
-//     through a 3-stage 72 KB ring. The second workgroup covers a tile's prologue (segment
-//     lookup, first loads) and epilogue, which a one-workgroup shape leaves bare at 16 steps.
+//   gemm_tile128_kernel (grouped down projection, K = I = 512: few steps per tile; router
+//     logits, N = E = 256: few tiles): 128 x 256 tiles, two workgroups of 8 waves per CU, each
+//     wave a 64 x 64 block; 32 columns per step through a 3-stage 72 KB ring. The second
+//     workgroup covers a tile's prologue (segment lookup, first loads) and epilogue, which a
+//     one-workgroup shape leaves bare at 16 steps.
 // Operand tiles go from global memory straight into LDS (global_load_lds_dwordx4, no register
 // staging). A wave-wide LDS-DMA instruction writes 1 KB contiguously: lane l takes row l / c,
 // 16-byte slot l % c (c = chunks per row), fetching global chunk (l % c) ^ swz(row), so that
@@ -459,8 +460,8 @@ void gemm_tile_kernel(TileArgs p) {
 }
 
 // ================================================================================================
-// 128 x 256 tiles (grouped down projection, K = I is short): 8 waves of 64 x 64, two workgroups
-// per CU (while one waits at a barrier or on its prologue, the other computes), 32-column steps
+// 128 x 256 tiles (grouped down projection, K = I is short; router logits, N = E is narrow): 8
+// waves of 64 x 64, two workgroups per CU (while one waits at a barrier or on its prologue, the other computes), 32-column steps
 // through a 3-stage 72 KB LDS ring; a step's fragment reads are all issued before its MFMAs.
 // ================================================================================================
 namespace mid {
@@ -621,7 +622,9 @@ extern "C" int sym_moe_router_logits_split(const void* x, const void* w_planes, 
               "moe_router_logits_split: E=%d must be a positive multiple of 16", E);
   SYM_REQUIRE(H > 0 && H % big::kTK == 0, SYM_ERR_UNSUPPORTED,
               "moe_router_logits_split: H=%d must be a positive multiple of %d", H, big::kTK);
-  namespace C = big;
+  // 128 x 256 tiles, two workgroups per CU: with N = E = 256 columns and three planes, 256-row
+  // tiles would leave more than half of the CUs idle at T ~ 10k
+  namespace C = mid;
   SYM_REQUIRE((T + C::kTM - 1) / C::kTM <= 65535, SYM_ERR_UNSUPPORTED,
               "moe_router_logits_split: T=%d too large", T);
   SYM_REQUIRE(fits_4g(T, H) && fits_4g(E, H), SYM_ERR_UNSUPPORTED,
@@ -638,10 +641,10 @@ extern "C" int sym_moe_router_logits_split(const void* x, const void* w_planes, 
   p.w_zstride = (long long)E * H;
   p.out_zstride = (long long)T * E;
   (void)hipGetLastError();
-  hipLaunchKernelGGL((gemm_tile_kernel<kDense>),
+  hipLaunchKernelGGL((gemm_tile128_kernel<kDense>),
                      dim3((E + C::kTN - 1) / C::kTN, (T + C::kTM - 1) / C::kTM, 3), dim3(C::kThreads),
                      0, (hipStream_t)stream, p);
-  return sym_host::check_launch("gemm_tile_kernel");
+  return sym_host::check_launch("gemm_tile128_kernel");
 }
 
 static int check_grouped(const char* what, int T, int H, int I, int rows, int max_segments) {
