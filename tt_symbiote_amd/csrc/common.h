@@ -97,12 +97,56 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
   return __builtin_bit_cast(bf16x8, v);
 }
 
+// 16 bytes per lane from global memory (base + 32-bit byte offset) into LDS at lds_base + 16 *
+// lane (LDS-DMA, global_load_lds_dwordx4; lds_base wave-uniform, in M0). Written as asm so that
+// the compiler does not add its own (conservative) waits for these LDS writes: the kernels wait
+// for them explicitly (s_waitcnt vmcnt) before the barrier that publishes the data. M0 is written
+// here only; no other instruction of the kernels that use this reads M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+// base and lds_base are wave-uniform by construction; readfirstlane states it where the
+// compiler cannot prove it (values derived from lane shuffles), at no cost where it can.
+__device__ __forceinline__ void dma16(const uint16_t* base, uint32_t off,
+                                      const uint16_t* lds_base) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_base);
+  // (readfirstlane returns int: each half goes through uint32_t, so that the low half is not
+  // sign-extended into the high one)
+  const uint64_t g = (uint64_t)(uintptr_t)base;
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32));
+  const uint64_t gu = ((uint64_t)hi << 32) | (uint64_t)lo;
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
+               "s"((const uint16_t*)(uintptr_t)gu)
+               : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+// 8 bytes per lane from LDS, transposed within each group of 16 lanes (gfx950
+// ds_read_b64_tr_b16): lane 16G + i receives, as its 16-bit elements j = 0..3, element i % 4 of
+// the 8 bytes that lane 16G + 4j + i / 4 addresses. p points into __shared__ memory.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(p));
+  return __builtin_bit_cast(uint2, r);
+}
+
 // 16x16x32 bf16 MFMA, fp32 accumulate. Operand layout (wave64):
 //   A[16 x 32]: lane l holds A[l % 16][8*(l/16) .. 8*(l/16)+7]
 //   B[32 x 16]: lane l holds B[8*(l/16) .. +7][l % 16]
 //   D[16 x 16]: lane l holds D[4*(l/16) + i][l % 16], i = 0..3
 __device__ __forceinline__ floatx4 mfma16x16x32(const uint4& a, const uint4& b, floatx4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+// 32x32x16 bf16 MFMA, fp32 accumulate. Operand layout (wave64):
+//   A[32 x 16]: lane l holds A[l % 32][8*(l/32) .. 8*(l/32)+7]
+//   B[16 x 32]: lane l holds B[8*(l/32) .. +7][l % 32]
+//   D[32 x 32]: lane l holds D[8*j + 4*(l/32) + i][l % 32] in element 4j + i, j, i = 0..3
+__device__ __forceinline__ floatx16 mfma32x32x16(const uint4& a, const uint4& b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }
 
 }  // namespace sym

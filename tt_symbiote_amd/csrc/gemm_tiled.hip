@@ -67,29 +67,8 @@ struct TileArgs {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-// 16 bytes per lane from global memory (base + 32-bit byte offset) into LDS at lds_base + 16 *
-// lane (lds_base wave-uniform, in M0). Written as asm so that the compiler does not add its own
-// (conservative) waits for these LDS writes: the kernels wait for them explicitly
-// (SYM_TILE_SYNC) before the barrier that publishes a stage.
-// (M0 is written here only; no other instruction of these kernels reads it.)
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// base and lds_base are wave-uniform by construction; readfirstlane states it where the
-// compiler cannot prove it (values derived from lane shuffles), at no cost where it can.
-__device__ __forceinline__ void dma16(const uint16_t* base, uint32_t off,
-                                      const uint16_t* lds_base) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds_base);
-  // (readfirstlane returns int: each half goes through uint32_t, so that the low half is not
-  // sign-extended into the high one)
-  const uint64_t g = (uint64_t)(uintptr_t)base;
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g);
-  const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32));
-  const uint64_t gu = ((uint64_t)hi << 32) | (uint64_t)lo;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
-               "s"((const uint16_t*)(uintptr_t)gu)
-               : "memory", "m0");
-}
-#pragma clang diagnostic pop
+// dma16 (common.h) moves 16 bytes per lane from global memory into LDS; the kernels below wait
+// for it explicitly (SYM_TILE_SYNC) before the barrier that publishes a stage.
 
 // Wait until at most N of this wave's vector-memory loads are outstanding (the LDS-DMA of later
 // steps) and for this wave's LDS reads, then the workgroup barrier. The asm is a compiler memory

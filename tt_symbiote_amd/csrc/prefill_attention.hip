@@ -20,97 +20,81 @@
 
 namespace sym {
 
-constexpr int kPD = 128;           // head dim
-constexpr int kPQ = 128;           // queries per workgroup
-constexpr int kPK = 64;            // keys per block
-constexpr int kPKStride = kPD + 8; // LDS row stride of K (elements)
-constexpr float kLazyMax = 8.f;      // log2 headroom of the lazily rescaled softmax
-constexpr int kPVStride = kPK + 4; // LDS row stride of V^T: 34 dwords, so the 16 rows of an
-                                   // 8-byte fragment read start in distinct bank pairs
+constexpr int kPD = 128;              // head dim
+constexpr int kPQ = 128;              // queries per workgroup
+constexpr int kPK = 64;               // keys per block
+constexpr int kRowElems = kPD;        // one key's 128 dims (256 bytes) per LDS row
+constexpr int kStageElems = kPK * kRowElems;  // one operand (K or V) of one key block: 16 KB
+constexpr float kLazyMax = 8.f;       // log2 headroom of the lazily rescaled softmax
 
-// 16 bytes as a native vector (an array of these stays in registers across the key-block loop;
-// one of HIP's uint4 struct was left in scratch memory)
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// LDS layout of a key block: K and V row-major (row r = key k0 + r, 256 bytes), their 16-byte
+// chunks c stored at slot c ^ swizzle(r) of the row, so that both kinds of fragment read touch
+// distinct banks without padding (which the LDS-DMA's contiguous 1 KB writes cannot leave):
+//   K: swizzle r & 15      - the 16 rows of a K fragment read (one chunk each) hit 16 slots;
+//   V: swizzle 2 * (r & 7) - a transposed V read (16 rows x 32 bytes) hits every slot twice.
+__device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
+__device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((r & 7) << 1); }
 
-// Loads of one key block (keys k0 .. k0+63 of a sequence, clamped to its last key L-1) for the
-// staging below: kreg[j] = K chunk (idx%16) of key idx/16, vreg[i][u] = V chunk idx/32 of key
-// 2(idx%32)+u, with idx = tid + 256j (resp. 256i). k / v point at the sequence's first token of
-// this kv head.
-__device__ __forceinline__ void load_kv_block(const uint16_t* __restrict__ k,
-                                              const uint16_t* __restrict__ v, int Hkv, int L,
-                                              int k0, int tid, u32x4 (&kreg)[4],
-                                              u32x4 (&vreg)[2][2]) {
-  // element offsets from the sequence's first row in 32 bits with 24-bit multiplies (the host
-  // checks max_seqlen * Hkv * 128 < 2^31)
-  const unsigned row = (unsigned)Hkv * kPD;
-  const int kk = k0 + (tid >> 4), kc = (tid & 15) * 8;
+// Instruction order of one overlapped stretch: NR groups of (RD LDS reads, then MPG times one
+// MFMA followed by NV VALU instructions), so the softmax of one half issues between the MFMAs
+// of the other.
+template <int NR, int RD, int MPG, int NV>
+__device__ __forceinline__ void interleave_mfma_valu() {
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const unsigned kr = (unsigned)min(kk + 16 * j, L - 1);
-    kreg[j] = *reinterpret_cast<const u32x4*>(k + (__umul24(kr, row) + kc));
-  }
-  const int vk = k0 + 2 * (tid & 31), vc = (tid >> 5) * 8;
+  for (int r = 0; r < NR; ++r) {
+    if constexpr (RD > 0) __builtin_amdgcn_sched_group_barrier(0x100, RD, 0);  // LDS reads
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const unsigned kr = (unsigned)min(vk + u, L - 1);
-      vreg[i][u] = *reinterpret_cast<const u32x4*>(v + (__umul24(kr, row) + vc + 64 * i));
+    for (int i = 0; i < MPG; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);  // VALU
     }
   }
 }
 
-// Stores one key block's registers (from load_kv_block) into an LDS stage:
-//   K: item j = tid + 256j is (key idx/16, 16-byte chunk idx%16), stored row-major;
-//   V: item i = tid + 256i is (key pair p = idx%32, chunk c = idx/32): the chunk of keys 2p and
-//      2p+1 is transposed into 8 dwords (dim c*8+e: key 2p in the low half, 2p+1 in the high
-//      half), so the 32 lanes of a pair-row write 128 contiguous bytes of sVt (no bank
-//      conflicts).
-__device__ __forceinline__ void stage_kv_block(uint16_t* __restrict__ sK,
-                                               uint16_t* __restrict__ sVt, int tid,
-                                               const u32x4 (&kreg)[4],
-                                               const u32x4 (&vreg)[2][2]) {
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = tid + 256 * j;
-    *reinterpret_cast<u32x4*>(&sK[(idx >> 4) * kPKStride + (idx & 15) * 8]) = kreg[j];
-  }
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int idx = tid + 256 * i;
-    const int p = idx & 31, c = idx >> 5;
-    const u32x4 a = vreg[i][0], b = vreg[i][1];
-    uint32_t* dst = reinterpret_cast<uint32_t*>(&sVt[(c * 8) * kPVStride + 2 * p]);
-#pragma unroll
-    for (int mm = 0; mm < 4; ++mm) {
-      // dims 2mm (low halves) and 2mm+1 (high halves) of keys 2p (low) and 2p+1 (high)
-      dst[(2 * mm) * (kPVStride / 2)] = __builtin_amdgcn_perm(b[mm], a[mm], 0x05040100u);
-      dst[(2 * mm + 1) * (kPVStride / 2)] = __builtin_amdgcn_perm(b[mm], a[mm], 0x07060302u);
-    }
-  }
+// Makes the P^T operands of a half exist at this point: without it the compiler sinks the
+// exponentials below the rescale branch, out of the stretch where they overlap the MFMAs.
+__device__ __forceinline__ void pin_operands(const uint4 (&p)[2]) {
+  asm volatile("" ::"v"(p[0].x), "v"(p[0].y), "v"(p[0].z), "v"(p[0].w), "v"(p[1].x),
+               "v"(p[1].y), "v"(p[1].z), "v"(p[1].w));
 }
 
-// Maximum over lanes l, l^16, l^32, l^48 (the four lanes that hold one query's keys) with the
-// gfx950 cross-row swaps: v_permlane32_swap of x with itself leaves x of lane l^32 in the other
-// register of the pair (likewise v_permlane16_swap for l^16), all in VALU.
-__device__ __forceinline__ float max_over_rows(float x) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+// v_max_f32 / v_max3_f32 without the canonicalising maxima that fmaxf adds for operands the
+// compiler cannot prove canonical (the scores hold no NaN)
+__device__ __forceinline__ float vmax(float a, float b) {
+  float r;
+  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
+  return r;
+}
+__device__ __forceinline__ float vmax3(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// Maxima of both query tiles over the four lanes l, l^16, l^32, l^48 that hold one query's keys,
+// with the gfx950 cross-row swaps: v_permlane32_swap of (x0, x1) pairs the upper half of x0
+// with the lower half of x1, so one maximum reduces tile 0 over l^32 in lanes 0-31 and tile 1
+// in lanes 32-63; a v_permlane16_swap step reduces over l^16, and a last v_permlane32_swap
+// hands each tile's result to all 64 lanes.
+__device__ __forceinline__ void max_over_rows2(float& x0, float& x1) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0), __float_as_uint(x1), false,
                                                   false);
-  const float a0 = __uint_as_float(a[0]), a1 = __uint_as_float(a[1]);
-  const float y = a0 > a1 ? a0 : a1;
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(y), __float_as_uint(y), false,
+  const float z = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(z), __float_as_uint(z), false,
                                                   false);
-  const float b0 = __uint_as_float(b[0]), b1 = __uint_as_float(b[1]);
-  return b0 > b1 ? b0 : b1;
+  const float w = vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(w), __float_as_uint(w), false,
+                                                  false);
+  x0 = __uint_as_float(c[0]);
+  x1 = __uint_as_float(c[1]);
 }
 
 __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, const int32_t* __restrict__ cu_seqlens, int Hq, int Hkv,
     float scale_log2, uint16_t* __restrict__ out) {
-  // two stages: block kb+1 is stored while block kb is read
-  __shared__ __align__(16) uint16_t sK[2][kPK * kPKStride];
-  __shared__ __align__(16) uint16_t sVt[2][kPD * kPVStride];
+  // two stages of (K, V): block kb+1 is loaded into one while block kb is read from the other
+  __shared__ __align__(16) uint16_t lds[2][2][kStageElems];
 
   // Query blocks in decreasing order over the whole grid (z slowest): the blocks with the most
   // key blocks under the causal mask, of every sequence and head, are dispatched first and the
@@ -145,120 +129,198 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int d = 0; d < 8; ++d) o[t][d] = floatx4{0.f, 0.f, 0.f, 0.f};
-  // running max (log2 domain) of the lane's query (the same in its 4 lanes r16 + 16*kq) and the
-  // lane's share of its running sum (the four shares are added after the last key block: every
-  // rescale multiplies all four by the same factor)
-  float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+  // running max (log2 domain) of the lane's query (the same in its 4 lanes r16 + 16*kq), and the
+  // running sum of its weights: ls = ONES P^T on the MFMA (a 16 x 32 A operand of bf16 ones), so
+  // every element of ls[t] is the sum over the bf16 weights that O^T accumulates
+  float m[2] = {-INFINITY, -INFINITY};
+  floatx4 ls[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
+  const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
 
   const int q_last = min(q0 + kPQ, L) - 1;
   const int nkb = q_last / kPK + 1;
-  // Key block kb is read from stage kb&1 while block kb+1, loaded into registers during block
-  // kb-1, is stored into the other stage and block kb+2 is loaded; one barrier per block (the
-  // stage written during block kb was last read during block kb-1, before that block's barrier).
-  u32x4 kreg[4], vreg[2][2];
+
+  // LDS-DMA of key block kb_ (keys past the sequence clamped to its last) into stage kb_ & 1:
+  // wave w moves rows 16w .. 16w+15 of K and of V, 4 rows (1 KB) per instruction; lane (row
+  // lane/16, slot lane%16) fetches the chunk that the slot holds. Byte offsets from the
+  // sequence's first row fit in 32 bits (the host checks max_seqlen * Hkv * 128 < 2^31).
   const uint16_t* kbase = k + ((size_t)s0 * Hkv + g) * kPD;
   const uint16_t* vbase = v + ((size_t)s0 * Hkv + g) * kPD;
-  load_kv_block(kbase, vbase, Hkv, L, 0, tid, kreg, vreg);
-  stage_kv_block(sK[0], sVt[0], tid, kreg, vreg);
-  if (nkb > 1) load_kv_block(kbase, vbase, Hkv, L, kPK, tid, kreg, vreg);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
+  const uint32_t row_bytes = (uint32_t)Hkv * kPD * 2;
+  const size_t block_elems = (size_t)kPK * Hkv * kPD;  // one key block of this sequence
+  uint32_t k_src[4], v_src[4];  // lane's byte offsets within a block (row r, slot lane%16)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * wave + 4 * i + (lane >> 4);
+    k_src[i] = r * row_bytes + 16 * k_slot(r, lane & 15);
+    v_src[i] = r * row_bytes + 16 * v_slot(r, lane & 15);
+  }
+  auto load_block = [&](int kb_) {
+    uint16_t* st = &lds[kb_ & 1][0][0];
+    const uint16_t* kb_k = kbase + kb_ * block_elems;
+    const uint16_t* kb_v = vbase + kb_ * block_elems;
+    if ((kb_ + 1) * kPK <= L) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        dma16(kb_k, k_src[i], st + (16 * wave + 4 * i) * kRowElems);
+        dma16(kb_v, v_src[i], st + kStageElems + (16 * wave + 4 * i) * kRowElems);
+      }
+    } else {  // the sequence's last block: rows past it repeat its last key
+      const int last = L - 1 - kb_ * kPK;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 16 * wave + 4 * i + (lane >> 4);
+        const uint32_t row = (uint32_t)min(r, last) * row_bytes;
+        dma16(kb_k, row + 16 * k_slot(r, lane & 15), st + (16 * wave + 4 * i) * kRowElems);
+        dma16(kb_v, row + 16 * v_slot(r, lane & 15),
+              st + kStageElems + (16 * wave + 4 * i) * kRowElems);
+      }
+    }
+  };
+
+  // Fragment addresses within a stage (elements):
+  //   K (A operand of S^T, rows 32h + 16jj + r16, dims 8kq + 32c): chunk kq + 4c of that row;
+  //   V (read transposed: lane s = r16 of group kq addresses key 4kq + s/4 (+ 32h, + 16 for
+  //   the upper four keys), dims 16d + 4(s%4) .. +3, and receives keys 4kq .. 4kq+3 of dim
+  //   16d + r16 - the A operand of O^T += V^T P^T in the key order of the score layout).
+  int k_off[4], v_off[8];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) k_off[c] = r16 * kRowElems + 8 * k_slot(r16, kq + 4 * c);
+  const int vr = 4 * kq + (r16 >> 2);
+#pragma unroll
+  for (int d = 0; d < 8; ++d)
+    v_off[d] = kStageElems + vr * kRowElems + 8 * v_slot(vr, 2 * d + ((r16 >> 1) & 1)) +
+               4 * (r16 & 1);
+
+  // One key block in two 32-key halves h: S^T of half 1 is issued while the softmax of half 0
+  // runs, and O^T += V^T P^T of half 0 while the softmax of half 1 runs, so a wave's MFMAs and
+  // VALU work overlap. MASK (the block crosses the diagonal or the sequence end) is a template
+  // flag so that each half's MFMAs and softmax form one branch-free stretch of code.
+  auto block = [&](auto mask_tag, int kb) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int k0 = kb * kPK;
-    const uint16_t* cK = sK[kb & 1];
-    const uint16_t* cVt = sVt[kb & 1];
-    // ---- S^T = K Q^T: lane holds keys k0 + 16j + 4*kq + i of query qrow[t] ----
-    floatx4 sc[2][4];
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) sc[t][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      uint4 kf[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j)
-        kf[j] = *reinterpret_cast<const uint4*>(&cK[(j * 16 + r16) * kPKStride + 8 * kq + 32 * c]);
+    if (kb + 1 < nkb) load_block(kb + 1);
+    const uint16_t* st = &lds[kb & 1][0][0];
+    // S^T of half h: sh[t][jj] holds keys k0 + 32h + 16jj + 4*kq + i of query qrow[t]
+    auto scores = [&](int hh, floatx4 (&sh)[2][2]) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) sc[t][j] = mfma16x16x32(kf[j], qf[t][c], sc[t][j]);
-    }
-    if (kb + 1 < nkb) {
-      stage_kv_block(sK[(kb + 1) & 1], sVt[(kb + 1) & 1], tid, kreg, vreg);
-      if (kb + 2 < nkb) load_kv_block(kbase, vbase, Hkv, L, k0 + 2 * kPK, tid, kreg, vreg);
-    }
-    // keys past a query of this wave (the diagonal) or past the sequence are masked
-    const bool masked = k0 + kPK - 1 > wq0 || k0 + kPK > L;
-    uint4 pf[2][2];  // P^T operands: [t][32-key chunk]
+        for (int jj = 0; jj < 2; ++jj) sh[t][jj] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      if (masked) {
+      for (int c = 0; c < 4; ++c) {
+        uint4 kf[2];
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int jj = 0; jj < 2; ++jj)
+          kf[jj] = *reinterpret_cast<const uint4*>(
+              st + k_off[c] + (32 * hh + 16 * jj) * kRowElems);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int key = k0 + 16 * j + 4 * kq + i;
-            if (key > qrow[t] || key >= L) sc[t][j][i] = -INFINITY;
-          }
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int jj = 0; jj < 2; ++jj) sh[t][jj] = mfma16x16x32(kf[jj], qf[t][c], sh[t][jj]);
       }
-      float mx = sc[t][0][0];
+    };
+    // Online softmax of half hh (log2 domain, lazily rescaled: the running max moves only when
+    // a score exceeds it by more than kLazyMax, so the weights stay below 2^kLazyMax; the
+    // result is the same softmax). Key 0 of block 0 is visible to every query, so the max is
+    // finite from the first half on. Leaves the P^T operands in pf, the rescale factors in al.
+    auto softmax = [&](int hh, floatx4 (&sh)[2][2], uint4 (&pf)[2], float (&al)[2]) {
+      float mx[2];
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int t = 0; t < 2; ++t) {
+        if constexpr (MASK) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[t][j][i]);
-      mx = max_over_rows(mx);
-      // Lazy rescaling: the running max (log2 domain) moves only when a score exceeds it by more
-      // than kLazyMax, so the weights stay below 2^kLazyMax and most blocks skip the rescale of
-      // the output; the result is the same softmax. Key 0 of block 0 is visible to every query,
-      // so the max is finite from the first block on.
-      const float mxs = mx * scale_log2;
-      const bool grow = mxs > m[t] + kLazyMax;  // true on the first block (m = -inf)
-      const float mn = grow ? mxs : m[t];
-      const float alpha = grow ? fast_exp2(m[t] - mn) : 1.f;
-      float rs = 0.f;
+          for (int jj = 0; jj < 2; ++jj)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pj = fast_exp2(fmaf(sc[t][j][i], scale_log2, -mn));
-          sc[t][j][i] = pj;
-          rs += pj;
+            for (int i = 0; i < 4; ++i) {
+              const int key = k0 + 32 * hh + 16 * jj + 4 * kq + i;
+              if (key > qrow[t] || key >= L) sh[t][jj][i] = -INFINITY;
+            }
         }
-      m[t] = mn;
-      l[t] = l[t] * alpha + rs;
-      if (__any(alpha != 1.f)) {
-#pragma unroll
-        for (int d = 0; d < 8; ++d)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) o[t][d][i] *= alpha;
+        mx[t] = vmax(vmax3(sh[t][0][0], sh[t][0][1], sh[t][0][2]),
+                     vmax3(sh[t][0][3], sh[t][1][0], vmax3(sh[t][1][1], sh[t][1][2], sh[t][1][3])));
       }
+      max_over_rows2(mx[0], mx[1]);
 #pragma unroll
-      for (int cc = 0; cc < 2; ++cc)
-        pf[t][cc] = make_uint4(pack_bf16x2(sc[t][2 * cc][0], sc[t][2 * cc][1]),
-                               pack_bf16x2(sc[t][2 * cc][2], sc[t][2 * cc][3]),
-                               pack_bf16x2(sc[t][2 * cc + 1][0], sc[t][2 * cc + 1][1]),
-                               pack_bf16x2(sc[t][2 * cc + 1][2], sc[t][2 * cc + 1][3]));
-    }
-    // ---- O^T += V^T P^T: A = V^T rows d*16 + r16, keys 32cc + 4kq + {0..3, 16..19} ----
+      for (int t = 0; t < 2; ++t) {
+        const float mxs = mx[t] * scale_log2;
+        const bool grow = mxs > m[t] + kLazyMax;  // true on the first half (m = -inf)
+        const float mn = grow ? mxs : m[t];
+        al[t] = grow ? fast_exp2(m[t] - mn) : 1.f;
+        m[t] = mn;
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
+        for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) sh[t][jj][i] = fast_exp2(fmaf(sh[t][jj][i], scale_log2, -mn));
+        pf[t] = make_uint4(pack_bf16x2(sh[t][0][0], sh[t][0][1]),
+                           pack_bf16x2(sh[t][0][2], sh[t][0][3]),
+                           pack_bf16x2(sh[t][1][0], sh[t][1][1]),
+                           pack_bf16x2(sh[t][1][2], sh[t][1][3]));
+      }
+    };
+    auto rescale = [&](const float (&al)[2]) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+        if (__any(al[t] != 1.f)) {
+#pragma unroll
+          for (int d = 0; d < 8; ++d)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[t][d][i] *= al[t];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ls[t][i] *= al[t];
+        }
+    };
+    // O^T += V^T P^T of half hh: A = V^T rows 16d + r16, keys 32hh + 4kq + {0..3, 16..19}
+    auto pv = [&](int hh, const uint4 (&pf)[2]) {
 #pragma unroll
       for (int d = 0; d < 8; ++d) {
-        const uint16_t* vr = &cVt[(d * 16 + r16) * kPVStride + 32 * cc + 4 * kq];
-        const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vr + 16);
+        const uint2 lo = lds_read_tr16(st + v_off[d] + (32 * hh) * kRowElems);
+        const uint2 hi = lds_read_tr16(st + v_off[d] + (32 * hh + 16) * kRowElems);
         const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
 #pragma unroll
-        for (int t = 0; t < 2; ++t) o[t][d] = mfma16x16x32(vf, pf[t][cc], o[t][d]);
+        for (int t = 0; t < 2; ++t) o[t][d] = mfma16x16x32(vf, pf[t], o[t][d]);
       }
-    }
-    __syncthreads();  // every wave is done with stage kb&1 and has stored block kb+1
-  }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) ls[t] = mfma16x16x32(ones, pf[t], ls[t]);
+    };
+    floatx4 s0[2][2], s1[2][2];
+    uint4 p0[2], p1[2];
+    float a0[2], a1[2];
+    scores(0, s0);
+    __builtin_amdgcn_sched_barrier(0);
+    scores(1, s1);
+    softmax(0, s0, p0, a0);
+    interleave_mfma_valu<4, 2, 4, 6>();
+    pin_operands(p0);
+    __builtin_amdgcn_sched_barrier(0);
+    rescale(a0);
+    __builtin_amdgcn_sched_barrier(0);
+    pv(0, p0);
+    softmax(1, s1, p1, a1);
+    interleave_mfma_valu<8, 2, 2, 6>();
+    interleave_mfma_valu<1, 0, 2, 6>();
+    pin_operands(p1);
+    __builtin_amdgcn_sched_barrier(0);
+    rescale(a1);
+    pv(1, p1);
+    // this wave's DMA of block kb+1 has landed and its reads of stage kb&1 are done; after the
+    // barrier every wave's are
+    asm volatile("s_waitcnt vmcnt(0)\n\ts_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  };
+
+  load_block(0);
+  asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+  // Blocks from kb_mask on hold keys past a query of this wave (the diagonal) or past the
+  // sequence and are masked: two loops in sequence (one branch between the two block bodies in
+  // every iteration makes the register allocator spill). Every wave runs nkb blocks in all.
+  const int kb_mask = min(min(wq0 + 1, L) / kPK, nkb);
+  int kb = 0;
+  for (; kb < kb_mask; ++kb) block(std::false_type{}, kb);
+  for (; kb < nkb; ++kb) block(std::true_type{}, kb);
+
   // ---- normalise and store: lane holds dims d*16 + 4*kq + i of query qrow[t] ----
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
-    float lt = l[t] + __shfl_xor(l[t], 16);
-    lt += __shfl_xor(lt, 32);
+    const float lt = ls[t][0];
     if (qrow[t] < L) {
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
       uint16_t* orow = out + ((size_t)(s0 + qrow[t]) * Hq + h) * kPD + 4 * kq;
