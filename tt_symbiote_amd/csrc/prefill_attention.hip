@@ -7,15 +7,17 @@
 // cu_seqlens (positions 0 .. L-1 of each sequence).
 //
 // Attention design (gfx950): one workgroup of 4 waves per (128-query block, query head,
-// sequence); each wave owns 32 queries (two 16-query tiles) and keeps its Q fragments in
-// registers. Key blocks of 64 tokens are staged in LDS (K row-major, V transposed). The wave
-// computes the transposed scores S^T = K Q^T on v_mfma_f32_16x16x32_bf16, so a lane holds 16
-// keys of one query per tile: the online softmax (log2 domain) reduces a query over the lane's
-// own values and two xor shuffles, and the exponentiated scores, packed to bf16, are already the
-// B operand of O^T += V^T P^T (the MFMA's k index is free to follow the score layout: lane group
-// kq takes keys 4kq .. 4kq+3 of two adjacent 16-key tiles, and reads the matching V^T columns as
-// two 8-byte pieces). Only key blocks at or before the query block are visited, and only the
-// blocks that cross the diagonal or the sequence end are masked.
+// sequence); each wave owns 32 queries and keeps their Q fragments in registers. Key blocks of 64
+// tokens are moved by LDS-DMA into one of two LDS stages (K and V row-major, XOR-swizzled) while
+// the previous block is computed. The wave computes the transposed scores S^T = K Q^T on
+// v_mfma_f32_32x32x16_bf16 (two 32-key tiles), so a lane holds 16 keys of one query per tile and
+// lane l^32 the other 16: the online softmax (log2 domain, lazily rescaled) reduces a query over
+// the lane's own values and one cross-half swap, and the exponentiated scores, packed to bf16,
+// are already the B operand of O^T += V^T P^T (the MFMA's k index follows the score layout), whose
+// A operand comes from transposing LDS reads of row-major V. A key block is computed in two 32-key
+// halves so that one half's softmax issues between the other half's MFMAs. Only key blocks at or
+// before the query block are visited, and only the blocks that cross the diagonal or the sequence
+// end are masked.
 #include "common.h"
 
 namespace sym {
@@ -31,9 +33,10 @@ constexpr float kLazyMax = 8.f;       // log2 headroom of the lazily rescaled so
 // chunks c stored at slot c ^ swizzle(r) of the row, so that both kinds of fragment read touch
 // distinct banks without padding (which the LDS-DMA's contiguous 1 KB writes cannot leave):
 //   K: swizzle r & 15      - the 16 rows of a K fragment read (one chunk each) hit 16 slots;
-//   V: swizzle 2 * (r & 7) - a transposed V read (16 rows x 32 bytes) hits every slot twice.
+//   V: swizzle 4 * (r & 3) - a transposed V read (per 32 lanes: 4 rows x 64 bytes) hits
+//                            4 distinct 64-byte windows.
 __device__ __forceinline__ int k_slot(int r, int c) { return c ^ (r & 15); }
-__device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((r & 7) << 1); }
+__device__ __forceinline__ int v_slot(int r, int c) { return c ^ ((r & 3) << 2); }
 
 // Instruction order of one overlapped stretch: NR groups of (RD LDS reads, then MPG times one
 // MFMA followed by NV VALU instructions), so the softmax of one half issues between the MFMAs
@@ -71,22 +74,12 @@ __device__ __forceinline__ float vmax3(float a, float b, float c) {
   return r;
 }
 
-// Maxima of both query tiles over the four lanes l, l^16, l^32, l^48 that hold one query's keys,
-// with the gfx950 cross-row swaps: v_permlane32_swap of (x0, x1) pairs the upper half of x0
-// with the lower half of x1, so one maximum reduces tile 0 over l^32 in lanes 0-31 and tile 1
-// in lanes 32-63; a v_permlane16_swap step reduces over l^16, and a last v_permlane32_swap
-// hands each tile's result to all 64 lanes.
-__device__ __forceinline__ void max_over_rows2(float& x0, float& x1) {
-  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0), __float_as_uint(x1), false,
+// Maximum over lanes l and l^32 (the two lanes that hold one query's keys): v_permlane32_swap
+// of x with itself leaves the other half's value in the second register of the pair.
+__device__ __forceinline__ float max_over_halves(float x) {
+  const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
-  const float z = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
-  const auto b = __builtin_amdgcn_permlane16_swap(__float_as_uint(z), __float_as_uint(z), false,
-                                                  false);
-  const float w = vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
-  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(w), __float_as_uint(w), false,
-                                                  false);
-  x0 = __uint_as_float(c[0]);
-  x1 = __uint_as_float(c[1]);
+  return vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
 }
 
 __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
@@ -108,41 +101,36 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
   const int g = h / (Hq / Hkv);
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar mask branches
-  const int r16 = lane & 15, kq = lane >> 4;
+  const int n32 = lane & 31, hp = lane >> 5;  // the lane's query column and key half
 
-  // Q fragments (B operand of S^T): column r16 = query q0 + wave*32 + t*16 + r16 (clamped),
-  // dims 8*kq + 32*c
+  // Q fragments (B operand of S^T): column n32 = query q0 + wave*32 + n32 (clamped), dims
+  // 16c + 8hp .. +7
   const int wq0 = q0 + wave * 32;
-  int qrow[2];
-  uint4 qf[2][4];
+  const int qrow = wq0 + n32;
+  uint4 qf[8];
+  {
+    const uint16_t* qr = q + ((size_t)(s0 + min(qrow, L - 1)) * Hq + h) * kPD + 8 * hp;
 #pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    qrow[t] = wq0 + t * 16 + r16;
-    const int qi = min(qrow[t], L - 1);
-    const uint16_t* qr = q + ((size_t)(s0 + qi) * Hq + h) * kPD + 8 * kq;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) qf[t][c] = *reinterpret_cast<const uint4*>(qr + 32 * c);
+    for (int c = 0; c < 8; ++c) qf[c] = *reinterpret_cast<const uint4*>(qr + 16 * c);
   }
-  // O^T: lane holds dims d*16 + 4*kq + i of its query (tile t)
-  floatx4 o[2][8];
+  // O^T tiles dt: lane holds dims 32dt + 8j + 4hp + i of query qrow in element 4j + i
+  floatx16 o[4];
 #pragma unroll
-  for (int t = 0; t < 2; ++t)
+  for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
-    for (int d = 0; d < 8; ++d) o[t][d] = floatx4{0.f, 0.f, 0.f, 0.f};
-  // running max (log2 domain) of the lane's query (the same in its 4 lanes r16 + 16*kq), and the
-  // running sum of its weights: ls = ONES P^T on the MFMA (a 16 x 32 A operand of bf16 ones), so
-  // every element of ls[t] is the sum over the bf16 weights that O^T accumulates
-  float m[2] = {-INFINITY, -INFINITY};
-  floatx4 ls[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-  const uint4 ones = make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
+    for (int e = 0; e < 16; ++e) o[dt][e] = 0.f;
+  // running max (log2 domain) of the lane's query (the same in lanes l and l^32) and the lane's
+  // share of its running sum (the two shares are added after the last key block: every rescale
+  // multiplies both by the same factor)
+  float m = -INFINITY, l = 0.f;
 
   const int q_last = min(q0 + kPQ, L) - 1;
   const int nkb = q_last / kPK + 1;
 
   // LDS-DMA of key block kb_ (keys past the sequence clamped to its last) into stage kb_ & 1:
   // wave w moves rows 16w .. 16w+15 of K and of V, 4 rows (1 KB) per instruction; lane (row
-  // lane/16, slot lane%16) fetches the chunk that the slot holds. Byte offsets from the
-  // sequence's first row fit in 32 bits (the host checks max_seqlen * Hkv * 128 < 2^31).
+  // lane/16, slot lane%16) fetches the chunk that the slot holds. Byte offsets within a block fit
+  // in 32 bits (the host checks max_seqlen * Hkv * 128 < 2^31).
   const uint16_t* kbase = k + ((size_t)s0 * Hkv + g) * kPD;
   const uint16_t* vbase = v + ((size_t)s0 * Hkv + g) * kPD;
   const uint32_t row_bytes = (uint32_t)Hkv * kPD * 2;
@@ -178,126 +166,116 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
   };
 
   // Fragment addresses within a stage (elements):
-  //   K (A operand of S^T, rows 32h + 16jj + r16, dims 8kq + 32c): chunk kq + 4c of that row;
-  //   V (read transposed: lane s = r16 of group kq addresses key 4kq + s/4 (+ 32h, + 16 for
-  //   the upper four keys), dims 16d + 4(s%4) .. +3, and receives keys 4kq .. 4kq+3 of dim
-  //   16d + r16 - the A operand of O^T += V^T P^T in the key order of the score layout).
-  int k_off[4], v_off[8];
+  //   K (A operand of S^T, row 32kt + n32, dims 16c + 8hp .. +7): chunk 2c + hp of that row;
+  //   V (read transposed: lane s of 16-lane group G addresses key row 4(G/2) + s/4 (+ 32kt +
+  //   16p, + 8 for the upper four keys), dims 32dt + 16(G%2) + 4(s%4) .. +3, and receives keys
+  //   4hp .. 4hp+3 of dim 32dt + n32: the A operand of O^T += V^T P^T in the score layout's key
+  //   order).
+  int k_off[8], v_off[4];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) k_off[c] = r16 * kRowElems + 8 * k_slot(r16, kq + 4 * c);
-  const int vr = 4 * kq + (r16 >> 2);
+  for (int c = 0; c < 8; ++c) k_off[c] = n32 * kRowElems + 8 * k_slot(n32, 2 * c + hp);
+  {
+    const int G = lane >> 4, sl = lane & 15;
+    const int vr = 4 * (G >> 1) + (sl >> 2);
 #pragma unroll
-  for (int d = 0; d < 8; ++d)
-    v_off[d] = kStageElems + vr * kRowElems + 8 * v_slot(vr, 2 * d + ((r16 >> 1) & 1)) +
-               4 * (r16 & 1);
+    for (int dt = 0; dt < 4; ++dt)
+      v_off[dt] = kStageElems + vr * kRowElems +
+                  8 * v_slot(vr, 4 * dt + 2 * (G & 1) + ((sl >> 1) & 1)) + 4 * (sl & 1);
+  }
 
-  // One key block in two 32-key halves h: S^T of half 1 is issued while the softmax of half 0
-  // runs, and O^T += V^T P^T of half 0 while the softmax of half 1 runs, so a wave's MFMAs and
-  // VALU work overlap. MASK (the block crosses the diagonal or the sequence end) is a template
-  // flag so that each half's MFMAs and softmax form one branch-free stretch of code.
+  // One key block in two 32-key halves kt: S^T of half 1 is issued while the softmax of half 0
+  // runs, and O^T += V^T P^T of half 0 while the softmax of half 1 runs. MASK (the block crosses
+  // the diagonal or the sequence end) is a template flag so that each half's MFMAs and softmax
+  // form one branch-free stretch of code.
   auto block = [&](auto mask_tag, int kb) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int k0 = kb * kPK;
     if (kb + 1 < nkb) load_block(kb + 1);
     const uint16_t* st = &lds[kb & 1][0][0];
-    // S^T of half h: sh[t][jj] holds keys k0 + 32h + 16jj + 4*kq + i of query qrow[t]
-    auto scores = [&](int hh, floatx4 (&sh)[2][2]) {
+    // S^T of half kt: lane holds keys k0 + 32kt + 8j + 4hp + i of query qrow (element 4j + i)
+    auto scores = [&](int kt) {
+      floatx16 sc;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+      for (int e = 0; e < 16; ++e) sc[e] = 0.f;
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj) sh[t][jj] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < 8; ++c) {
+        const uint4 kf = *reinterpret_cast<const uint4*>(st + k_off[c] + 32 * kt * kRowElems);
+        sc = mfma32x32x16(kf, qf[c], sc);
+      }
+      return sc;
+    };
+    // Online softmax of half kt (log2 domain, lazily rescaled: the running max moves only when a
+    // score exceeds it by more than kLazyMax, so the weights stay below 2^kLazyMax; the result
+    // is the same softmax). Key 0 of block 0 is visible to every query, so the max is finite
+    // from the first half on. Returns the P^T operands (k-steps of keys 16p .. 16p+15) and
+    // leaves the rescale factor in al.
+    auto softmax = [&](int kt, floatx16& sc, uint4 (&pf)[2], float& al) {
+      if constexpr (MASK) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        uint4 kf[2];
+        for (int j = 0; j < 4; ++j)
 #pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-          kf[jj] = *reinterpret_cast<const uint4*>(
-              st + k_off[c] + (32 * hh + 16 * jj) * kRowElems);
+          for (int i = 0; i < 4; ++i) {
+            const int key = k0 + 32 * kt + 8 * j + 4 * hp + i;
+            if (key > qrow || key >= L) sc[4 * j + i] = -INFINITY;
+          }
+      }
+      float mx = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]),
+                       vmax3(sc[6], sc[7], sc[8]));
+      mx = vmax3(mx, vmax3(sc[9], sc[10], sc[11]), vmax3(sc[12], sc[13], vmax(sc[14], sc[15])));
+      mx = max_over_halves(mx);
+      const float mxs = mx * scale_log2;
+      const bool grow = mxs > m + kLazyMax;  // true on the first half (m = -inf)
+      const float mn = grow ? mxs : m;
+      al = grow ? fast_exp2(m - mn) : 1.f;
+      m = mn;
+      float rs = 0.f;
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+      for (int e = 0; e < 16; ++e) {
+        sc[e] = fast_exp2(fmaf(sc[e], scale_log2, -mn));
+        rs += sc[e];
+      }
+      l = l * al + rs;
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj) sh[t][jj] = mfma16x16x32(kf[jj], qf[t][c], sh[t][jj]);
+      for (int pp = 0; pp < 2; ++pp)
+        pf[pp] = make_uint4(pack_bf16x2(sc[8 * pp + 0], sc[8 * pp + 1]),
+                            pack_bf16x2(sc[8 * pp + 2], sc[8 * pp + 3]),
+                            pack_bf16x2(sc[8 * pp + 4], sc[8 * pp + 5]),
+                            pack_bf16x2(sc[8 * pp + 6], sc[8 * pp + 7]));
+    };
+    auto rescale = [&](float al) {
+      if (__any(al != 1.f)) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[dt][e] *= al;
       }
     };
-    // Online softmax of half hh (log2 domain, lazily rescaled: the running max moves only when
-    // a score exceeds it by more than kLazyMax, so the weights stay below 2^kLazyMax; the
-    // result is the same softmax). Key 0 of block 0 is visible to every query, so the max is
-    // finite from the first half on. Leaves the P^T operands in pf, the rescale factors in al.
-    auto softmax = [&](int hh, floatx4 (&sh)[2][2], uint4 (&pf)[2], float (&al)[2]) {
-      float mx[2];
+    // O^T += V^T P^T of half kt: k-step p covers keys 32kt + 16p + {4hp .. 4hp+3, 8+4hp .. 11+4hp}
+    auto pv = [&](int kt, const uint4 (&pf)[2]) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        if constexpr (MASK) {
+      for (int pp = 0; pp < 2; ++pp)
 #pragma unroll
-          for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int key = k0 + 32 * hh + 16 * jj + 4 * kq + i;
-              if (key > qrow[t] || key >= L) sh[t][jj][i] = -INFINITY;
-            }
+        for (int dt = 0; dt < 4; ++dt) {
+          const uint16_t* vp = st + v_off[dt] + (32 * kt + 16 * pp) * kRowElems;
+          const uint2 lo = lds_read_tr16(vp);
+          const uint2 hi = lds_read_tr16(vp + 8 * kRowElems);
+          o[dt] = mfma32x32x16(make_uint4(lo.x, lo.y, hi.x, hi.y), pf[pp], o[dt]);
         }
-        mx[t] = vmax(vmax3(sh[t][0][0], sh[t][0][1], sh[t][0][2]),
-                     vmax3(sh[t][0][3], sh[t][1][0], vmax3(sh[t][1][1], sh[t][1][2], sh[t][1][3])));
-      }
-      max_over_rows2(mx[0], mx[1]);
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const float mxs = mx[t] * scale_log2;
-        const bool grow = mxs > m[t] + kLazyMax;  // true on the first half (m = -inf)
-        const float mn = grow ? mxs : m[t];
-        al[t] = grow ? fast_exp2(m[t] - mn) : 1.f;
-        m[t] = mn;
-#pragma unroll
-        for (int jj = 0; jj < 2; ++jj)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) sh[t][jj][i] = fast_exp2(fmaf(sh[t][jj][i], scale_log2, -mn));
-        pf[t] = make_uint4(pack_bf16x2(sh[t][0][0], sh[t][0][1]),
-                           pack_bf16x2(sh[t][0][2], sh[t][0][3]),
-                           pack_bf16x2(sh[t][1][0], sh[t][1][1]),
-                           pack_bf16x2(sh[t][1][2], sh[t][1][3]));
-      }
     };
-    auto rescale = [&](const float (&al)[2]) {
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-        if (__any(al[t] != 1.f)) {
-#pragma unroll
-          for (int d = 0; d < 8; ++d)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[t][d][i] *= al[t];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) ls[t][i] *= al[t];
-        }
-    };
-    // O^T += V^T P^T of half hh: A = V^T rows 16d + r16, keys 32hh + 4kq + {0..3, 16..19}
-    auto pv = [&](int hh, const uint4 (&pf)[2]) {
-#pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        const uint2 lo = lds_read_tr16(st + v_off[d] + (32 * hh) * kRowElems);
-        const uint2 hi = lds_read_tr16(st + v_off[d] + (32 * hh + 16) * kRowElems);
-        const uint4 vf = make_uint4(lo.x, lo.y, hi.x, hi.y);
-#pragma unroll
-        for (int t = 0; t < 2; ++t) o[t][d] = mfma16x16x32(vf, pf[t], o[t][d]);
-      }
-#pragma unroll
-      for (int t = 0; t < 2; ++t) ls[t] = mfma16x16x32(ones, pf[t], ls[t]);
-    };
-    floatx4 s0[2][2], s1[2][2];
     uint4 p0[2], p1[2];
-    float a0[2], a1[2];
-    scores(0, s0);
+    float a0, a1;
+    floatx16 s0 = scores(0);
     __builtin_amdgcn_sched_barrier(0);
-    scores(1, s1);
+    floatx16 s1 = scores(1);
     softmax(0, s0, p0, a0);
-    interleave_mfma_valu<4, 2, 4, 6>();
+    interleave_mfma_valu<8, 1, 1, 8>();
     pin_operands(p0);
     __builtin_amdgcn_sched_barrier(0);
     rescale(a0);
     __builtin_amdgcn_sched_barrier(0);
     pv(0, p0);
     softmax(1, s1, p1, a1);
-    interleave_mfma_valu<8, 2, 2, 6>();
-    interleave_mfma_valu<1, 0, 2, 6>();
+    interleave_mfma_valu<8, 2, 1, 8>();
     pin_operands(p1);
     __builtin_amdgcn_sched_barrier(0);
     rescale(a1);
@@ -317,18 +295,21 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
   for (; kb < kb_mask; ++kb) block(std::false_type{}, kb);
   for (; kb < nkb; ++kb) block(std::true_type{}, kb);
 
-  // ---- normalise and store: lane holds dims d*16 + 4*kq + i of query qrow[t] ----
-#pragma unroll
-  for (int t = 0; t < 2; ++t) {
-    const float lt = ls[t][0];
-    if (qrow[t] < L) {
+  // ---- normalise and store: lane holds dims 32dt + 8j + 4hp + i of query qrow ----
+  {
+    const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(l), __float_as_uint(l), false,
+                                                    false);
+    const float lt = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    if (qrow < L) {
       const float inv = lt > 0.f ? 1.f / lt : 0.f;
-      uint16_t* orow = out + ((size_t)(s0 + qrow[t]) * Hq + h) * kPD + 4 * kq;
+      uint16_t* orow = out + ((size_t)(s0 + qrow) * Hq + h) * kPD + 4 * hp;
 #pragma unroll
-      for (int d = 0; d < 8; ++d)
-        *reinterpret_cast<uint2*>(orow + d * 16) =
-            make_uint2(pack_bf16x2(o[t][d][0] * inv, o[t][d][1] * inv),
-                       pack_bf16x2(o[t][d][2] * inv, o[t][d][3] * inv));
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          *reinterpret_cast<uint2*>(orow + 32 * dt + 8 * j) =
+              make_uint2(pack_bf16x2(o[dt][4 * j] * inv, o[dt][4 * j + 1] * inv),
+                         pack_bf16x2(o[dt][4 * j + 2] * inv, o[dt][4 * j + 3] * inv));
     }
   }
 }
