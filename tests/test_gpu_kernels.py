@@ -52,6 +52,9 @@ def test_rmsnorm(device, rows, cols):
 ROUTE_CASES = [
     # T, E, n_group, topk_group, top_k, kind
     (1, 256, 8, 4, 8, "randn"),
+    (16, 64, 8, 4, 4, "ties"),
+    (48, 128, 4, 2, 6, "extreme"),
+    (64, 256, 8, 4, 16, "zipf"),        # top-16
     (32, 256, 8, 4, 8, "randn"),
     (64, 256, 8, 4, 8, "randn"),
     (65, 256, 8, 4, 8, "randn"),
@@ -607,6 +610,22 @@ def test_prefill_attention(device, lens, Hq, Hkv, qscale):
         ref = F.scaled_dot_product_attention(qs[None], ks[None], vs[None], is_causal=True,
                                              scale=0.0884)[0].transpose(0, 1)
         _close(out[a:b], ref, atol=1e-2, rtol=1e-2)
+
+
+def test_prefill_attention_deterministic(device):
+    """Repeated launches over many ragged sequences (several workgroups per CU, of different
+    lengths) give bit-identical outputs. A row maximum read from the score accumulator before
+    the MFMA has written it changes the softmax only in rounding, so only this catches it."""
+    lens = [267, 1843, 877, 1609, 2030, 939, 2010, 367]
+    g = torch.Generator().manual_seed(11)
+    T = sum(lens)
+    q = torch.randn(T, 16, 128, generator=g).bfloat16().to(device)
+    k = torch.randn(T, 4, 128, generator=g).bfloat16().to(device)
+    v = torch.randn(T, 4, 128, generator=g).bfloat16().to(device)
+    cu = torch.tensor([0] + list(np.cumsum(lens)), dtype=torch.int32).to(device)
+    ref = hip_ops.prefill_attention(q, k, v, cu, max(lens), 0.0884)
+    for _ in range(8):
+        assert torch.equal(hip_ops.prefill_attention(q, k, v, cu, max(lens), 0.0884), ref)
 
 
 def test_prefill_prologue_matches_decode_prologue(device):

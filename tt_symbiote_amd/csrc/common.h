@@ -101,7 +101,10 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const uint4& v) {
 // lane (LDS-DMA, global_load_lds_dwordx4; lds_base wave-uniform, in M0). Written as asm so that
 // the compiler does not add its own (conservative) waits for these LDS writes: the kernels wait
 // for them explicitly (s_waitcnt vmcnt) before the barrier that publishes the data. M0 is written
-// here only; no other instruction of the kernels that use this reads M0.
+// here only; no other instruction of the kernels that use this reads M0. On this generation an
+// LDS-DMA instruction needs one wait state after an SALU write of M0 (else it may take the
+// previous M0, i.e. the previous DMA's destination); the compiler inserts no wait states inside
+// inline asm, hence the s_nop.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 // base and lds_base are wave-uniform by construction; readfirstlane states it where the
@@ -115,7 +118,7 @@ __device__ __forceinline__ void dma16(const uint16_t* base, uint32_t off,
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)g);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(g >> 32));
   const uint64_t gu = ((uint64_t)hi << 32) | (uint64_t)lo;
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(lds), "v"(off),
                "s"((const uint16_t*)(uintptr_t)gu)
                : "memory", "m0");
 }

@@ -61,25 +61,16 @@ __device__ __forceinline__ void pin_operands(const uint4 (&p)[2]) {
                "v"(p[1].y), "v"(p[1].z), "v"(p[1].w));
 }
 
-// v_max_f32 / v_max3_f32 without the canonicalising maxima that fmaxf adds for operands the
-// compiler cannot prove canonical (the scores hold no NaN)
-__device__ __forceinline__ float vmax(float a, float b) {
-  float r;
-  asm("v_max_f32 %0, %1, %2" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-__device__ __forceinline__ float vmax3(float a, float b, float c) {
-  float r;
-  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
-  return r;
-}
-
 // Maximum over lanes l and l^32 (the two lanes that hold one query's keys): v_permlane32_swap
 // of x with itself leaves the other half's value in the second register of the pair.
+// (Maxima are written as compiler-visible operations, never as inline asm, here and below: the
+// compiler inserts no wait states before inline asm that reads an MFMA result, so such an asm
+// could read the accumulator before the MFMA has written it.)
 __device__ __forceinline__ float max_over_halves(float x) {
   const auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
                                                   false);
-  return vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const float a0 = __uint_as_float(a[0]), a1 = __uint_as_float(a[1]);
+  return a0 > a1 ? a0 : a1;
 }
 
 __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
@@ -199,8 +190,12 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
       for (int e = 0; e < 16; ++e) sc[e] = 0.f;
 #pragma unroll
       for (int c = 0; c < 8; ++c) {
-        const uint4 kf = *reinterpret_cast<const uint4*>(st + k_off[c] + 32 * kt * kRowElems);
+        uint4 kf = *reinterpret_cast<const uint4*>(st + k_off[c] + 32 * kt * kRowElems);
         sc = mfma32x32x16(kf, qf[c], sc);
+        // With a zero accumulator the compiler may give the 16-register result the registers of
+        // the (then dead) A operand. An asm that reads and writes kf after the MFMA keeps kf live
+        // across it (and cannot move above it), so the two stay apart.
+        if (c == 0) asm volatile("" : "+v"(kf.x), "+v"(kf.y), "+v"(kf.z), "+v"(kf.w));
       }
       return sc;
     };
@@ -219,9 +214,10 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
             if (key > qrow || key >= L) sc[4 * j + i] = -INFINITY;
           }
       }
-      float mx = vmax3(vmax3(sc[0], sc[1], sc[2]), vmax3(sc[3], sc[4], sc[5]),
-                       vmax3(sc[6], sc[7], sc[8]));
-      mx = vmax3(mx, vmax3(sc[9], sc[10], sc[11]), vmax3(sc[12], sc[13], vmax(sc[14], sc[15])));
+      float mx = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])),
+                       fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(sc[8], sc[9]), fmaxf(sc[10], sc[11])),
+                           fmaxf(fmaxf(sc[12], sc[13]), fmaxf(sc[14], sc[15]))));
       mx = max_over_halves(mx);
       const float mxs = mx * scale_log2;
       const bool grow = mxs > m + kLazyMax;  // true on the first half (m = -inf)
@@ -286,6 +282,11 @@ __global__ __launch_bounds__(256, 2) void prefill_attention_kernel(
   };
 
   load_block(0);
+  // The compiler's own wait for the Q loads, here: it cannot see the waits inside the asm below
+  // and would otherwise place them in the key-block loop, where they would also wait for the
+  // next block's DMA.
+#pragma unroll
+  for (int c = 0; c < 8; ++c) asm volatile("" ::"v"(qf[c].x), "v"(qf[c].y), "v"(qf[c].z), "v"(qf[c].w));
   asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
   // Blocks from kb_mask on hold keys past a query of this wave (the diagonal) or past the
   // sequence and are masked: two loops in sequence (one branch between the two block bodies in
