@@ -131,6 +131,8 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
   __shared__ float s_red[kLinWaves][MT][4][64];
   __shared__ float s_ss[NORM ? kLinWaves : 1][16 * MT];
   __shared__ float s_r[16 * MT];
+  // gamma of the single-batch path (K = 64 * U * kLinWaves), staged once per workgroup
+  __shared__ __align__(16) uint16_t s_g[NORM ? 64 * U * kLinWaves : 1];
   const int col0 = blockIdx.x * 16;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -157,10 +159,13 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
     bool done = false;
     if constexpr (NORM) {
       if (nsteps == U * kLinWaves) {
-        // one batch per wave: activations, weights and gamma in flight together; the sums of
+        // one batch per wave: activations, gamma and weights in flight together; the sums of
         // squares come from the activation registers, and the same registers feed the MFMAs.
         // The activations are issued first, so the norm statistics (which wait for them only;
-        // loads complete in order) are reduced while the weights are still arriving.
+        // loads complete in order) are reduced while the weights are still arriving. The wave's
+        // 512 bytes of gamma take one load (lane l: k = 4l .. 4l+3 of its range) into LDS, read
+        // back after the statistics barrier: the MFMA layout would need eight loads in which
+        // 16 lanes each read the same address, which cost about 1 us of load issue.
         uint4 b[U][2], a[MT][U][2], gm[U][2];
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
@@ -170,18 +175,14 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
             a[mt][s][0] = ldg16(xr[mt] + k);
             a[mt][s][1] = ldg16(xr[mt] + k + 8);
           }
+        const int kw = s_beg << 6;  // this wave's first k
+        const uint2 gl = *reinterpret_cast<const uint2*>(gamma + kw + 4 * lane);
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int s = 0; s < U; ++s) {
           const int k = (s_beg + s) << 6;
           b[s][0] = ldg16(wr + k);
           b[s][1] = ldg16(wr + k + 8);
-        }
-#pragma unroll
-        for (int s = 0; s < U; ++s) {
-          const int k = (s_beg + s) << 6;
-          gm[s][0] = ldg16(gr + k);
-          gm[s][1] = ldg16(gr + k + 8);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -193,6 +194,7 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
           v += __shfl_xor(v, 32);
           if (kq == 0) s_ss[wave][mt * 16 + r16] = v;
         }
+        *reinterpret_cast<uint2*>(&s_g[kw + 4 * lane]) = gl;
         __syncthreads();
         if (threadIdx.x < 16 * MT) {
           float t = 0.f;
@@ -201,6 +203,12 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
           s_r[threadIdx.x] = rsqrtf(t / (float)K + eps);
         }
         __syncthreads();
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          const int k = ((s_beg + s) << 6) + kq * 16;
+          gm[s][0] = *reinterpret_cast<const uint4*>(&s_g[k]);
+          gm[s][1] = *reinterpret_cast<const uint4*>(&s_g[k + 8]);
+        }
         // normalised rows in place, one K-step at a time (a scheduling barrier after each
         // keeps the compiler from converting all of them ahead of the MFMAs)
 #pragma unroll
@@ -309,6 +317,9 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
   __shared__ float s_red[kLinWaves][MT][4][64];
   __shared__ float s_ss[NORM ? kLinWaves : 1][16 * MT];
   __shared__ float s_r[16 * MT];
+  // gamma (K = 64 * U * kLinWaves values), staged once: each wave stores its 512 bytes with
+  // one load before the first pass's statistics barrier, and every pass reads it from LDS
+  __shared__ __align__(16) uint16_t s_g[NORM ? 64 * U * kLinWaves : 1];
   const int col0 = blockIdx.x * 16;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -341,6 +352,10 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
     }
   };
   load_rows(0);
+  if constexpr (NORM) {
+    const uint2 gl = *reinterpret_cast<const uint2*>(gamma + wave * U * 64 + 4 * lane);
+    *reinterpret_cast<uint2*>(&s_g[wave * U * 64 + 4 * lane]) = gl;
+  }
   const float bias_v = bias ? bf16_to_f32(bias[e_col]) : 0.f;
 
   for (int mb = 0; mb < M; mb += 16 * MT) {
@@ -352,14 +367,9 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = floatx4{0.f, 0.f, 0.f, 0.f};
     if constexpr (NORM) {
-      // gamma is reloaded per pass (cache hits) rather than held: the registers go to the
-      // weights
+      // gamma comes from LDS in each pass (after the statistics barrier below), rather than
+      // held in registers: they go to the weights
       uint4 gm[U][2];
-#pragma unroll
-      for (int s = 0; s < U; ++s) {
-        gm[s][0] = ldg16(gamma + k0 + s * 64);
-        gm[s][1] = ldg16(gamma + k0 + s * 64 + 8);
-      }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         float v = 0.f;
@@ -377,6 +387,11 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
         s_r[threadIdx.x] = rsqrtf(t / (float)K + eps);
       }
       __syncthreads();
+#pragma unroll
+      for (int s = 0; s < U; ++s) {
+        gm[s][0] = *reinterpret_cast<const uint4*>(&s_g[k0 + s * 64]);
+        gm[s][1] = *reinterpret_cast<const uint4*>(&s_g[k0 + s * 64 + 8]);
+      }
       // normalised rows in place, one K-step at a time (a scheduling barrier after each keeps
       // the compiler from converting all of them ahead of the MFMAs)
 #pragma unroll
