@@ -524,19 +524,27 @@ void gemm_tile128_kernel(TileArgs p) {
 
   // Step k: wait for its stage (the DMA of step k + 1 may still be in flight), barrier (every
   // wave is also done with step k - 1's stage), issue step k + 2 into that stage, MFMAs. Step k
-  // uses stage k % 3.
+  // uses stage k % 3. A wave whose 64-row band lies wholly past the tile's valid rows (a
+  // segment's last tile) keeps the loads and barriers but skips its fragment reads and MFMAs:
+  // a template flag, so that neither K loop carries a branch.
   const int nk = K / kTK;
+  const bool m_on = wm * 64 < loc.rows;
   issue(0, smem);
   if (nk > 1) issue(1, smem + kStage);
-  int cur = 0;  // stage of step kt (element offset)
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 >= nk) SYM_TILE_SYNC(0);
-    else SYM_TILE_SYNC(3);  // step kt + 1's three loads may still fly
-    const int nxt = cur == 0 ? 2 * kStage : cur - kStage;  // stage of step kt + 2
-    if (kt + 2 < nk) issue(kt + 2, smem + nxt);
-    compute(smem + cur);
-    cur = cur == 2 * kStage ? 0 : cur + kStage;
-  }
+  auto loop = [&](auto with_mfma) {
+    int cur = 0;  // stage of step kt (element offset)
+    for (int kt = 0; kt < nk; ++kt) {
+      if (kt + 1 >= nk) SYM_TILE_SYNC(0);
+      else SYM_TILE_SYNC(3);  // step kt + 1's three loads may still fly
+      const int nxt = cur == 0 ? 2 * kStage : cur - kStage;  // stage of step kt + 2
+      if (kt + 2 < nk) issue(kt + 2, smem + nxt);
+      if constexpr (decltype(with_mfma)::value) compute(smem + cur);
+      cur = cur == 2 * kStage ? 0 : cur + kStage;
+    }
+  };
+  if (m_on) loop(std::true_type{});
+  else loop(std::false_type{});
+  if (!m_on) return;
 
   const int col0 = MODE == kGateUp ? loc.ct * (kTN / 2) + wn * (kWC / 2) : loc.ct * kTN + wn * kWC;
   store_block<MODE, kNJ>(p, acc, loc, wm * 64, col0, lane);
