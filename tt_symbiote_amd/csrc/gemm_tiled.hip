@@ -504,17 +504,19 @@ void gemm_tile128_kernel(TileArgs p) {
 #pragma unroll
     for (int j = 0; j < kNJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](const uint16_t* stage) {
-    u32x4 fa[4], fb[kNJ];
+  // MFMAs of one step over the first NI 16-row sub-tiles of the wave's 64-row band
+  auto compute = [&](auto ni_tag, const uint16_t* stage) {
+    constexpr int NI = decltype(ni_tag)::value;
+    u32x4 fa[NI], fb[kNJ];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
       fa[i] = *reinterpret_cast<const u32x4*>(stage + a_frag0 + i * 16 * kTK);
 #pragma unroll
     for (int j = 0; j < kNJ; ++j)
       fb[j] = *reinterpret_cast<const u32x4*>(stage + b_frag0 + b_row(j) * kTK);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < kNJ; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
@@ -524,27 +526,33 @@ void gemm_tile128_kernel(TileArgs p) {
 
   // Step k: wait for its stage (the DMA of step k + 1 may still be in flight), barrier (every
   // wave is also done with step k - 1's stage), issue step k + 2 into that stage, MFMAs. Step k
-  // uses stage k % 3. A wave whose 64-row band lies wholly past the tile's valid rows (a
-  // segment's last tile) keeps the loads and barriers but skips its fragment reads and MFMAs:
-  // a template flag, so that neither K loop carries a branch.
+  // uses stage k % 3. In a segment's last tile a wave computes only the 16-row sub-tiles of its
+  // 64-row band that hold valid rows (none when the band lies wholly past them) and keeps the
+  // loads and barriers: the sub-tile count is a template parameter, so no K loop carries a
+  // branch.
   const int nk = K / kTK;
-  const bool m_on = wm * 64 < loc.rows;
+  const int ni = min(max((loc.rows - wm * 64 + 15) >> 4, 0), 4);
   issue(0, smem);
   if (nk > 1) issue(1, smem + kStage);
-  auto loop = [&](auto with_mfma) {
+  auto loop = [&](auto ni_tag) {
     int cur = 0;  // stage of step kt (element offset)
     for (int kt = 0; kt < nk; ++kt) {
       if (kt + 1 >= nk) SYM_TILE_SYNC(0);
       else SYM_TILE_SYNC(3);  // step kt + 1's three loads may still fly
       const int nxt = cur == 0 ? 2 * kStage : cur - kStage;  // stage of step kt + 2
       if (kt + 2 < nk) issue(kt + 2, smem + nxt);
-      if constexpr (decltype(with_mfma)::value) compute(smem + cur);
+      if constexpr (decltype(ni_tag)::value > 0) compute(ni_tag, smem + cur);
       cur = cur == 2 * kStage ? 0 : cur + kStage;
     }
   };
-  if (m_on) loop(std::true_type{});
-  else loop(std::false_type{});
-  if (!m_on) return;
+  switch (ni) {
+    case 4: loop(std::integral_constant<int, 4>{}); break;
+    case 3: loop(std::integral_constant<int, 3>{}); break;
+    case 2: loop(std::integral_constant<int, 2>{}); break;
+    case 1: loop(std::integral_constant<int, 1>{}); break;
+    default: loop(std::integral_constant<int, 0>{}); break;
+  }
+  if (ni == 0) return;
 
   const int col0 = MODE == kGateUp ? loc.ct * (kTN / 2) + wn * (kWC / 2) : loc.ct * kTN + wn * kWC;
   store_block<MODE, kNJ>(p, acc, loc, wm * 64, col0, lane);
