@@ -286,22 +286,18 @@ static_assert(kADma == 4 && kBDma == 4, "the prologue wait counts");
 __device__ __forceinline__ int swz(int r) { return r & 7; }
 }  // namespace big
 
+// One 256 x 256 tile at loc (p is a copy: tile_weights moves its output pointer to the tile's
+// plane). The stages are smem + s * kStage, s = 0, 1 (64 KB each: every fragment read of a stage
+// is within the 64 KB immediate offset of an LDS instruction from the stage base).
 template <int MODE>
-__global__ __launch_bounds__(big::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void gemm_tile_kernel(TileArgs p) {
+__device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_t* smem) {
   using namespace big;
-  // stage s = [A | B] at smem + s * kStage (64 KB each): every fragment read of a stage is
-  // within the 64 KB immediate offset of an LDS instruction from the stage base
-  __shared__ __align__(1024) uint16_t smem[2 * kStage];
-
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
   const int wm = wave / kWavesN, wn = wave % kWavesN;
   const int r16 = lane & 15, kq = lane >> 4;
   const int K = p.K;
 
-  TileLoc loc;
-  if (!locate_tile<MODE, kTM>(p, lane, loc)) return;
   const uint16_t* wbase = tile_weights<MODE>(p, loc);
 
   // ---- LDS-DMA sources: this wave fills A rows kARows w .. and B rows kBRows w .. of every
@@ -436,6 +432,110 @@ void gemm_tile_kernel(TileArgs p) {
 
   const int col0 = MODE == kGateUp ? loc.ct * (kTN / 2) + wn * (kWC / 2) : loc.ct * kTN + wn * kWC;
   store_block<MODE, kNJ>(p, acc, loc, wm * 64, col0, lane);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(big::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_tile_kernel(TileArgs p) {
+  using namespace big;
+  __shared__ __align__(1024) uint16_t smem[2 * kStage];
+  TileLoc loc;
+  if (!locate_tile<MODE, kTM>(p, threadIdx.x & 63, loc)) return;
+  big_tile<MODE>(p, loc, smem);
+}
+
+// Segment list of the grouped modes in LDS (at most kPersistSeg segments): the first row tile
+// of every segment (segments past the list: the total), its row count, first row and expert.
+constexpr int kPersistSeg = 512;
+struct SegTable {
+  int pre[kPersistSeg], cnt[kPersistSeg], off[kPersistSeg];
+  uint16_t exp[kPersistSeg];
+  int total;
+};
+
+// Wave 0 reads the segment list (all loads in flight together with n_segments; lane l owns
+// segments 8l .. 8l+7) and scans the row-tile counts of tiles of TM rows into the table.
+template <int TM>
+__device__ __forceinline__ void load_seg_table(const TileArgs& p, SegTable& t) {
+  const int lane = threadIdx.x & 63;
+  if (threadIdx.x >= 64) return;
+  int c[8], o[8], e[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int sg = lane * 8 + i;
+    const bool in = sg < p.max_segments;
+    c[i] = in ? p.seg_count[sg] : 0;
+    o[i] = in ? p.seg_offset[sg] : 0;
+    e[i] = in ? p.seg_expert[sg] : 0;
+  }
+  const int nseg = p.n_segments[0];
+  int pre[8], run = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    pre[i] = run;
+    run += lane * 8 + i < nseg ? (c[i] + TM - 1) / TM : 0;
+  }
+  int x = run;  // inclusive scan of the lanes' tile counts
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int sg = lane * 8 + i;
+    t.pre[sg] = x - run + pre[i];
+    t.cnt[sg] = c[i];
+    t.off[sg] = o[i];
+    t.exp[sg] = (uint16_t)e[i];
+  }
+  if (lane == 63) t.total = x;
+}
+
+// Row tile g (of TM rows) of the table: the last segment whose first row tile is <= g (binary
+// search, the same in every lane).
+template <int TM>
+__device__ __forceinline__ TileLoc seg_tile(const SegTable& t, int g, int ct) {
+  int lo = 0, hi = kPersistSeg - 1;
+  while (lo < hi) {
+    const int md = (lo + hi + 1) >> 1;
+    if (t.pre[md] <= g) lo = md;
+    else hi = md - 1;
+  }
+  const int rt = g - t.pre[lo];
+  TileLoc loc;
+  loc.e = __builtin_amdgcn_readfirstlane((int)t.exp[lo]);
+  loc.row0 = __builtin_amdgcn_readfirstlane(t.off[lo] + rt * TM);
+  loc.rows = __builtin_amdgcn_readfirstlane(min(TM, t.cnt[lo] - rt * TM));
+  loc.ct = __builtin_amdgcn_readfirstlane(ct);
+  loc.z = 0;
+  return loc;
+}
+
+// Grouped modes of the 256 x 256 tiles on a persistent grid (one workgroup per CU, a multiple
+// of 8): the segment list is read and scanned once per workgroup into LDS and each tile then
+// finds its segment there. gemm_tile_kernel's per-tile lookup is a memory round trip behind
+// the other workgroups' operand loads that no second workgroup on the CU hides; here only a
+// workgroup's first tile pays it. Workgroup b takes linear ids b, b + G, ... through xcd_tile,
+// so it stays on its XCD's contiguous run of tiles.
+template <int MODE>
+__global__ __launch_bounds__(big::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void gemm_tile_persistent(TileArgs p, int nx) {
+  using namespace big;
+  __shared__ __align__(1024) uint16_t smem[2 * kStage];
+  __shared__ SegTable tab;
+  load_seg_table<kTM>(p, tab);
+  __syncthreads();
+  const int total = tab.total * nx;  // (row tile, column tile) pairs
+  for (int lin = blockIdx.x;; lin += gridDim.x) {
+    const int t = xcd_tile(lin, total);
+    if (t < 0) break;
+    const int g = t / nx;
+    const TileLoc loc = seg_tile<kTM>(tab, g, t - g * nx);
+    // every wave is done with the previous tile's stages before this tile's DMA refills them
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    big_tile<MODE>(p, loc, smem);
+  }
 }
 
 // ================================================================================================
@@ -687,8 +787,15 @@ extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int row
   p.out_bf16 = (uint16_t*)h;
   (void)hipGetLastError();
   namespace C = big;
-  hipLaunchKernelGGL((gemm_tile_kernel<kGateUp>),
-                     dim3((I + C::kTN / 2 - 1) / (C::kTN / 2), rows / C::kTM + max_segments),
+  const int nx = (I + C::kTN / 2 - 1) / (C::kTN / 2);
+  if (max_segments <= kPersistSeg) {
+    // one workgroup per CU, a multiple of 8 (one run of tiles per XCD)
+    const int grid = std::max(8, sym_host::cu_count() / 8 * 8);
+    hipLaunchKernelGGL((gemm_tile_persistent<kGateUp>), dim3(grid), dim3(C::kThreads), 0,
+                       (hipStream_t)stream, p, nx);
+    return sym_host::check_launch("gemm_tile_persistent");
+  }
+  hipLaunchKernelGGL((gemm_tile_kernel<kGateUp>), dim3(nx, rows / C::kTM + max_segments),
                      dim3(C::kThreads), 0, (hipStream_t)stream, p);
   return sym_host::check_launch("gemm_tile_kernel");
 }
