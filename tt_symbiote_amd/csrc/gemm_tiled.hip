@@ -234,8 +234,11 @@ __device__ __forceinline__ void store_block(const TileArgs& p, const floatx4 (&a
         float h[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
+          // silu(g) = g / (1 + 2^(-g log2(e))) by v_exp_f32 and v_rcp_f32 (about 1 ulp each;
+          // h is rounded to bf16 next). g -> -inf: 1 / inf = 0; g -> +inf: 1 / 1.
           const float g = acc[i][j][q], u = acc[i][j + NJ / 2][q];
-          h[q] = g / (1.0f + expf(-g)) * u;
+          const float e = __builtin_amdgcn_exp2f(g * -1.44269504f);
+          h[q] = g * __builtin_amdgcn_rcpf(1.0f + e) * u;
         }
         *reinterpret_cast<uint2*>(p.out_bf16 + orow * p.N + col) =
             make_uint2(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]));
