@@ -345,6 +345,8 @@ def test_grouped_swiglu(device, T, E, H, I, top_k, skew, kernel):
     (130, 256, 576, True, False, torch.bfloat16),
     (77, 400, 192, True, True, torch.float32),          # N not a multiple of the 256-wide tile
     (300, 16, 128, False, False, torch.bfloat16),
+    (8500, 2048, 128, True, True, torch.float32),       # 256 whole tiles + 128-row tail tiles
+    (9000, 2304, 128, False, False, torch.bfloat16),    # 252 whole tiles + tail, ragged last tile
 ])
 def test_gemm_tiled(device, M, N, K, bias, res, out_dtype):
     g = torch.Generator().manual_seed(M + N + K)
