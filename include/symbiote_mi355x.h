@@ -379,6 +379,9 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
  *   expert). y is fp32, or bf16 when y_bf16 != 0 (half the bytes written here and read back by
  *   sym_moe_unpermute_combine). H % 64 == 0, I % 64 == 0; x / h, the weights and h / y
  *   16-byte aligned; x, h and one expert's weights each under 4 GB.
+ *   sym_moe_gate_up_tiled hands out its tiles from a per-device ticket counter that each launch
+ *   leaves at zero: its launches on one device must not overlap (use one stream, or order the
+ *   streams); replaying a captured launch is fine.
  */
 int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
                   int N, int K, void* out, int out_fp32, void* stream);

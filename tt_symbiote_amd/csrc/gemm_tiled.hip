@@ -305,8 +305,14 @@ __device__ __forceinline__ int swz(int r) { return r & 7; }
 // One 256 x 256 tile at loc (p is a copy: tile_weights moves its output pointer to the tile's
 // plane). The stages are smem + s * kStage, s = 0, 1 (64 KB each: every fragment read of a stage
 // is within the 64 KB immediate offset of an LDS instruction from the stage base).
-template <int MODE>
-__device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_t* smem) {
+// hook() runs in every thread after the K loop, before the epilogue (the persistent kernel
+// hands out its next tile there, when no operand load of the tile is in flight).
+struct NoHook {
+  __device__ void operator()() const {}
+};
+template <int MODE, typename Hook = NoHook>
+__device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_t* smem,
+                                         Hook hook = Hook{}) {
   using namespace big;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
@@ -444,6 +450,7 @@ __device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_
   };
   if (m_on) loop(std::true_type{});
   else loop(std::false_type{});
+  hook();
   if (!m_on) return;
 
   const int col0 = MODE == kGateUp ? loc.ct * (kTN / 2) + wn * (kWC / 2) : loc.ct * kTN + wn * kWC;
@@ -528,29 +535,66 @@ __device__ __forceinline__ TileLoc seg_tile(const SegTable& t, int g, int ct) {
   return loc;
 }
 
+// Tile tickets of gemm_tile_persistent, one counter per XCD. Zero between launches: the
+// workgroup that draws an XCD's last ticket resets its counter. Launches that overlap on one
+// device (different streams) would share them, so such launches must be stream-ordered.
+__device__ int g_tile_ticket[8];
+
 // Grouped modes of the 256 x 256 tiles on a persistent grid (one workgroup per CU, a multiple
 // of 8): the segment list is read and scanned once per workgroup into LDS and each tile then
 // finds its segment there. gemm_tile_kernel's per-tile lookup is a memory round trip behind
 // the other workgroups' operand loads that no second workgroup on the CU hides; here only a
-// workgroup's first tile pays it. Workgroup b takes linear ids b, b + G, ... through xcd_tile,
-// so it stays on its XCD's contiguous run of tiles.
+// workgroup's first tile pays it. Workgroups are dispatched to the XCDs round-robin by id, so
+// XCD x = blockIdx.x % 8 owns the contiguous run of tiles that xcd_tile gives it (the column
+// tiles of a row tile and the row tiles of an expert meet in its L2). Its W = gridDim.x / 8
+// workgroups take the run's first W tiles in order and then draw the rest from the XCD's
+// ticket counter: tiles of a segment's last rows are shorter, and a static share would leave
+// the workgroups that drew several whole tiles last. Thread 0 draws one tile ahead (the ticket
+// for the tile after the current one is drawn at the current one's hook, or at the start), so
+// the fetch-add has a whole tile to return. Tickets 0 .. run - 1 are drawn, one per tile of
+// the run (a ticket past the run ends the drawing workgroup); whoever reads run - 1 is the
+// last to touch the counter and resets it.
 template <int MODE>
 __global__ __launch_bounds__(big::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_tile_persistent(TileArgs p, int nx) {
   using namespace big;
   __shared__ __align__(1024) uint16_t smem[2 * kStage];
   __shared__ SegTable tab;
+  __shared__ int s_next;
   load_seg_table<kTM>(p, tab);
   __syncthreads();
   const int total = tab.total * nx;  // (row tile, column tile) pairs
-  for (int lin = blockIdx.x;; lin += gridDim.x) {
-    const int t = xcd_tile(lin, total);
-    if (t < 0) break;
+  const int x = blockIdx.x & 7, wpx = gridDim.x >> 3;
+  const int q = total >> 3, r = total & 7;
+  const int run0 = x * q + min(x, r), run = q + (x < r ? 1 : 0);  // this XCD's tiles
+  // a per-lane (to the compiler: divergent) address, so the fetch-add is issued as it stands
+  // and its result is waited for only where it is used
+  int zero = 0;
+  asm volatile("" : "+v"(zero));
+  int* ticket = g_tile_ticket + x + zero;
+  int i = blockIdx.x >> 3;  // index in the run
+  int pend = 0;             // thread 0: the ticket drawn for the tile after the current one
+  if (threadIdx.x == 0 && i < run)
+    pend = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  while (i < run) {
+    const int t = run0 + i;
     const int g = t / nx;
     const TileLoc loc = seg_tile<kTM>(tab, g, t - g * nx);
-    // every wave is done with the previous tile's stages before this tile's DMA refills them
+    // every wave is done with the previous tile's stages (and s_next) before this tile's DMA
+    // refills them
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-    big_tile<MODE>(p, loc, smem);
+    big_tile<MODE>(p, loc, smem, [&]() {
+      if (threadIdx.x == 0) {
+        const int nxt = wpx + pend;
+        if (pend == run - 1)
+          __hip_atomic_store(ticket, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (nxt < run)
+          pend = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_next = nxt;
+      }
+    });
+    __syncthreads();
+    i = __builtin_amdgcn_readfirstlane(s_next);
   }
 }
 
