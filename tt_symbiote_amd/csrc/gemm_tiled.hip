@@ -9,13 +9,14 @@
 // 16 rows x 64 bytes (a 32-column step of K-major rows) reaches ~30 B/clk per CU from L2, one of
 // 8 rows x 128 bytes ~50 B/clk, while LDS reads (~190 B/clk) and back-to-back MFMAs (94% of
 // peak) have room; and the chip clocks down to 1.5-2.1 GHz under these kernels. Two tile shapes:
-//   gemm_tile_kernel (dense projections, grouped gate/up): 256 x 256 tiles, one
+//   gemm_tile_kernel / gemm_tile_persistent (dense projections; grouped gate/up and down on a
+//     persistent grid while the segment list has at most 512 entries): 256 x 256 tiles, one
 //     workgroup of 8 waves per CU, each wave a 64 x 128 block (4 x 8 v_mfma_f32_16x16x32_bf16
 //     tiles). The K loop moves 64 columns per step (128-byte rows: whole cache lines) through two
 //     64 KB LDS stages; each step is computed in two 32-column halves whose fragment reads
 //     overlap the other half's MFMAs, with one barrier per step.
-//   gemm_tile128_kernel (grouped down projection, K = I = 512: few steps per tile; router
-//     logits, N = E = 256: few tiles): 128 x 256 tiles, two workgroups of 8 waves per CU, each
+//   gemm_tile128_kernel (router logits, N = E = 256: few tiles; grouped down projection over
+//     longer segment lists): 128 x 256 tiles, two workgroups of 8 waves per CU, each
 //     wave a 64 x 64 block; 32 columns per step through a 3-stage 72 KB ring. The second
 //     workgroup covers a tile's prologue (segment lookup, first loads) and epilogue, which a
 //     one-workgroup shape leaves bare at 16 steps.
@@ -925,6 +926,12 @@ extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
   if (y_bf16) p.out_bf16 = (uint16_t*)y;
   else p.out_f32 = (float*)y;
   (void)hipGetLastError();
+  if (max_segments <= kPersistSeg) {
+    const int grid = std::max(8, sym_host::cu_count() / 8 * 8);
+    hipLaunchKernelGGL((gemm_tile_persistent<kDown>), dim3(grid), dim3(big::kThreads), 0,
+                       (hipStream_t)stream, p, (H + big::kTN - 1) / big::kTN);
+    return sym_host::check_launch("gemm_tile_persistent");
+  }
   namespace C = mid;
   hipLaunchKernelGGL((gemm_tile128_kernel<kDown>),
                      dim3((H + C::kTN - 1) / C::kTN, rows / C::kTM + max_segments),
