@@ -368,7 +368,7 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
 
 /* ---------------------------------------------------------------------------------------
  * Tiled GEMMs for prefill-size batches (MFMA-bound; 256 x 256 output tiles, 128 x 256 for the
- * grouped down projection).
+ * grouped down projection over segment lists of more than 512 entries).
  * sym_gemm_bf16: out[M, N] = a[M, K] . w[N, K]^T (+ bias[N] bf16) (+ residual[M, N] fp32),
  *   bf16 out, or fp32 when out_fp32 != 0. Replaces the QKV / dense projections at sequence length
  *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 16 == 0, K % 64 == 0; a, w, out and
@@ -379,9 +379,10 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
  *   expert). y is fp32, or bf16 when y_bf16 != 0 (half the bytes written here and read back by
  *   sym_moe_unpermute_combine). H % 64 == 0, I % 64 == 0; x / h, the weights and h / y
  *   16-byte aligned; x, h and one expert's weights each under 4 GB.
- *   sym_moe_gate_up_tiled hands out its tiles from a per-device ticket counter that each launch
- *   leaves at zero: its launches on one device must not overlap (use one stream, or order the
- *   streams); replaying a captured launch is fine.
+ *   With at most 512 segments, sym_moe_gate_up_tiled and sym_moe_down_tiled hand out their
+ *   tiles from a per-device ticket counter that each launch leaves at zero: their launches on one
+ *   device must not overlap (use one stream, or order the streams); replaying a captured launch
+ *   is fine.
  */
 int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
                   int N, int K, void* out, int out_fp32, void* stream);
