@@ -274,13 +274,64 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v + dpp_row<0x140>(v);
 }
 
+// Live workgroups first. With compact set, the workgroup with linear id L (x fastest over the
+// grid (splits, Hkv, B)) takes kv head L % Hkv and item L / Hkv, where sequence b owns
+// max(ceil(ctx_b / S), 1) consecutive items in sequence order (one for a sequence with nothing
+// cached, which writes the zero output): the workgroups of absent splits all come after the
+// live ones in dispatch order instead of between them. Lane l reads the positions of sequences
+// 4l .. 4l + 3 (B <= 256); a prefix scan over the lanes and a ballot find the item's sequence.
+// Returns false past the last item. Results are wave-uniform.
+__device__ __forceinline__ bool decode_item(const int32_t* __restrict__ positions, int B,
+                                            int max_context, int S, int Hkv, int& split, int& g,
+                                            int& b) {
+  const int L = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+  g = L % Hkv;
+  const int item = L / Hkv;
+  const int lane = threadIdx.x & 63;
+  int cnt[4], pre[4], run = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int sq = lane * 4 + i;
+    int c = 0;
+    if (sq < B) {
+      const int ctx = min(positions[sq] + 1, max_context);
+      c = ctx <= 0 ? 1 : (ctx + S - 1) / S;
+    }
+    cnt[i] = c;
+    pre[i] = run;
+    run += c;
+  }
+  int x = run;  // inclusive scan over the lanes
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int y = __shfl_up(x, d);
+    if (lane >= d) x += y;
+  }
+  if (item >= __shfl(x, 63)) return false;
+  const int excl = x - run;
+  const int l = __ffsll((long long)__ballot(item >= excl && item < x)) - 1;
+  int bb = 0, sp = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int st = __shfl(excl + pre[i], l);
+    const int c = __shfl(cnt[i], l);
+    if (item >= st && item < st + c) {
+      bb = l * 4 + i;
+      sp = item - st;
+    }
+  }
+  b = __builtin_amdgcn_readfirstlane(bb);
+  split = __builtin_amdgcn_readfirstlane(sp);
+  return true;
+}
+
 template <int G, int TPW, bool FUSED>
 __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_kernel(
     const uint16_t* __restrict__ q, FusedQKV fq, uint16_t* __restrict__ k_pool,
     uint16_t* __restrict__ v_pool, const int32_t* __restrict__ block_tables,
     const int32_t* __restrict__ positions, int Hkv, int block_size, int mbps, int num_blocks,
     int max_context, float scale_log2, float* __restrict__ ws_o, float* __restrict__ ws_ml,
-    int max_splits, uint16_t* __restrict__ out) {
+    int max_splits, uint16_t* __restrict__ out, int compact) {
   constexpr int D = kHeadDim;
   constexpr int SPLIT = 4 * TPW;   // tokens per workgroup
   constexpr int KT = TPW / 16;     // 16-token MFMA tiles per wave
@@ -293,7 +344,8 @@ __global__ __launch_bounds__(kAttnThreads, kBf16MinBlocks) void paged_decode_ker
   __shared__ unsigned s_row[SPLIT];  // K/V pool row of each token (always an in-bounds row)
   __shared__ int s_ok[SPLIT];        // token is inside the split and its page-table entry is valid
 
-  const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  if (compact && !decode_item(positions, gridDim.z, max_context, SPLIT, Hkv, split, g, b)) return;
   const int Hq = Hkv * G;
   const int tid = threadIdx.x;
   const int pos = positions[b];
@@ -876,7 +928,7 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
     const int32_t* __restrict__ block_tables, const int32_t* __restrict__ positions, int Hkv,
     int block_size, int mbps, int num_blocks, int max_context, float scale_log2,
     float* __restrict__ ws_o, float* __restrict__ ws_ml, int max_splits,
-    uint16_t* __restrict__ out) {
+    uint16_t* __restrict__ out, int compact) {
   constexpr int D = kHeadDim;
   constexpr int TPW = kTPW8;
   constexpr int SPLIT = kSplit8;
@@ -888,7 +940,8 @@ __global__ __launch_bounds__(kAttnThreads, G >= 8 ? 1 : kFp8MinBlocks) void page
   __shared__ float s_stat[2][G][4];  // each wave's max and sum of its tokens, per head
   __shared__ unsigned s_row[SPLIT];
 
-  const int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  int split = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
+  if (compact && !decode_item(positions, gridDim.z, max_context, SPLIT, Hkv, split, g, b)) return;
   const int Hq = Hkv * G;
   const int tid = threadIdx.x;
   const int pos = positions[b];
@@ -1351,6 +1404,12 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
   // mapping from row to row; the extra split starts at or past max_context and exits at once.
   // (fp8 batch 128, 1024-8192 tokens: 32 -> 33 splits, 153 -> 123 us.)
   const dim3 grid(max_splits | 1, Hkv, B), block(kAttnThreads);
+  // live workgroups first in dispatch order (decode_item), up to 256 sequences, for the bf16
+  // cache: batch 32 with 128-4096 cached tokens (about one round of workgroups), split kernel
+  // 26.6-26.7 against 27.6-27.7 us. The fp8 cache's batch 128 with 1024-8192 tokens (several
+  // rounds) runs slower that way (120.6-120.9 against 115.3-116.5 us) and keeps the odd-width
+  // grid order.
+  const int compact = !fp8 && B <= 256 ? 1 : 0;
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* kp = (uint16_t*)k_pool;
   uint16_t* vp = (uint16_t*)v_pool;
@@ -1362,12 +1421,12 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
     hipLaunchKernelGGL((paged_decode_fp8_kernel<GG, FF>), grid, block, 0, s, qq, f, kp8, vp8,   \
                        k_scale, v_scale, block_tables, positions, Hkv, block_size,              \
                        max_blocks_per_seq, num_blocks, max_context, scale_log2, ws_o, ws_ml,    \
-                       max_splits, (uint16_t*)out);                                             \
+                       max_splits, (uint16_t*)out, compact);                                    \
   else                                                                                          \
     hipLaunchKernelGGL((paged_decode_kernel<GG, kTPW, FF>), grid, block, 0, s, qq, f, kp, vp,   \
                        block_tables, positions, Hkv, block_size, max_blocks_per_seq,            \
                        num_blocks, max_context, scale_log2, ws_o, ws_ml, max_splits,            \
-                       (uint16_t*)out)
+                       (uint16_t*)out, compact)
 #define SYM_LAUNCH_DECODE_G(FF)               \
   switch (G) {                                \
     case 1: SYM_LAUNCH_DECODE(1, FF); break;  \
