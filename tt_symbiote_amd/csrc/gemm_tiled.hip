@@ -366,8 +366,10 @@ __device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_
   auto b_row = [](int j) {
     return MODE == kGateUp ? (j < kNJ / 2 ? 0 : kTN / 2) + (j % (kNJ / 2)) * 16 : j * 16;
   };
-  // a wave whose 64 rows are all past `rows` computes nothing (it still loads and syncs)
-  const bool m_on = wm * 64 < loc.rows;
+  // the wave computes the first ni 16-row sub-tiles of its 64-row band that hold valid rows; a
+  // wave whose 64 rows are all past `rows` computes nothing (it still loads and syncs)
+  const int ni = min(max((loc.rows - wm * 64 + 15) >> 4, 0), 4);
+  const bool m_on = ni > 0;
 
   floatx4 acc[4][kNJ];
 #pragma unroll
@@ -377,29 +379,35 @@ __device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_
 
   // fragments of one 32-column half: [0..3] A rows, [4..] B columns
   constexpr int kNF = 4 + kNJ;
-  auto read_frags = [&](const uint16_t* stage, int slot, u32x4 (&f)[kNF]) {
+  // NI: sub-tiles of the band computed (A fragments read for those only)
+  auto read_frags = [&](auto ni_tag, const uint16_t* stage, int slot, u32x4 (&f)[kNF]) {
+    constexpr int NI = decltype(ni_tag)::value;
     const uint16_t* sA = stage + a_frag0 + slot;
     const uint16_t* sB = stage + b_frag0 + slot;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = *reinterpret_cast<const u32x4*>(sA + i * 16 * kTK);
+    for (int i = 0; i < NI; ++i) f[i] = *reinterpret_cast<const u32x4*>(sA + i * 16 * kTK);
 #pragma unroll
     for (int j = 0; j < kNJ; ++j) f[4 + j] = *reinterpret_cast<const u32x4*>(sB + b_row(j) * kTK);
   };
-  auto mfmas = [&](const u32x4 (&f)[kNF]) {  // transposed tiles (B first), see store_block
+  auto mfmas = [&](auto ni_tag, const u32x4 (&f)[kNF]) {  // transposed tiles (B first), see store_block
+    constexpr int NI = decltype(ni_tag)::value;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < NI; ++i)
 #pragma unroll
       for (int j = 0; j < kNJ; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             __builtin_bit_cast(bf16x8, f[4 + j]), __builtin_bit_cast(bf16x8, f[i]), acc[i][j],
             0, 0, 0);
   };
-  // one LDS read between every two MFMAs (the reads feed the other half's MFMAs)
-  auto interleave = [&]() {
+  // one LDS read between every two MFMAs (the reads feed the other half's MFMAs); the whole
+  // band only (partial bands leave the order to the compiler)
+  auto interleave = [&](auto ni_tag) {
+    if constexpr (decltype(ni_tag)::value == 4) {
 #pragma unroll
-    for (int i = 0; i < kNF; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      for (int i = 0; i < kNF; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+      }
     }
   };
 
@@ -409,8 +417,8 @@ __device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_
   // MFMAs of half 1 while half 0 of step kt + 1 is read.
   const int nk = K / kTK;
   auto stage_of = [&](int kt) { return smem + (kt & 1) * kStage; };
-  auto loop = [&](auto with_mfma) {
-    constexpr bool kMfma = decltype(with_mfma)::value;
+  auto loop = [&](auto ni_tag) {
+    constexpr bool kMfma = decltype(ni_tag)::value > 0;
     u32x4 fa[kNF], fb[kNF];
     // the weight rows of steps 0 and 1 go first: the A rows may wait for their row indices
     // (GATE_UP gathers them). Step 0 in, step 1's A loads (or, for a wave without A rows, its
@@ -428,29 +436,34 @@ __device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_
     } else {
       SYM_TILE_SYNC(0);
     }
-    if constexpr (kMfma) read_frags(smem, slot0, fa);
+    if constexpr (kMfma) read_frags(ni_tag, smem, slot0, fa);
     for (int kt = 0; kt < nk - 1; ++kt) {
       if constexpr (kMfma) {
-        read_frags(stage_of(kt), slot1, fb);
-        mfmas(fa);
-        interleave();
+        read_frags(ni_tag, stage_of(kt), slot1, fb);
+        mfmas(ni_tag, fa);
+        interleave(ni_tag);
       }
       SYM_TILE_SYNC(0);
       if (kt + 2 < nk) issue(kt + 2, smem + (kt & 1) * kStage);
       if constexpr (kMfma) {
-        read_frags(stage_of(kt + 1), slot0, fa);
-        mfmas(fb);
-        interleave();
+        read_frags(ni_tag, stage_of(kt + 1), slot0, fa);
+        mfmas(ni_tag, fb);
+        interleave(ni_tag);
       }
     }
     if constexpr (kMfma) {  // the last step
-      read_frags(stage_of(nk - 1), slot1, fb);
-      mfmas(fa);
-      mfmas(fb);
+      read_frags(ni_tag, stage_of(nk - 1), slot1, fb);
+      mfmas(ni_tag, fa);
+      mfmas(ni_tag, fb);
     }
   };
-  if (m_on) loop(std::true_type{});
-  else loop(std::false_type{});
+  switch (ni) {
+    case 4: loop(std::integral_constant<int, 4>{}); break;
+    case 3: loop(std::integral_constant<int, 3>{}); break;
+    case 2: loop(std::integral_constant<int, 2>{}); break;
+    case 1: loop(std::integral_constant<int, 1>{}); break;
+    default: loop(std::integral_constant<int, 0>{}); break;
+  }
   hook();
   if (!m_on) return;
 
