@@ -83,7 +83,9 @@ __device__ __forceinline__ void top2_merge(float& t1, float& t2, float o1, float
 // The partner patterns used for the group top-2 (xor 1, xor 2, half mirror, mirror, then xor 16
 // and xor 32) always pair disjoint lane sets, so no expert is counted twice.
 // Logits of token t for this lane's experts: all partial sums loaded unconditionally (one
-// batch of EPL * n_parts loads), then added left to right.
+// batch of EPL * kLogitParts loads, parts past n_parts repeat the last one and are not added),
+// then added left to right. (A load under q < n_parts would be waited for at the end of its
+// branch: one round trip per part.)
 template <int EPL>
 __device__ __forceinline__ void load_token_logits(const float* __restrict__ logits, int n_parts,
                                                   size_t part_stride, int t, int E, int lane,
@@ -92,7 +94,7 @@ __device__ __forceinline__ void load_token_logits(const float* __restrict__ logi
   for (int q = 0; q < kLogitParts; ++q)
 #pragma unroll
     for (int j = 0; j < EPL; ++j)
-      parts[q][j] = q < n_parts ? logits[q * part_stride + (size_t)t * E + lane * EPL + j] : 0.f;
+      parts[q][j] = logits[(size_t)min(q, n_parts - 1) * part_stride + (size_t)t * E + lane * EPL + j];
 }
 
 template <int EPL>
