@@ -379,22 +379,25 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
  *   expert). y is fp32, or bf16 when y_bf16 != 0 (half the bytes written here and read back by
  *   sym_moe_unpermute_combine). H % 64 == 0, I % 64 == 0; x / h, the weights and h / y
  *   16-byte aligned; x, h and one expert's weights each under 4 GB.
- *   With at most 512 segments, sym_moe_gate_up_tiled and sym_moe_down_tiled hand out their
- *   tiles from a per-device ticket counter that each launch leaves at zero: their launches on one
- *   device must not overlap (use one stream, or order the streams); replaying a captured launch
- *   is fine.
+ *   workspace: sym_moe_tiled_workspace_bytes() bytes (8 per-XCD tile counters), zeroed by the
+ *   caller before its first use. With at most 512 segments the two kernels hand out their tiles
+ *   from these counters, and every launch leaves them at zero again, so one workspace serves
+ *   any number of stream-ordered launches (and graph replays). Launches that may overlap in time
+ *   (on different streams) must use different workspaces. A smaller workspace returns
+ *   SYM_ERR_WORKSPACE.
  */
+size_t sym_moe_tiled_workspace_bytes(void);
 int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
                   int N, int K, void* out, int out_fp32, void* stream);
 int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int rows,
                           const int32_t* sorted_tokens, const int32_t* seg_expert,
                           const int32_t* seg_offset, const int32_t* seg_count,
                           const int32_t* n_segments, int max_segments, const void* w_gate_up,
-                          void* h, void* stream);
+                          void* h, void* workspace, size_t workspace_bytes, void* stream);
 int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows, const int32_t* seg_expert,
                        const int32_t* seg_offset, const int32_t* seg_count,
                        const int32_t* n_segments, int max_segments, const void* w_down, void* y,
-                       int y_bf16, void* stream);
+                       int y_bf16, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Model ends of greedy generation (the embedding and final-norm swap of TTNNBailingMoeV2Model,

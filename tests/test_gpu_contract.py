@@ -118,6 +118,16 @@ def test_decoder_layer_decode_without_cache_position_uses_the_counter(device):
         assert cache.get_seq_length(0) == 8
     assert torch.equal(outs[0], outs[1])
     assert torch.equal(caches[0].key_cache(0), caches[1].key_cache(0))
+    # a prompt continuing the cached sequences is refused whatever device its positions are on
+    # (the host counter is checked), and nothing is written
+    k_before = caches[0].key_cache(0).clone()
+    for pos in (torch.arange(8, 15, device=device), torch.arange(8, 15), None):
+        with pytest.raises(NotImplementedError, match="cached position"):
+            layer(prompt, past_key_values=caches[0], cache_position=pos)
+    assert torch.equal(caches[0].key_cache(0), k_before) and caches[0].get_seq_length(0) == 8
+    caches[0].reset()
+    layer(prompt, past_key_values=caches[0], cache_position=torch.arange(7, device=device))
+    assert caches[0].get_seq_length(0) == 7
 
 
 def _first_divergence(a: torch.Tensor, b: torch.Tensor):

@@ -307,6 +307,11 @@ def _gemm_case(T, E, H, I, top_k, seed, device, with_shared=True, skew=False):
     (200, 64, 256, 128, 6, True),       # segments of > 64 rows (several passes)
     (700, 64, 512, 256, 8, True),       # segments of several 128-row tiles
     (300, 64, 512, 192, 6, True),       # I not a multiple of the 128 h columns of a tile
+    # 513 segment entries (E = 512 + shared): the tiled GEMMs leave the persistent kernel for
+    # the per-tile lookup kernels (gemm_tile_kernel gate/up, gemm_tile128_kernel down)
+    (700, 512, 512, 256, 8, True),      # skewed: segments spanning several 128- and 256-row tiles
+    (300, 512, 512, 192, 6, True),      # and I not a multiple of 128
+    (40, 512, 512, 128, 8, False),      # many one- and two-row segments
 ])
 def test_grouped_swiglu(device, T, E, H, I, top_k, skew, kernel):
     x, wgu, wd, res = _gemm_case(T, E, H, I, top_k, seed=T + E, device=device, skew=skew)
@@ -336,6 +341,56 @@ def test_grouped_swiglu(device, T, E, H, I, top_k, skew, kernel):
                                            kernel=kernel, y_dtype=torch.bfloat16)
         assert yb.dtype == torch.bfloat16
         assert torch.equal(yb.cpu(), yk.bfloat16())
+
+
+def test_grouped_tiled_workspace_reentrant(device):
+    """The tiled grouped GEMMs keep their tile counters in the caller's workspace: two streams
+    running prefill-size launches at the same time, each with its own workspace, give the bytes
+    of serial runs, and back-to-back launches with different segment lists on one workspace
+    leave it zeroed."""
+    H, I, E = 2048, 512, 256
+    cases = [_gemm_case(T, E, H, I, 8, seed=T, device=device, skew=skew)
+             for T, skew in ((1500, True), (900, False))]
+    dev_cases = [(x.to(device), res, wgu.to(device), wd.to(device))
+                 for x, wgu, wd, res in cases]
+
+    def run(i, ws):
+        x, res, wgu, wd = dev_cases[i]
+        return hip_ops.moe_grouped_swiglu(x, res, wgu, wd, kernel="tiled",
+                                          y_dtype=torch.bfloat16, workspace=ws)
+
+    serial = [tuple(t.clone() for t in run(i, hip_ops.moe_tiled_workspace(device)))
+              for i in range(2)]
+    # one workspace, different segment lists back to back
+    ws = hip_ops.moe_tiled_workspace(device)
+    for i in (0, 1, 0, 1, 1, 0):
+        h, y = run(i, ws)
+        assert torch.equal(h, serial[i][0]) and torch.equal(y, serial[i][1])
+    torch.cuda.synchronize()
+    assert int(ws.count_nonzero()) == 0
+    # two default-priority streams at once, a workspace each
+    streams = [torch.cuda.Stream(device), torch.cuda.Stream(device)]
+    wss = [hip_ops.moe_tiled_workspace(device) for _ in range(2)]
+    torch.cuda.synchronize()
+    for rep in range(4):
+        outs = [None, None]
+        for i in (0, 1):
+            with torch.cuda.stream(streams[i]):
+                outs[i] = run(i, wss[i])
+        torch.cuda.synchronize()
+        for i in (0, 1):
+            assert torch.equal(outs[i][0], serial[i][0]), (rep, i, "h")
+            assert torch.equal(outs[i][1], serial[i][1]), (rep, i, "y")
+    assert all(int(w.count_nonzero()) == 0 for w in wss)
+
+
+def test_grouped_tiled_workspace_checked(device):
+    x, wgu, wd, res = _gemm_case(300, 64, 512, 128, 4, seed=1, device=device)
+    small = torch.zeros(hip_ops._lib.query("sym_moe_tiled_workspace_bytes") - 4,
+                        dtype=torch.uint8, device=device)
+    with pytest.raises(hip_ops._lib.SymbioteKernelError, match="workspace"):
+        hip_ops.moe_grouped_swiglu(x.to(device), res, wgu.to(device), wd.to(device),
+                                   kernel="tiled", workspace=small)
 
 
 @pytest.mark.parametrize("M,N,K,bias,res,out_dtype", [

@@ -53,3 +53,33 @@ def test_noalloc_decode_rejects_requests_beyond_its_scratch(device):
     out = torch.empty_like(q)
     with pytest.raises(SymbioteKernelError, match="scratch"):
         hip_ops.paged_gqa_decode_noalloc(q, kp, kp, pt, pos, 0.1, out)
+
+
+def test_noalloc_decode_in_a_captured_graph(device):
+    """Captured in a HIP graph (the callers it is for) and replayed with new queries and shorter
+    contexts written eagerly between replays: every replay equals sym_paged_gqa_decode."""
+    scale = 128 ** -0.5
+    ctx, q, (kp, vp, pt, pos) = _case(device, 16, 64, 2048, 23)
+    out = torch.empty_like(q)
+    # the first call locates the scratch array; it runs before the capture, on the side stream
+    # the capture uses
+    side = torch.cuda.Stream(device)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        hip_ops.paged_gqa_decode_noalloc(q, kp, vp, pt, pos, scale, out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        hip_ops.paged_gqa_decode_noalloc(q, kp, vp, pt, pos, scale, out)
+    gen = torch.Generator().manual_seed(24)
+    base = ctx.positions.clone()
+    for rep in range(4):
+        q.copy_(torch.randn(tuple(q.shape), generator=gen).bfloat16())
+        frac = torch.rand(base.shape, generator=gen) if rep else torch.ones(base.shape)
+        pos.copy_((base.float() * frac).to(torch.int32))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = hip_ops.paged_gqa_decode(q, kp, vp, pt, pos, scale)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), f"replay {rep} differs from sym_paged_gqa_decode"

@@ -66,6 +66,7 @@ struct TileArgs {
   long long out_zstride;    // ... and output plane out + z * out_zstride (elements)
   int full_rt;              // DENSE with tail_rows > 0: row tiles 0 .. full_rt - 1 have TM rows,
   int tail_rows;            // the rows from full_rt * TM on tiles of tail_rows (one plane)
+  int* tickets;             // gemm_tile_persistent: the caller's 8 per-XCD tile counters
 };
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -549,10 +550,11 @@ __device__ __forceinline__ TileLoc seg_tile(const SegTable& t, int g, int ct) {
   return loc;
 }
 
-// Tile tickets of gemm_tile_persistent, one counter per XCD. Zero between launches: the
-// workgroup that draws an XCD's last ticket resets its counter. Launches that overlap on one
-// device (different streams) would share them, so such launches must be stream-ordered.
-__device__ int g_tile_ticket[8];
+// Tile tickets of gemm_tile_persistent: one counter per XCD in the caller's workspace
+// (kTicketBytes), zero before the launch. The workgroup that draws an XCD's last ticket resets
+// its counter, so a launch leaves the workspace zeroed for the next launch that uses it; launches
+// that may overlap in time (different streams) take different workspaces.
+constexpr size_t kTicketBytes = 8 * sizeof(int);
 
 // Grouped modes of the 256 x 256 tiles on a persistent grid (one workgroup per CU, a multiple
 // of 8): the segment list is read and scanned once per workgroup into LDS and each tile then
@@ -585,7 +587,7 @@ void gemm_tile_persistent(TileArgs p, int nx) {
   // and its result is waited for only where it is used
   int zero = 0;
   asm volatile("" : "+v"(zero));
-  int* ticket = g_tile_ticket + x + zero;
+  int* ticket = p.tickets + x + zero;
   int i = blockIdx.x >> 3;  // index in the run
   int pend = 0;             // thread 0: the ticket drawn for the tile after the current one
   if (threadIdx.x == 0 && i < run)
@@ -874,12 +876,26 @@ static int check_grouped(const char* what, int T, int H, int I, int rows, int ma
   return SYM_OK;
 }
 
+// The tile-ticket workspace of the grouped tiled GEMMs (zeroed once by the caller, left zeroed
+// by every launch).
+static int check_tickets(const char* what, const void* workspace, size_t workspace_bytes) {
+  SYM_REQUIRE(workspace_bytes >= kTicketBytes, SYM_ERR_WORKSPACE,
+              "%s: workspace of %zu bytes, %zu needed", what, workspace_bytes, kTicketBytes);
+  SYM_REQUIRE(workspace && aligned(workspace, 4), SYM_ERR_INVALID,
+              "%s: workspace must be a non-null 4-byte aligned device pointer", what);
+  return SYM_OK;
+}
+
+extern "C" size_t sym_moe_tiled_workspace_bytes(void) { return kTicketBytes; }
+
 extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int rows,
                                      const int32_t* sorted_tokens, const int32_t* seg_expert,
                                      const int32_t* seg_offset, const int32_t* seg_count,
                                      const int32_t* n_segments, int max_segments,
-                                     const void* w_gate_up, void* h, void* stream) {
+                                     const void* w_gate_up, void* h, void* workspace,
+                                     size_t workspace_bytes, void* stream) {
   int rc = check_grouped("moe_gate_up_tiled", T, H, I, rows, max_segments);
+  if (!rc) rc = check_tickets("moe_gate_up_tiled", workspace, workspace_bytes);
   if (rc || rows == 0 || T == 0) return rc;
   SYM_REQUIRE(x && sorted_tokens && seg_expert && seg_offset && seg_count && n_segments &&
                   w_gate_up && h,
@@ -899,6 +915,7 @@ extern "C" int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int row
   p.N = I;
   p.K = H;
   p.out_bf16 = (uint16_t*)h;
+  p.tickets = (int*)workspace;
   (void)hipGetLastError();
   namespace C = big;
   const int nx = (I + C::kTN / 2 - 1) / (C::kTN / 2);
@@ -918,8 +935,9 @@ extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
                                   const int32_t* seg_expert, const int32_t* seg_offset,
                                   const int32_t* seg_count, const int32_t* n_segments,
                                   int max_segments, const void* w_down, void* y, int y_bf16,
-                                  void* stream) {
+                                  void* workspace, size_t workspace_bytes, void* stream) {
   int rc = check_grouped("moe_down_tiled", T, H, I, rows, max_segments);
+  if (!rc) rc = check_tickets("moe_down_tiled", workspace, workspace_bytes);
   if (rc || rows == 0 || T == 0) return rc;
   SYM_REQUIRE(h && seg_expert && seg_offset && seg_count && n_segments && w_down && y,
               SYM_ERR_INVALID, "moe_down_tiled: null pointer argument");
@@ -938,6 +956,7 @@ extern "C" int sym_moe_down_tiled(const void* h, int T, int H, int I, int rows,
   p.K = I;
   if (y_bf16) p.out_bf16 = (uint16_t*)y;
   else p.out_f32 = (float*)y;
+  p.tickets = (int*)workspace;
   (void)hipGetLastError();
   if (max_segments <= kPersistSeg) {
     const int grid = std::max(8, sym_host::cu_count() / 8 * 8);

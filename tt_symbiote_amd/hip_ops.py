@@ -844,6 +844,14 @@ def moe_route_permute(logits: torch.Tensor, bias: torch.Tensor, *, n_group: int,
 TILED_MIN_TOKENS = 128  # from this many tokens the expert GEMMs use the tiled (MFMA-bound) kernels
 
 
+def moe_tiled_workspace(device=None) -> torch.Tensor:
+    """A zeroed tile-counter workspace for the tiled grouped expert GEMMs
+    (``sym_moe_tiled_workspace_bytes()`` bytes). Every launch leaves it zeroed, so it can be
+    reused by any number of launches ordered on one stream."""
+    dev = device if device is not None else torch.device("cuda", torch.cuda.current_device())
+    return torch.zeros(_lib.query("sym_moe_tiled_workspace_bytes"), dtype=torch.uint8, device=dev)
+
+
 FP8_BLOCK = 128
 
 
@@ -888,13 +896,17 @@ def quantize_block_fp8(w: torch.Tensor) -> BlockFp8:
 def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
                        w_down, h: Optional[torch.Tensor] = None,
                        y: Optional[torch.Tensor] = None, kernel: str = "auto",
-                       y_dtype: torch.dtype = torch.float32):
+                       y_dtype: torch.dtype = torch.float32,
+                       workspace: Optional[torch.Tensor] = None):
     """h = silu(x Wg^T) * (x Wu^T), y = h Wd^T per segment; returns (h [rows, I], y [rows, H]).
     The weights are bf16 tensors, or BlockFp8 (fp8 e4m3fn + 128 x 128 block scales, dequantized
     in the kernel). ``kernel``: "stream" (weight-streaming kernels for decode-size segments),
     "tiled" (256 x 256 / 128 x 256 MFMA tiles for prefill-size segments, bf16 only) or "auto"
     (tiled from TILED_MIN_TOKENS tokens with bf16 weights). ``y_dtype``: fp32, or bf16 with the tiled kernels
-    (half the bytes of y written and read back by the combine)."""
+    (half the bytes of y written and read back by the combine). ``workspace``: the tiled
+    kernels' tile counters (:func:`moe_tiled_workspace`, zeroed, left zeroed by every launch);
+    a fresh one per call when None. Calls that may overlap on different streams need different
+    workspaces."""
     _check(x, "x", torch.bfloat16)
     if x.dim() != 2:
         raise ValueError(f"x must be [T, H], got {tuple(x.shape)}")
@@ -954,14 +966,19 @@ def moe_grouped_swiglu(x: torch.Tensor, route: RouteResult, w_gate_up,
             _ptr(s_down), _ptr(y), stream))
         return h, y
     if tiled:
+        if workspace is None:
+            workspace = moe_tiled_workspace(dev)
+        _check(workspace, "workspace", torch.uint8, dev)
+        ws, ws_bytes = _ptr(workspace), workspace.numel()
         _timed("moe_gate_up", lambda: _lib.call(
             "sym_moe_gate_up_tiled", _ptr(x), T, H, I, rows, _ptr(route.sorted_tokens),
             _ptr(route.seg_expert), _ptr(route.seg_offset), _ptr(route.seg_count),
-            _ptr(route.n_segments), max_segments, _ptr(w_gate_up), _ptr(h), stream))
+            _ptr(route.n_segments), max_segments, _ptr(w_gate_up), _ptr(h), ws, ws_bytes,
+            stream))
         _timed("moe_down", lambda: _lib.call(
             "sym_moe_down_tiled", _ptr(h), T, H, I, rows, _ptr(route.seg_expert),
             _ptr(route.seg_offset), _ptr(route.seg_count), _ptr(route.n_segments), max_segments,
-            _ptr(w_down), _ptr(y), 1 if y.dtype == torch.bfloat16 else 0, stream))
+            _ptr(w_down), _ptr(y), 1 if y.dtype == torch.bfloat16 else 0, ws, ws_bytes, stream))
         return h, y
     _timed("moe_gate_up", lambda: _lib.call(
         "sym_moe_gate_up", _ptr(x), T, H, I, _ptr(route.sorted_tokens), _ptr(route.seg_expert),

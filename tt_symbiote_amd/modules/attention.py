@@ -249,11 +249,10 @@ class HIPBailingMoEAttention(StatefulHIPModule):
         if B > cache.page_table.shape[0]:
             raise ValueError(f"{B} prompts for a page table of {cache.page_table.shape[0]} rows")
         pos = cache_position if cache_position is not None else position_ids
-        if isinstance(pos, torch.Tensor) and pos.device.type == "cpu" and pos.numel():
-            if int(pos.reshape(-1)[0]) != 0:
-                raise NotImplementedError(
-                    "prefill starting at a cached position (a prompt continuing earlier tokens); "
-                    "as the reference's prefill, prompts start at position 0")
+        if prefill_continues(cache, self.layer_idx, pos):
+            raise NotImplementedError(
+                "prefill starting at a cached position (a prompt continuing earlier tokens); "
+                "as the reference's prefill, prompts start at position 0")
         positions, seq_ids, cu = equal_length_packing(B, S, x.device)
         out = self.prefill_varlen(x.reshape(B * S, H).contiguous(), cu, S, positions, seq_ids,
                                   cache)
@@ -275,6 +274,16 @@ class HIPBailingMoEAttention(StatefulHIPModule):
         o = self.decode_from_qkv(qkv, cache, cache_position, position_ids)
         out = hip_ops.linear(o, d["dense_w"], d["dense_b"])
         return out.view(B, 1, H), None, cache
+
+
+def prefill_continues(cache: HIPPagedAttentionKVCache, layer_idx: int, pos) -> bool:
+    """True when a prefill would continue a cached sequence instead of starting at position 0:
+    the layer's host counter is past 0 (checked without a device sync, whatever device the
+    positions are on), or host-side positions start past 0."""
+    if cache.get_seq_length(layer_idx) != 0:
+        return True
+    return (isinstance(pos, torch.Tensor) and pos.device.type == "cpu" and pos.numel() > 0
+            and int(pos.reshape(-1)[0]) != 0)
 
 
 def equal_length_packing(B: int, S: int, device):

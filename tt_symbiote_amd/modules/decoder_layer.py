@@ -18,7 +18,8 @@ import torch
 
 from .. import hip_ops
 from ..core.module import StatefulHIPModule
-from .attention import HIPBailingMoEAttention, equal_length_packing, varlen_packing
+from .attention import HIPBailingMoEAttention, equal_length_packing, prefill_continues, \
+    varlen_packing
 from .moe import HIPBailingMoE, HIPBailingMoeV2MLP
 
 
@@ -120,6 +121,11 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
         if S != 1:
             # equal-length prompts, positions 0 .. S-1 of page-table rows 0 .. B-1
             kv = attn._cache_of(cache, None)
+            pos = cache_position if cache_position is not None else position_ids
+            if prefill_continues(kv, attn.layer_idx, pos):
+                raise NotImplementedError(
+                    "prefill starting at a cached position (a prompt continuing earlier "
+                    "tokens); as the reference's prefill, prompts start at position 0")
             positions, seq_ids, cu = equal_length_packing(B, S, x.device)
             out = self.prefill_varlen(x.view(B * S, H), cu, S, kv, positions=positions,
                                       seq_ids=seq_ids)

@@ -27,7 +27,7 @@ import torch
 
 from .. import hip_ops
 from ..core.module import StatefulHIPModule, StatelessHIPModule
-from .attention import equal_length_packing
+from .attention import equal_length_packing, prefill_continues
 from .decoder_layer import HIPBailingMoEDecoderLayer
 
 
@@ -161,10 +161,9 @@ class HIPBailingMoeV2Model(StatefulHIPModule):
             h = self.final_norm(h.view(B, self.hidden_size)).view(B, 1, self.hidden_size)
         else:
             pos = cache_position if cache_position is not None else position_ids
-            if isinstance(pos, torch.Tensor) and pos.device.type == "cpu" and pos.numel():
-                if int(pos.reshape(-1)[0]) != 0:
-                    raise NotImplementedError("prefill starting at a cached position; prompts "
-                                              "start at position 0 (as the reference's prefill)")
+            if prefill_continues(cache, 0, pos):
+                raise NotImplementedError("prefill starting at a cached position; prompts "
+                                          "start at position 0 (as the reference's prefill)")
             if B > cache.page_table.shape[0]:
                 raise ValueError(f"{B} prompts for a page table of {cache.page_table.shape[0]} "
                                  "rows")
