@@ -409,3 +409,34 @@ def decoder_layer_from_weights(w: dict, shape, layer_idx: int = 0,
             cp(moe.shared_experts.up_proj.weight, sgu[Is:])
             cp(moe.shared_experts.down_proj.weight, w["shared_down"])
     return layer.eval()
+
+
+def dense_decoder_layer_from_weights(w: dict, shape, intermediate_size: int,
+                                     dtype: torch.dtype = torch.float32) -> BailingMoeV2DecoderLayer:
+    """Oracle decoder layer with the dense SwiGLU MLP (layer_idx < first_k_dense_replace,
+    modeling_bailing_moe_v2.py:388-399) from a weights dict with the attention and norm keys of
+    :func:`decoder_layer_from_weights` plus mlp_gate / mlp_up [I, H] and mlp_down [H, I]."""
+    cfg = config_from_shape(shape, first_k_dense_replace=1, intermediate_size=intermediate_size)
+    with torch.device("meta"):
+        layer = BailingMoeV2DecoderLayer(cfg, 0)
+    layer = layer.to_empty(device="cpu").to(dtype)
+    assert isinstance(layer.mlp, BailingMoeV2MLP)
+
+    def cp(dst, src):
+        dst.data.copy_(src.detach().to("cpu", dtype))
+
+    with torch.no_grad():
+        cp(layer.input_layernorm.weight, w["ln1"])
+        cp(layer.post_attention_layernorm.weight, w["ln2"])
+        att = layer.attention
+        cp(att.query_key_value.weight, w["qkv_w"])
+        cp(att.dense.weight, w["dense_w"])
+        if shape.use_qk_norm:
+            cp(att.query_layernorm.weight, w["q_norm"])
+            cp(att.key_layernorm.weight, w["k_norm"])
+        att.rotary_emb.inv_freq = rope_inv_freq(shape.head_dim, shape.partial_rotary_factor,
+                                                shape.rope_theta)
+        cp(layer.mlp.gate_proj.weight, w["mlp_gate"])
+        cp(layer.mlp.up_proj.weight, w["mlp_up"])
+        cp(layer.mlp.down_proj.weight, w["mlp_down"])
+    return layer.eval()

@@ -201,19 +201,119 @@ def test_prefill_layer_8_prompts_zipf(device):
         assert err <= TOL
 
 
+# The whole-model run's oracle checkpoints: sequences (one per prefill group of 8 prompts, at
+# both ends of the batch), layers (the dense layer, the first and the last MoE layer) and decode
+# steps (the first and the last).
+TRACK_SEQS = (0, 21, 42, 63)
+TRACK_LAYERS = (0, 1, 19)
+TRACK_STEPS = (1, 127)
+
+
+def _bf16_half_ulp(y: torch.Tensor) -> torch.Tensor:
+    """Half the bf16 spacing at each value of y (the most that rounding y to bf16 moves it)."""
+    _, e = torch.frexp(y.float())
+    return torch.ldexp(torch.ones_like(y, dtype=torch.float32), e - 9)
+
+
+class _LayerTap:
+    """Records, in the eager loop, the tracked sequences' rows entering and leaving one decoder
+    layer and the GPU's expert choice for them: at the prompt's last token (prefill) and at
+    the tracked decode steps (the layer's n-th decode call is step n)."""
+
+    def __init__(self, layer, seqs, steps):
+        self.seqs, self.steps, self.step = seqs, steps, 0
+        self.rec = {}
+        mlp = layer.mlp
+        moe = not layer.is_dense_layer
+        if moe:
+            mlp.keep_last_route = True
+        fwd, pre = layer.forward, layer.prefill_varlen
+
+        def keep(point, x, y, rows, seqs_here):
+            x, y = x.reshape(-1, x.shape[-1]), y.reshape(-1, y.shape[-1])
+            idx = mlp.last_route.topk_idx if moe else None
+            for b, r in zip(seqs_here, rows):
+                self.rec[(b, point)] = (x[r].cpu(), y[r].cpu(),
+                                        None if idx is None else idx[r].cpu().long())
+
+        def forward(hidden_states, *a, **kw):
+            out = fwd(hidden_states, *a, **kw)
+            self.step += 1
+            if self.step in self.steps:
+                keep(self.step, hidden_states, out[0], list(self.seqs), list(self.seqs))
+            return out
+
+        def prefill_varlen(x, cu_seqlens, max_seqlen, cache, positions=None, seq_ids=None):
+            out = pre(x, cu_seqlens, max_seqlen, cache, positions=positions, seq_ids=seq_ids)
+            sid = seq_ids.cpu()
+            here = [b for b in self.seqs if bool((sid == b).any())]
+            rows = [int((sid == b).nonzero().max()) for b in here]
+            keep(0, x, out, rows, here)
+            return out
+
+        layer.forward, layer.prefill_varlen = forward, prefill_varlen
+
+
+class _HeadTap:
+    """Records every greedy call of the LM head in the eager loop: its input (the GPU's final
+    normed hidden rows) and the ids it chose."""
+
+    def __init__(self, head):
+        self.calls = []
+        greedy = head.greedy
+
+        def tapped(x, ids=None):
+            out = greedy(x, ids=ids)
+            self.calls.append((x.reshape(-1, x.shape[-1]).clone(), out.clone()))
+            return out
+
+        head.greedy = tapped
+
+
+def _routed_oracle(oracle_layer, gpu_idx, run):
+    """Run the oracle MoE layer with the GPU's expert choice ``gpu_idx`` [n, K]; the oracle's
+    own choice may differ only at a router near tie. Returns the output."""
+    gate = oracle_layer.mlp.gate
+    gate.route_override = gpu_idx
+    try:
+        with torch.no_grad():
+            out = run()
+    finally:
+        gate.route_override = None
+    logits = gate.last_routing[0]
+    kw = dict(n_group=gate.n_group, topk_group=gate.topk_group, top_k=gate.top_k)
+    own, _ = route_torch(logits, gate.expert_bias, routed_scale=1.0, **kw)
+    diff = (own.sort(-1).values != gpu_idx.sort(-1).values).any(-1)
+    if bool(diff.any()):
+        m = selection_margins(logits, gate.expert_bias, **kw)[diff]
+        assert bool((m < FLIP_MARGIN).all()), f"routing differs at margins {m.tolist()}"
+    return out
+
+
 def test_whole_model_generate_graph_equals_eager(device):
+    """The 20-layer, vocab-157184 model at batch 64 (prompts of 2048 tokens, 128 greedy tokens):
+      * the captured decode loop gives exactly the eager loop's tokens;
+      * layers 0 (dense), 1 and 19 against the fp32 oracle layer for 4 sequences at the prompt's
+        last token and at decode steps 1 and 127: the oracle runs the recorded input row over
+        the sequence's own cache pages as the GPU wrote them, with the GPU's expert choice;
+        max-abs 2e-2 on the layer output beyond the rounding of the output to bf16, and the
+        new K/V slot as the oracle writes it;
+      * every chosen token (64 x 128) is the argmax of exact (float64) logits of the GPU's own
+        final hidden rows, or equal to the maximum within fp32 summation rounding."""
+    from oracle.bailing_moe_v2 import dense_decoder_layer_from_weights
     from tt_symbiote_amd.generate import greedy_generate
     from tt_symbiote_amd.modules.model import HIPBailingMoeV2Model, HIPLMHead
+    from tt_symbiote_amd.workloads import dense_layer_weights
 
     shape = LING_MINI_2
     mc = model_config()
     B, L, n_new, V, H = mc["batch"], mc["prompt_len"], mc["new_tokens"], mc["vocab_size"], \
         shape.hidden_size
+    dense_I = mc["dense_intermediate_size"]
     layers = []
     for i in range(mc["num_layers"]):
         if i < mc["first_k_dense_replace"]:
-            layer = build_dense_decoder_layer(shape, mc["dense_intermediate_size"], seed=i,
-                                              device=device, layer_idx=i)
+            layer = build_dense_decoder_layer(shape, dense_I, seed=i, device=device, layer_idx=i)
         else:
             lw = layer_weights(shape, seed=i, device=device)
             layer = build_decoder_layer(lw, shape, layer_idx=i)
@@ -234,7 +334,23 @@ def test_whole_model_generate_graph_equals_eager(device):
     cache = ts.HIPPagedAttentionKVCache(mc["num_layers"], shape.num_kv_heads, shape.head_dim,
                                         cfg, device=device)
     prompts = torch.randint(0, V, (B, L), generator=torch.Generator().manual_seed(7))
+
+    taps = {i: _LayerTap(layers[i], TRACK_SEQS, TRACK_STEPS) for i in TRACK_LAYERS}
+    head_tap = _HeadTap(head)
     eager = greedy_generate(trunk, head, prompts, cache, n_new, use_graph=False)
+    del head.greedy                                 # the graph run uses the plain method
+    for i in TRACK_LAYERS:
+        del layers[i].forward, layers[i].prefill_varlen
+    # the tracked sequences' pages as the eager loop wrote them (the graph loop rewrites them
+    # with the same bytes)
+    bs = mc["block_size"]
+    nblk = (L + n_new - 1 + bs - 1) // bs
+    pages = {}
+    for i in TRACK_LAYERS:
+        for b in TRACK_SEQS:
+            blocks = cache.page_table[b, :nblk].long().to(device)
+            pages[(i, b)] = (cache.key_cache(i)[blocks].float().cpu(),
+                             cache.value_cache(i)[blocks].float().cpu())
     cache.reset()
     graph = greedy_generate(trunk, head, prompts, cache, n_new, use_graph=True)
     assert eager.tokens.shape == (B, n_new)
@@ -243,4 +359,71 @@ def test_whole_model_generate_graph_equals_eager(device):
     # the tokens are not degenerate (a stuck loop would repeat one id)
     assert len(torch.unique(graph.tokens)) > B
     print(f"whole model: {B} x {n_new} tokens identical between the captured and the eager "
-          f"loop; decode {graph.decode_s / graph.decode_steps * 1e3:.2f} ms/step")
+          f"loop; decode {graph.decode_s / graph.decode_steps * 1e3:.2f} ms/step", flush=True)
+
+    # every greedy choice against exact logits of the GPU's own final hidden rows
+    w64 = head.weight.double()
+    n_rows = ties = 0
+    min_gap = float("inf")
+    for x, ids in head_tap.calls:
+        logits = x.double() @ w64.T
+        top2 = logits.topk(2, dim=-1)
+        picked = logits.gather(1, ids.long()[:, None])[:, 0]
+        gap = top2.values[:, 0] - picked
+        exact = ids.long() == top2.indices[:, 0]
+        assert bool(((gap <= 1e-4) | exact).all()), \
+            f"LM head choice {gap.max().item():.3e} below the maximum logit"
+        ties += int((~exact).sum())
+        n_rows += ids.numel()
+        min_gap = min(min_gap, float((top2.values[:, 0] - top2.values[:, 1]).min()))
+    del w64
+    assert n_rows == B * n_new
+    print(f"LM head: {n_rows} choices, {n_rows - ties} the exact argmax, {ties} within fp32 "
+          f"rounding of it; smallest top-2 gap {min_gap:.3e}", flush=True)
+
+    # the tracked layers against the oracle over the GPU-written pages
+    worst, scale = {}, {}
+    for i in TRACK_LAYERS:
+        if i < mc["first_k_dense_replace"]:
+            w = dense_layer_weights(shape, dense_I, seed=i, device=device)
+            oracle = dense_decoder_layer_from_weights({k: v.cpu() for k, v in w.items()},
+                                                      shape, dense_I)
+        else:
+            w = layer_weights(shape, seed=i, device=device)
+            oracle = decoder_layer_from_weights({k: v.cpu() for k, v in w.items()}, shape)
+        del w
+        for b in TRACK_SEQS:
+            kb, vb = pages[(i, b)]
+            for point in (0,) + TRACK_STEPS:
+                x_in, y_gpu, idx = taps[i].rec[(b, point)]
+                p = L - 1 + point                # the position of the token the layer ran
+                ref_cache = PagedKVCacheRef([kb.clone()], [vb.clone()],
+                                            torch.arange(nblk)[None])
+                run = lambda: oracle(x_in.float().view(1, 1, H), past_key_value=ref_cache,
+                                     cache_position=torch.tensor([p]))[0]
+                if idx is None:
+                    with torch.no_grad():
+                        y_ref = run()
+                else:
+                    y_ref = _routed_oracle(oracle, idx[None], run)
+                y_ref = y_ref.view(H)
+                # the 2e-2 bar on top of the bf16 output's own rounding (half an ulp of the
+                # exact value): the residual stream grows through the layers (|y| above 8 at
+                # layer 19), where rounding alone exceeds 2e-2
+                excess = (y_gpu.float() - y_ref).abs() - _bf16_half_ulp(y_ref)
+                err = excess.max().item()
+                scale[(i, point)] = max(scale.get((i, point), 0.0), y_ref.abs().max().item())
+                slot = (p // bs, p % bs)
+                kv_err = max((kb[slot[0], :, slot[1]] -
+                              ref_cache.k_pools[0][slot[0], :, slot[1]]).abs().max().item(),
+                             (vb[slot[0], :, slot[1]] -
+                              ref_cache.v_pools[0][slot[0], :, slot[1]]).abs().max().item())
+                worst[(i, point)] = max(worst.get((i, point), 0.0), err)
+                assert err <= TOL, \
+                    f"layer {i} seq {b} position {p}: max err {err:.3e} beyond bf16 rounding"
+                assert kv_err <= 3e-2, f"layer {i} seq {b} position {p}: K/V slot {kv_err:.3e}"
+        del oracle
+    print("oracle checkpoints, max over sequences " + str(TRACK_SEQS) + " of the error beyond "
+          "the output's bf16 rounding (and max |y|): " + "; ".join(
+              f"layer {i} {'prefill' if pt == 0 else 'step ' + str(pt)} {e:.2e} "
+              f"({scale[(i, pt)]:.1f})" for (i, pt), e in sorted(worst.items())), flush=True)

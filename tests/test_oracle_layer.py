@@ -159,3 +159,29 @@ def test_partial_rope_properties(factor):
     n_out = out[..., :h] ** 2 + out[..., h:rd] ** 2
     torch.testing.assert_close(n_in, n_out)                     # pairs keep their norm
     torch.testing.assert_close(apply(apply(q, 300), 477), apply(q, 777), rtol=1e-4, atol=1e-4)
+
+
+def test_dense_decoder_layer_from_weights_wiring():
+    """The dense-MLP oracle layer holds the dict's matrices in their places (gate, up and down
+    not swapped) and computes h1 + down(silu(gate(n)) * up(n)) on n = RMSNorm(h1)."""
+    import dataclasses
+
+    from oracle.bailing_moe_v2 import dense_decoder_layer_from_weights
+    from tt_symbiote_amd.workloads import LING_MINI_2, dense_layer_weights
+
+    shape = dataclasses.replace(LING_MINI_2, hidden_size=256, num_heads=2, num_kv_heads=1)
+    w = dense_layer_weights(shape, intermediate_size=384, seed=4)
+    layer = dense_decoder_layer_from_weights(w, shape, 384)
+    assert torch.equal(layer.mlp.gate_proj.weight, w["mlp_gate"].float())
+    assert torch.equal(layer.mlp.up_proj.weight, w["mlp_up"].float())
+    assert torch.equal(layer.mlp.down_proj.weight, w["mlp_down"].float())
+    assert torch.equal(layer.attention.query_key_value.weight, w["qkv_w"].float())
+    x = torch.randn(1, 5, 256, generator=torch.Generator().manual_seed(5))
+    with torch.no_grad():
+        out = layer(x)[0]
+        h1 = x + layer.attention(layer.input_layernorm(x))[0]
+        n = layer.post_attention_layernorm(h1)
+        g = n @ w["mlp_gate"].float().T
+        u = n @ w["mlp_up"].float().T
+        want = h1 + (g * torch.sigmoid(g) * u) @ w["mlp_down"].float().T
+    torch.testing.assert_close(out, want, rtol=1e-5, atol=1e-5)

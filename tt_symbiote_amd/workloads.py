@@ -244,24 +244,37 @@ def build_decoder_layer(w: Dict[str, torch.Tensor], shape: LayerShape = LING_MIN
                                                   eps=shape.rms_norm_eps)
 
 
+def dense_layer_weights(shape: LayerShape = LING_MINI_2, intermediate_size: int = 5120,
+                        seed: int = 0, device="cpu", std: float = 0.02) -> Dict[str, torch.Tensor]:
+    """Random-init weights of a decoder layer with the dense SwiGLU MLP (the layers before
+    first_k_dense_replace): the attention and norm entries of :func:`layer_weights` plus
+    ``mlp_gate`` / ``mlp_up`` [intermediate, H] and ``mlp_down`` [H, intermediate], bf16."""
+    w = layer_weights(dataclasses.replace(shape, num_experts=8, moe_intermediate_size=128,
+                                          num_shared_experts=0), seed=seed, device=device,
+                      std=std)
+    for k in ("gate_w", "expert_bias", "gate_up", "down"):
+        del w[k]
+    dev = torch.device(device)
+    g = torch.Generator(device=dev).manual_seed(seed + 1000)
+    H = shape.hidden_size
+    w["mlp_gate"] = _randn(g, (intermediate_size, H), dev, std).to(torch.bfloat16)
+    w["mlp_up"] = _randn(g, (intermediate_size, H), dev, std).to(torch.bfloat16)
+    w["mlp_down"] = _randn(g, (H, intermediate_size), dev, std).to(torch.bfloat16)
+    return w
+
+
 def build_dense_decoder_layer(shape: LayerShape = LING_MINI_2, intermediate_size: int = 5120,
                               seed: int = 0, device="cpu", layer_idx: int = 0,
                               std: float = 0.02):
     """HIP decoder layer with the dense SwiGLU MLP (the layers before first_k_dense_replace),
-    random-init like :func:`layer_weights`."""
+    weights from :func:`dense_layer_weights`."""
     from .modules.attention import HIPBailingMoEAttention
     from .modules.decoder_layer import HIPBailingMoEDecoderLayer
     from .modules.moe import HIPBailingMoeV2MLP
 
-    w = layer_weights(dataclasses.replace(shape, num_experts=8, moe_intermediate_size=128,
-                                          num_shared_experts=0), seed=seed, device=device,
-                      std=std)
-    dev = torch.device(device)
-    g = torch.Generator(device=dev).manual_seed(seed + 1000)
+    w = dense_layer_weights(shape, intermediate_size, seed=seed, device=device, std=std)
     H = shape.hidden_size
-    gate = _randn(g, (intermediate_size, H), dev, std).to(torch.bfloat16)
-    up = _randn(g, (intermediate_size, H), dev, std).to(torch.bfloat16)
-    down = _randn(g, (H, intermediate_size), dev, std).to(torch.bfloat16)
+    gate, up, down = w["mlp_gate"], w["mlp_up"], w["mlp_down"]
     attn = HIPBailingMoEAttention.from_weights(
         num_heads=shape.num_heads, num_kv_heads=shape.num_kv_heads, head_dim=shape.head_dim,
         hidden_size=H, qkv_weight=w["qkv_w"], dense_weight=w["dense_w"],
