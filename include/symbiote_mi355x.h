@@ -42,7 +42,7 @@ typedef enum {
 
 /* Message for the last non-zero status returned on the calling thread. */
 const char* sym_last_error(void);
-/* ABI revision; bumped on any signature change. */
+/* ABI revision; bumped on any signature change (2: workspace of the tiled grouped GEMMs). */
 int sym_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------
@@ -55,6 +55,11 @@ int sym_abi_version(void);
  */
 int sym_rmsnorm_bf16(const void* x, const void* residual, const void* weight, int rows, int cols,
                      float eps, void* out, float* residual_out, void* stream);
+/* sym_rmsnorm_bf16 with fp32 x (a projection's fp32 output, e.g. the attention's dense
+ * projection at prefill size), so the layer's residual stream s = x + residual is formed
+ * without rounding x to bf16 first. x and residual_out 16-byte aligned. */
+int sym_rmsnorm_f32(const float* x, const void* residual, const void* weight, int rows, int cols,
+                    float eps, void* out, float* residual_out, void* stream);
 
 /* ---------------------------------------------------------------------------------------
  * Skinny GEMM for the decode projections: out[M, N] = x[M, K] . w[N, K]^T (+ bias[N]).

@@ -25,7 +25,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.sym_abi_version() == 1
+    assert lib.sym_abi_version() == 2
 
 
 def test_workspace_queries():

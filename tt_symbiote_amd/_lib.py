@@ -27,6 +27,7 @@ _SIGNATURES = {
     "sym_last_error": (ctypes.c_char_p, []),
     "sym_abi_version": (_c_int, []),
     "sym_rmsnorm_bf16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_float, _vp, _vp, _vp]),
+    "sym_rmsnorm_f32": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _c_float, _vp, _vp, _vp]),
     "sym_attn_decode_prologue": (
         _c_int,
         [_vp, _vp, _vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _c_int,

@@ -38,4 +38,4 @@ int cu_count() {
 }  // namespace sym_host
 
 extern "C" const char* sym_last_error(void) { return g_error; }
-extern "C" int sym_abi_version(void) { return 1; }
+extern "C" int sym_abi_version(void) { return 2; }

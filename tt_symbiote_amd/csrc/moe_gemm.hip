@@ -32,6 +32,77 @@ __device__ __forceinline__ uint4 ld16(const uint16_t* p) {
   return *reinterpret_cast<const uint4*>(p);
 }
 
+// Segment of a tile of the grid-stride loops below.
+struct SegInfo {
+  int e, row0, cnt;
+};
+// The grid-stride loops below walk the live tiles from the last one down: the last segment is the
+// shared expert, whose T rows take the most passes, so its tiles start first instead of forming
+// the kernel's tail. Metadata is read with scalar loads written out in asm (the compiler would
+// otherwise wait between dependent loads it could issue together, or sink a prefetch to its
+// use); their destinations are early-clobber, so that no load overwrites the address of a later
+// one before it issues. The live segment count comes first, then the segments of a workgroup's
+// first two tiles in one round trip; a third or later tile (only at large batches) reads its
+// segment when it starts.
+__device__ __forceinline__ int load_segment_count(const int32_t* n_segments) {
+  int nseg;
+  asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)"
+               : "=&s"(nseg)
+               : "s"(n_segments)
+               : "memory");
+  return nseg;
+}
+__device__ __forceinline__ void load_two_segments(const int32_t* seg_expert,
+                                                  const int32_t* seg_offset,
+                                                  const int32_t* seg_count, int seg0, int seg1,
+                                                  SegInfo& m0, SegInfo& m1) {
+  asm volatile(
+      "s_load_dword %0, %6, 0x0\n\t"
+      "s_load_dword %1, %7, 0x0\n\t"
+      "s_load_dword %2, %8, 0x0\n\t"
+      "s_load_dword %3, %9, 0x0\n\t"
+      "s_load_dword %4, %10, 0x0\n\t"
+      "s_load_dword %5, %11, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(m0.e), "=&s"(m0.row0), "=&s"(m0.cnt), "=&s"(m1.e), "=&s"(m1.row0), "=&s"(m1.cnt)
+      : "s"(seg_expert + seg0), "s"(seg_offset + seg0), "s"(seg_count + seg0),
+        "s"(seg_expert + seg1), "s"(seg_offset + seg1), "s"(seg_count + seg1)
+      : "memory");
+}
+__device__ __forceinline__ SegInfo load_segment(const int32_t* seg_expert,
+                                                const int32_t* seg_offset,
+                                                const int32_t* seg_count, int seg) {
+  SegInfo m;
+  asm volatile(
+      "s_load_dword %0, %3, 0x0\n\t"
+      "s_load_dword %1, %4, 0x0\n\t"
+      "s_load_dword %2, %5, 0x0\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&s"(m.e), "=&s"(m.row0), "=&s"(m.cnt)
+      : "s"(seg_expert + seg), "s"(seg_offset + seg), "s"(seg_count + seg)
+      : "memory");
+  return m;
+}
+// Declares ntiles, m0 and m1 in a kernel with the arguments seg_expert, seg_offset, seg_count,
+// n_segments and tiles_per_seg: the workgroup's k-th tile is ntiles - 1 - (blockIdx.x + k *
+// gridDim.x); m0 / m1 hold the segments of its first two (an index clamped at 0 for a tile past
+// the live ones: read, not used).
+#define SYM_FIRST_SEGMENTS(ntiles, m0, m1)                                                     \
+  const int ntiles = load_segment_count(n_segments) * tiles_per_seg;                         \
+  SegInfo m0, m1;                                                                            \
+  load_two_segments(                                                                         \
+      seg_expert, seg_offset, seg_count,                                                     \
+      __builtin_amdgcn_readfirstlane(max(ntiles - 1 - (int)blockIdx.x, 0) / tiles_per_seg),  \
+      __builtin_amdgcn_readfirstlane(max(ntiles - 1 - (int)(blockIdx.x + gridDim.x), 0) /   \
+                                     tiles_per_seg),                                         \
+      m0, m1)
+// The segment of the it-th tile of this workgroup, tile wt.
+#define SYM_TILE_SEGMENT(it, wt, m0, m1)                       \
+  ((it) == 0   ? (m0)                                          \
+   : (it) == 1 ? (m1)                                          \
+               : load_segment(seg_expert, seg_offset, seg_count, \
+                              __builtin_amdgcn_readfirstlane((wt) / tiles_per_seg)))
+
 // Lane -> k mapping inside a 64-wide K step (the same for both MFMA operands, so any mapping
 // is exact): lane group kq = l / 16 takes k = kKLane * kq + 0..7 for the first MFMA and the same
 // + kKHalf for the second.
@@ -130,13 +201,14 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
     const int32_t* __restrict__ seg_count, const int32_t* __restrict__ n_segments,
     const uint16_t* __restrict__ w_gu, uint16_t* __restrict__ h, int tiles_per_seg) {
   __shared__ float s_red[4][1][2][4][64];
-  // the grid strides over the live tiles (segments * tiles_per_seg)
-  const int ntiles = n_segments[0] * tiles_per_seg;
-  for (int wt = blockIdx.x; wt < ntiles; wt += gridDim.x) {
+  // the grid strides over the live tiles (segments * tiles_per_seg), from the last one down
+  SYM_FIRST_SEGMENTS(ntiles, m0, m1);
+  int it = 0;
+  for (int ws = blockIdx.x; ws < ntiles; ws += gridDim.x, ++it) {
+    const int wt = ntiles - 1 - ws;
     const int seg = wt / tiles_per_seg;
-    const int e = seg_expert[seg];
-    const int row0 = seg_offset[seg];
-    const int cnt = seg_count[seg];
+    const SegInfo m = SYM_TILE_SEGMENT(it, wt, m0, m1);
+    const int e = m.e, row0 = m.row0, cnt = m.cnt;
     const int tile = wt - seg * tiles_per_seg;
     const int col0 = tile * 16;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -238,12 +310,13 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
     float* __restrict__ y, int tiles_per_seg) {
   // the grid strides over the live tiles; waves are independent (no LDS), so a wave whose
   // columns lie past H just moves on
-  const int ntiles = n_segments[0] * tiles_per_seg;
-  for (int wt = blockIdx.x; wt < ntiles; wt += gridDim.x) {
+  SYM_FIRST_SEGMENTS(ntiles, m0, m1);
+  int it = 0;
+  for (int ws = blockIdx.x; ws < ntiles; ws += gridDim.x, ++it) {
+    const int wt = ntiles - 1 - ws;
     const int seg = wt / tiles_per_seg;
-    const int e = seg_expert[seg];
-    const int row0 = seg_offset[seg];
-    const int cnt = seg_count[seg];
+    const SegInfo m = SYM_TILE_SEGMENT(it, wt, m0, m1);
+    const int e = m.e, row0 = m.row0, cnt = m.cnt;
     const int tile = wt - seg * tiles_per_seg;
     const int wave = threadIdx.x >> 6;
     const int lane = threadIdx.x & 63;
@@ -260,6 +333,87 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
       down_pass<1, U, kDownNT>(hbuf + (size_t)(row0 + mb) * I, I, rows, wd0, wd1, r16, kq, acc0,
                                acc1);
       down_store<1, kDownNT>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
+    }
+  }
+}
+
+// down projection for I <= 512 (NS = I / 64 K-steps), one wave per (segment, 16 output
+// columns) as moe_down_kernel, with two changes that double the weight bytes a wave has in
+// flight at the same occupancy:
+//  * a wave requests its 16 columns' weights over the whole of I at the start of the tile (NS x
+//    32 bytes per lane, one round trip per tile instead of one per batch of 4 K-steps), and
+//    keeps them in registers for every 16-row pass of the segment;
+//  * the segment's h rows (the A operand, shared by the workgroup's 4 waves) are copied once
+//    per pass into LDS by LDS-DMA, wave w moving rows 4w .. 4w+3 (clamped to the last row, so
+//    rows past the segment hold copies of it), and read back per K-step right before the
+//    MFMAs: no registers for A, and a quarter of the L2 reads of h.
+// The h DMA is issued before the weights, so waiting for it (vmcnt) leaves the weights in
+// flight.
+constexpr int kDownLdsSlot = 1024 + 16;  // bytes per staged row: 16 rows of an A read fall in
+                                         // distinct banks (row stride 260 dwords)
+template <int NS>
+__global__ __launch_bounds__(kGemmThreads) void moe_down_lds_kernel(
+    const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
+    const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
+    const int32_t* __restrict__ n_segments, const uint16_t* __restrict__ w_d,
+    float* __restrict__ y, int tiles_per_seg) {
+  static_assert(NS >= 1 && NS * 128 <= 1024, "one LDS-DMA instruction per staged row");
+  __shared__ __align__(16) uint16_t s_h[16 * kDownLdsSlot / 2];
+  SYM_FIRST_SEGMENTS(ntiles, m0, m1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  // a lane's chunk of a staged row (lanes past the row re-read its last 16 bytes and write
+  // them past the row's end inside its slot, never read)
+  const uint32_t dma_off = (uint32_t)min(lane * 16, NS * 128 - 16);
+  const uint16_t* a_frag = s_h + (r16 * kDownLdsSlot + kq * 32) / 2;
+  int it = 0;
+  for (int ws = blockIdx.x; ws < ntiles; ws += gridDim.x, ++it) {
+    const int wt = ntiles - 1 - ws;
+    const int seg = wt / tiles_per_seg;
+    const SegInfo m = SYM_TILE_SEGMENT(it, wt, m0, m1);
+    const int e = m.e, row0 = m.row0, cnt = m.cnt;
+    const int tile = wt - seg * tiles_per_seg;
+    const int col0 = (tile * 4 + wave) * 16;
+    const uint16_t* wd = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * kKLane;
+    uint4 b[NS][2];
+    for (int mb = 0; mb < cnt; mb += 16) {
+      const int rows = min(16, cnt - mb);
+      // every wave is done with the previous pass's rows before they are replaced
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const uint16_t* hb = hbuf + (size_t)(row0 + mb) * I;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = min(wave * 4 + j, rows - 1);
+        dma16(hb + (size_t)r * I, dma_off, s_h + (wave * 4 + j) * (kDownLdsSlot / 2));
+      }
+      if (mb == 0) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          b[s][0] = ld16(wd + (s << 6));
+          b[s][1] = ld16(wd + (s << 6) + kKHalf);
+        }
+        // this wave's rows have landed (the NS x 2 weight loads issued after them may still be
+        // in flight), then every wave's
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NS) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const uint4 a0 = *reinterpret_cast<const uint4*>(a_frag + s * 64);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(a_frag + s * 64 + kKHalf);
+        acc = mfma16x16x32(a0, b[s][0], acc);
+        acc = mfma16x16x32(a1, b[s][1], acc);
+      }
+      float* yrow = y + (size_t)(row0 + mb) * H + col0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = kq * 4 + i;
+        if (r < rows) yrow[(size_t)r * H + r16] = acc[i];
+      }
     }
   }
 }
@@ -354,12 +508,13 @@ __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_fp8_kernel(
     int tiles_per_seg) {
   __shared__ float s_red[4][1][2][4][64];
   // the grid strides over the live tiles (as moe_gate_up_kernel)
-  const int ntiles = n_segments[0] * tiles_per_seg;
-  for (int wt = blockIdx.x; wt < ntiles; wt += gridDim.x) {
+  SYM_FIRST_SEGMENTS(ntiles, m0, m1);
+  int it = 0;
+  for (int ws = blockIdx.x; ws < ntiles; ws += gridDim.x, ++it) {
+    const int wt = ntiles - 1 - ws;
     const int seg = wt / tiles_per_seg;
-    const int e = seg_expert[seg];
-    const int row0 = seg_offset[seg];
-    const int cnt = seg_count[seg];
+    const SegInfo m = SYM_TILE_SEGMENT(it, wt, m0, m1);
+    const int e = m.e, row0 = m.row0, cnt = m.cnt;
     const int tile = wt - seg * tiles_per_seg;
     const int col0 = tile * 16;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -394,12 +549,13 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_fp8_kernel(
     const int32_t* __restrict__ n_segments, const uint8_t* __restrict__ w_d,
     const float* __restrict__ s_d, float* __restrict__ y, int tiles_per_seg) {
   // the grid strides over the live tiles (as moe_down_kernel)
-  const int ntiles = n_segments[0] * tiles_per_seg;
-  for (int wt = blockIdx.x; wt < ntiles; wt += gridDim.x) {
+  SYM_FIRST_SEGMENTS(ntiles, m0, m1);
+  int it = 0;
+  for (int ws = blockIdx.x; ws < ntiles; ws += gridDim.x, ++it) {
+    const int wt = ntiles - 1 - ws;
     const int seg = wt / tiles_per_seg;
-    const int e = seg_expert[seg];
-    const int row0 = seg_offset[seg];
-    const int cnt = seg_count[seg];
+    const SegInfo m = SYM_TILE_SEGMENT(it, wt, m0, m1);
+    const int e = m.e, row0 = m.row0, cnt = m.cnt;
     const int tile = wt - seg * tiles_per_seg;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -579,6 +735,21 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
   const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
   const int steps = I / 64;  // K-steps of 64 per wave (one wave covers all of I)
   const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
+  if (steps <= 8) {
+#define SYM_LAUNCH_DOWN_LDS(NS)                                                                 \
+  case NS:                                                                                      \
+    hipLaunchKernelGGL((moe_down_lds_kernel<NS>), grid, block, 0, (hipStream_t)stream,           \
+                       (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,  \
+                       (const uint16_t*)w_down, y, tiles);                                       \
+    break;
+    switch (steps) {
+      SYM_LAUNCH_DOWN_LDS(1) SYM_LAUNCH_DOWN_LDS(2) SYM_LAUNCH_DOWN_LDS(3)
+      SYM_LAUNCH_DOWN_LDS(4) SYM_LAUNCH_DOWN_LDS(5) SYM_LAUNCH_DOWN_LDS(6)
+      SYM_LAUNCH_DOWN_LDS(7) SYM_LAUNCH_DOWN_LDS(8)
+    }
+#undef SYM_LAUNCH_DOWN_LDS
+    return sym_host::check_launch("moe_down_lds_kernel");
+  }
 #define SYM_LAUNCH_DOWN(UU)                                                                     \
   hipLaunchKernelGGL((moe_down_kernel<UU>), grid, block, 0, (hipStream_t)stream,                 \
                      (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \

@@ -1,4 +1,4 @@
-// Row RMSNorm with an optional fused residual add, bf16 in, fp32 statistics.
+// Row RMSNorm with an optional fused residual add, bf16 or fp32 in, fp32 statistics.
 // Reference: the decoder layer's input_layernorm / post_attention_layernorm and residual adds
 // (modeling_bailing_moe_v2.py:440-468), RMSNorm formula of DeepseekV2RMSNorm
 // (ttnn_normalization.py:54-68):
@@ -13,8 +13,21 @@ namespace sym {
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxPasses = 8;  // cols <= 256 * 8 * 8 = 16384
 
+// 8 consecutive values of a row as fp32: one 16-byte load of bf16, two of fp32
+__device__ __forceinline__ void load8(const uint16_t* p, float (&v)[8]) {
+  unpack8(*reinterpret_cast<const uint4*>(p), v);
+}
+__device__ __forceinline__ void load8(const float* p, float (&v)[8]) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+  v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// TX: uint16_t (bf16 x) or float (fp32 x, e.g. a projection's fp32 output)
+template <typename TX>
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
-    const uint16_t* __restrict__ x, const uint16_t* __restrict__ res,
+    const TX* __restrict__ x, const uint16_t* __restrict__ res,
     const uint16_t* __restrict__ w, int cols, float eps, uint16_t* __restrict__ out,
     float* __restrict__ res_out) {
   __shared__ float s_part[kNormThreads / 64];
@@ -27,7 +40,7 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(
   for (int p = 0; p < kNormMaxPasses; ++p) {
     const int c = (p * kNormThreads + tid) * 8;
     if (c < cols) {
-      unpack8(*reinterpret_cast<const uint4*>(x + base + c), v[p]);
+      load8(x + base + c, v[p]);
       if (res) {
         float r[8];
         unpack8(*reinterpret_cast<const uint4*>(res + base + c), r);
@@ -82,8 +95,28 @@ extern "C" int sym_rmsnorm_bf16(const void* x, const void* residual, const void*
               SYM_ERR_UNSUPPORTED, "rmsnorm: cols=%d (multiple of 8, <= %d)", cols,
               kNormThreads * 8 * kNormMaxPasses);
   (void)hipGetLastError();
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(rows), dim3(kNormThreads), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, (const uint16_t*)residual, (const uint16_t*)weight, cols,
-                     eps, (uint16_t*)out, residual_out);
+  hipLaunchKernelGGL(rmsnorm_kernel<uint16_t>, dim3(rows), dim3(kNormThreads), 0,
+                     (hipStream_t)stream, (const uint16_t*)x, (const uint16_t*)residual,
+                     (const uint16_t*)weight, cols, eps, (uint16_t*)out, residual_out);
+  return sym_host::check_launch("rmsnorm_kernel");
+}
+
+extern "C" int sym_rmsnorm_f32(const float* x, const void* residual, const void* weight, int rows,
+                               int cols, float eps, void* out, float* residual_out,
+                               void* stream) {
+  SYM_REQUIRE(rows >= 0, SYM_ERR_INVALID, "rmsnorm_f32: rows=%d < 0", rows);
+  if (rows == 0) return SYM_OK;
+  SYM_REQUIRE(x && weight && out, SYM_ERR_INVALID, "rmsnorm_f32: null pointer argument");
+  SYM_REQUIRE(!residual || residual_out, SYM_ERR_INVALID,
+              "rmsnorm_f32: residual given without residual_out");
+  SYM_REQUIRE(cols > 0 && cols % 8 == 0 && cols <= kNormThreads * 8 * kNormMaxPasses,
+              SYM_ERR_UNSUPPORTED, "rmsnorm_f32: cols=%d (multiple of 8, <= %d)", cols,
+              kNormThreads * 8 * kNormMaxPasses);
+  SYM_REQUIRE(((uintptr_t)x & 15) == 0 && (!residual_out || ((uintptr_t)residual_out & 15) == 0),
+              SYM_ERR_INVALID, "rmsnorm_f32: x and residual_out must be 16-byte aligned");
+  (void)hipGetLastError();
+  hipLaunchKernelGGL(rmsnorm_kernel<float>, dim3(rows), dim3(kNormThreads), 0,
+                     (hipStream_t)stream, x, (const uint16_t*)residual, (const uint16_t*)weight,
+                     cols, eps, (uint16_t*)out, residual_out);
   return sym_host::check_launch("rmsnorm_kernel");
 }

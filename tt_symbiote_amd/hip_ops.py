@@ -93,15 +93,17 @@ def _check_shape(t: torch.Tensor, name: str, shape: tuple) -> None:
 def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
             residual: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
             residual_out: Optional[torch.Tensor] = None):
-    """RMSNorm over the last dim (bf16 out). With ``residual`` (bf16): returns
-    (normed, x + residual) with the sum in fp32 (the layer's residual stream)."""
-    _check(x, "x", torch.bfloat16)
+    """RMSNorm over the last dim (bf16 out) of x in bf16 or fp32. With ``residual`` (bf16):
+    returns (normed, x + residual) with the sum in fp32 (the layer's residual stream)."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"x: dtype {x.dtype} (bf16 or fp32)")
+    _check(x, "x", x.dtype)
     cols = x.shape[-1]
     rows = x.numel() // cols if cols else 0
     _check(weight, "weight", torch.bfloat16, x.device)
     _check_shape(weight, "weight", (cols,))
     if out is None:
-        out = torch.empty_like(x)
+        out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
     _check(out, "out", torch.bfloat16, x.device)
     _check_shape(out, "out", tuple(x.shape))
     if residual is not None:
@@ -111,8 +113,9 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float,
             residual_out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
         _check(residual_out, "residual_out", torch.float32, x.device)
         _check_shape(residual_out, "residual_out", tuple(x.shape))
-    _lib.call("sym_rmsnorm_bf16", _ptr(x), _ptr(residual), _ptr(weight), rows, cols, float(eps),
-              _ptr(out), _ptr(residual_out), _stream())
+    _lib.call("sym_rmsnorm_f32" if x.dtype == torch.float32 else "sym_rmsnorm_bf16", _ptr(x),
+              _ptr(residual), _ptr(weight), rows, cols, float(eps), _ptr(out),
+              _ptr(residual_out), _stream())
     return (out, residual_out) if residual is not None else out
 
 

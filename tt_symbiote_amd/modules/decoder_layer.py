@@ -95,8 +95,9 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
         positions = positions.to(device=x.device, dtype=torch.int32).contiguous()
         seq_ids = seq_ids.to(device=x.device, dtype=torch.int32).contiguous()
         xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
+        # the dense projection's fp32 output joins the residual in fp32 (one rounding less)
         attn_out = self.attention.prefill_varlen(xn, cu_seqlens, max_seqlen, positions, seq_ids,
-                                                 cache)
+                                                 cache, out_dtype=torch.float32)
         xn2, h1 = hip_ops.rmsnorm(attn_out, self._dev["ln2"], self.eps, residual=x)
         return self.mlp(xn2, residual=h1)
 
@@ -139,14 +140,16 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
                 outputs += (None,)
             return outputs
         if self.is_dense_layer:
-            xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
-            attn_out = attn(
-                xn, position_embeddings=position_embeddings, attention_mask=attention_mask,
-                past_key_values=cache, cache_position=cache_position,
-                position_ids=position_ids)[0]
-            xn2, h1 = hip_ops.rmsnorm(attn_out.contiguous(), self._dev["ln2"], self.eps,
-                                      residual=x)
-            out = self.mlp(xn2, residual=h1)
+            # the attention half as in the MoE layers (input RMSNorm inside the QKV projection,
+            # the residual added in fp32 inside the dense projection); the post-attention
+            # RMSNorm then reads the fp32 residual stream
+            x2 = x.view(B, H)
+            qkv = attn.qkv_projection(x2, self._dev["ln1"], self.eps)
+            o = attn.decode_from_qkv(qkv, attn._cache_of(cache, None), cache_position,
+                                     position_ids)
+            h1, _ = attn.dense_residual(o, x2)
+            xn2 = hip_ops.rmsnorm(h1, self._dev["ln2"], self.eps)
+            out = self.mlp(xn2, residual=h1).view(B, S, H)
         else:
             # input RMSNorm inside the QKV projection; residual add and the post-attention
             # RMSNorm's statistics inside the dense projection; that RMSNorm itself inside the
