@@ -385,7 +385,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_lds_kernel(
       const uint16_t* hb = hbuf + (size_t)(row0 + mb) * I;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int r = min(wave * 4 + j, rows - 1);
+        const int r = __builtin_amdgcn_readfirstlane(min(wave * 4 + j, rows - 1));
         dma16(hb + (size_t)r * I, dma_off, s_h + (wave * 4 + j) * (kDownLdsSlot / 2));
       }
       if (mb == 0) {
@@ -495,10 +495,9 @@ __device__ __forceinline__ void gate_up_pass_fp8(const uint16_t* __restrict__ x,
 }
 
 // gate/up + SwiGLU with fp8 weights: w_gu [E+1, 2I, H] e4m3fn bytes, s_gu [E+1, 2I/128, H/128].
-// Workgroup = (segment, 16 columns of h) as in moe_gate_up_kernel. Both fp8 kernels launch with
-// one 128-wide K-step per load batch (U = 1): 82-90 VGPRs and 4-5 waves per SIMD, where U = 4
-// needs 190 registers (2 per SIMD): 124 against 137 us (gate/up), 79 against 84 us (down) at
-// batch 128.
+// Workgroup = (segment, 16 columns of h) as in moe_gate_up_kernel. It launches with two 128-wide
+// K-steps per load batch (U = 2, 112 VGPRs, 4 waves per SIMD): 99.2 against 101.5 us for U = 1
+// at batch 128 (U = 4 needs 190 registers, 2 waves per SIMD).
 template <int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_fp8_kernel(
     const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
@@ -600,6 +599,116 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_fp8_kernel(
         }
       }
       down_store<1>(acc0, acc1, rows, y + (size_t)(row0 + mb) * H + col0, H, r16, kq);
+    }
+  }
+}
+
+// The conversion of fp8x8_to_bf16x8 into registers that do not overlap the source: with the
+// builtins the compiler converts each weight register in place, which makes it reserve twice
+// the weight registers for a whole tile of loads in flight (196 instead of about 100).
+__device__ __forceinline__ uint4 fp8x8_to_bf16x8_apart(uint32_t w0, uint32_t w1) {
+  uint4 r;
+  asm("v_cvt_scalef32_pk_bf16_fp8 %0, %4, 1.0\n\t"
+      "v_cvt_scalef32_pk_bf16_fp8 %1, %4, 1.0 op_sel:[1,0,0]\n\t"
+      "v_cvt_scalef32_pk_bf16_fp8 %2, %5, 1.0\n\t"
+      "v_cvt_scalef32_pk_bf16_fp8 %3, %5, 1.0 op_sel:[1,0,0]"
+      : "=&v"(r.x), "=&v"(r.y), "=&v"(r.z), "=&v"(r.w)
+      : "v"(w0), "v"(w1));
+  return r;
+}
+
+// mfma_fp8_step with the weights converted by fp8x8_to_bf16x8_apart
+__device__ __forceinline__ floatx4 mfma_fp8_step_apart(const uint4 (&a)[4], const uint4 (&w)[2],
+                                                       floatx4 acc, float scale) {
+  floatx4 t = {0.f, 0.f, 0.f, 0.f};
+  t = mfma16x16x32(a[0], fp8x8_to_bf16x8_apart(w[0].x, w[0].y), t);
+  t = mfma16x16x32(a[1], fp8x8_to_bf16x8_apart(w[0].z, w[0].w), t);
+  t = mfma16x16x32(a[2], fp8x8_to_bf16x8_apart(w[1].x, w[1].y), t);
+  t = mfma16x16x32(a[3], fp8x8_to_bf16x8_apart(w[1].z, w[1].w), t);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] = fmaf(scale, t[i], acc[i]);
+  return acc;
+}
+
+// down projection with fp8 weights for I <= 512 (NS = I / 128 K-steps of 128), laid out as
+// moe_down_lds_kernel: one wave per (segment, 16 output columns); the wave requests its columns'
+// weight bytes over the whole of I (NS x 32 bytes per lane) and the NS block scales at the start
+// of the tile and keeps them for every pass; the segment's h rows are staged in LDS by LDS-DMA
+// once per pass for the workgroup's 4 waves and read back per K-step. Twice the weight bytes in
+// flight per wave of the U = 1 kernel (32 columns, one K-step per batch), at 84 instead of 88
+// registers (5 waves per SIMD). 32 columns per wave here need 136 registers (3 waves per
+// SIMD), or spill when held to 128.
+constexpr int kColsPerWG8Lds = 64;  // 4 waves x 16 columns
+template <int NS>
+__global__ __launch_bounds__(kGemmThreads) void moe_down_fp8_lds_kernel(
+    const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
+    const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
+    const int32_t* __restrict__ n_segments, const uint8_t* __restrict__ w_d,
+    const float* __restrict__ s_d, float* __restrict__ y, int tiles_per_seg) {
+  static_assert(NS >= 1 && NS * 256 <= 1024, "one LDS-DMA instruction per staged row");
+  __shared__ __align__(16) uint16_t s_h[16 * kDownLdsSlot / 2];
+  SYM_FIRST_SEGMENTS(ntiles, m0, m1);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int kq = lane >> 4;
+  const uint32_t dma_off = (uint32_t)min(lane * 16, NS * 256 - 16);
+  // a lane's A fragments of K-step st: 4 x 8 bf16 at k = 128 st + 32 kq + 8 j (the k order of
+  // the weight bytes it holds)
+  const uint16_t* a_frag = s_h + (r16 * kDownLdsSlot + kq * 64) / 2;
+  int it = 0;
+  for (int ws = blockIdx.x; ws < ntiles; ws += gridDim.x, ++it) {
+    const int wt = ntiles - 1 - ws;
+    const int seg = wt / tiles_per_seg;
+    const SegInfo m = SYM_TILE_SEGMENT(it, wt, m0, m1);
+    const int e = m.e, row0 = m.row0, cnt = m.cnt;
+    const int tile = wt - seg * tiles_per_seg;
+    const int col0 = (tile * 4 + wave) * 16;
+    const uint8_t* wd = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * 32;
+    const float* sd = s_d + ((size_t)e * (H >> 7) + (col0 >> 7)) * NS;
+    uint4 b[NS][2];
+    float c[NS];
+    for (int mb = 0; mb < cnt; mb += 16) {
+      const int rows = min(16, cnt - mb);
+      // every wave is done with the previous pass's rows before they are replaced
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      const uint16_t* hb = hbuf + (size_t)(row0 + mb) * I;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = __builtin_amdgcn_readfirstlane(min(wave * 4 + j, rows - 1));
+        dma16(hb + (size_t)r * I, dma_off, s_h + (wave * 4 + j) * (kDownLdsSlot / 2));
+      }
+      if (mb == 0) {
+#pragma unroll
+        for (int st = 0; st < NS; ++st) c[st] = sd[st];
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+          b[st][0] = ld16b(wd + (st << 7));
+          b[st][1] = ld16b(wd + (st << 7) + 16);
+        }
+        // this wave's rows have landed (the 2 NS weight loads issued after them may still be in
+        // flight), then every wave's
+        asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(2 * NS) : "memory");
+      } else {
+        asm volatile("s_waitcnt vmcnt(0)\n\ts_barrier" ::: "memory");
+      }
+      floatx4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        uint4 a[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          a[j] = *reinterpret_cast<const uint4*>(a_frag + st * 128 + 8 * j);
+        acc = mfma_fp8_step_apart(a, b[st], acc, c[st]);
+        // one step's fragments and conversions live at a time
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      float* yrow = y + (size_t)(row0 + mb) * H + col0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = kq * 4 + i;
+        if (r < rows) yrow[(size_t)r * H + r16] = acc[i];
+      }
     }
   }
 }
@@ -835,7 +944,7 @@ extern "C" int sym_moe_gate_up_fp8(const void* x, int T, int H, int I,
   hipLaunchKernelGGL((moe_gate_up_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,          \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
                      n_segments, (const uint8_t*)w_gate_up, s_gate_up, (uint16_t*)h, tiles)
-  SYM_LAUNCH_GATE_UP_FP8(1);
+  SYM_LAUNCH_GATE_UP_FP8(2);
 #undef SYM_LAUNCH_GATE_UP_FP8
   return sym_host::check_launch("moe_gate_up_fp8_kernel");
 }
@@ -850,6 +959,22 @@ extern "C" int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_
   SYM_REQUIRE(h && seg_expert && seg_offset && seg_count && n_segments && w_down && s_down && y,
               SYM_ERR_INVALID, "moe_down_fp8: null pointer argument");
   (void)hipGetLastError();
+  if (I <= 512) {
+    const int tiles = H / kColsPerWG8Lds;
+    const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
+#define SYM_LAUNCH_DOWN_FP8_LDS(NS)                                                             \
+  case NS:                                                                                      \
+    hipLaunchKernelGGL((moe_down_fp8_lds_kernel<NS>), grid, block, 0, (hipStream_t)stream,       \
+                       (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,  \
+                       (const uint8_t*)w_down, s_down, y, tiles);                                \
+    break;
+    switch (I / 128) {
+      SYM_LAUNCH_DOWN_FP8_LDS(1) SYM_LAUNCH_DOWN_FP8_LDS(2) SYM_LAUNCH_DOWN_FP8_LDS(3)
+      SYM_LAUNCH_DOWN_FP8_LDS(4)
+    }
+#undef SYM_LAUNCH_DOWN_FP8_LDS
+    return sym_host::check_launch("moe_down_fp8_lds_kernel");
+  }
   const int tiles = (H + kColsPerWG8 - 1) / kColsPerWG8;
   const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_DOWN_FP8(UU)                                                                 \
