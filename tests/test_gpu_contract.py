@@ -125,6 +125,9 @@ def test_decoder_layer_decode_without_cache_position_uses_the_counter(device):
         with pytest.raises(NotImplementedError, match="cached position"):
             layer(prompt, past_key_values=caches[0], cache_position=pos)
     assert torch.equal(caches[0].key_cache(0), k_before) and caches[0].get_seq_length(0) == 8
+    # the refused calls were recorded in the process-wide coverage ledger as failures
+    assert ts.compatibility.report(layer)["summary"]["runtime_failures"] >= 1
+    ts.compatibility.reset_runtime_observations()
     caches[0].reset()
     layer(prompt, past_key_values=caches[0], cache_position=torch.arange(7, device=device))
     assert caches[0].get_seq_length(0) == 7

@@ -123,6 +123,8 @@ def test_recipe_path_two_layer_model(device):
         for p in model.parameters():
             p.copy_(p.bfloat16().float())
     oracle_layers = [layer for layer in model.model.layers]
+    # the ledger is process-wide: count only this model's calls
+    ts.compatibility.reset_runtime_observations()
     ts.apply_recipe(model, kv_cache_kwargs={"block_size": 16, "max_num_blocks": 64,
                                             "batch_size": 4})
     ts.set_device(model, device)

@@ -196,8 +196,13 @@ def test_prefill_layer_8_prompts_zipf(device):
         if flips:
             margins = selection_margins(logits, gate.expert_bias, **kw)
             assert all(float(margins[t]) < FLIP_MARGIN for t in flips), (s, flips)
-        err = (out[a:b] - ref).abs().max().item()
-        print(f"prompt {s} ({L} tokens): max|gpu-oracle| = {err:.3e}, routing flips {len(flips)}")
+        diff = (out[a:b] - ref).abs()
+        # the 2e-2 bar on top of the bf16 output's own rounding (up to 1.6e-2 where |y| >= 4)
+        err = (diff - _bf16_half_ulp(ref)).max().item()
+        print(f"prompt {s} ({L} tokens): max|gpu-oracle| = {diff.max().item():.3e} "
+              f"({err:.3e} beyond the output's bf16 rounding, max |y| {ref.abs().max().item():.1f}, "
+              f"max|gpu-bf16(oracle)| {(out[a:b] - ref.bfloat16().float()).abs().max().item():.3e}), "
+              f"routing flips {len(flips)}")
         assert err <= TOL
 
 

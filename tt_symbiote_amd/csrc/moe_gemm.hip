@@ -944,7 +944,9 @@ extern "C" int sym_moe_gate_up_fp8(const void* x, int T, int H, int I,
   hipLaunchKernelGGL((moe_gate_up_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,          \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
                      n_segments, (const uint8_t*)w_gate_up, s_gate_up, (uint16_t*)h, tiles)
-  SYM_LAUNCH_GATE_UP_FP8(2);
+  // a wave's K-range is H / 512 steps of 128 (H % 512 == 0): two per batch when it is even
+  if ((H / 512) % 2 == 0) SYM_LAUNCH_GATE_UP_FP8(2);
+  else SYM_LAUNCH_GATE_UP_FP8(1);
 #undef SYM_LAUNCH_GATE_UP_FP8
   return sym_host::check_launch("moe_gate_up_fp8_kernel");
 }
