@@ -63,6 +63,7 @@ def parse_args():
 
 
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "moe_gate_up_kernel.decode_bs32.pmc.json")
+PMC_SUMMARY_FP8 = os.path.join(ROOT, "profiles", "moe_gate_up_fp8_kernel.decode_bs128.pmc.json")
 CALIB_BYTES = 512 << 20
 
 
@@ -79,12 +80,12 @@ def copy_calibration() -> None:
     _log(f"copy calibration: 3 x torch.neg over {CALIB_BYTES >> 20} MiB read + written")
 
 
-def measured_traffic():
+def measured_traffic(path: str = PMC_SUMMARY):
     """HBM bytes per launch of the gate/up kernel from the committed FETCH_SIZE / WRITE_SIZE
     summary of this workload (None when absent)."""
-    if not os.path.exists(PMC_SUMMARY):
+    if not os.path.exists(path):
         return None
-    with open(PMC_SUMMARY) as f:
+    with open(path) as f:
         return json.load(f).get("traffic_bytes")
 
 
@@ -605,7 +606,7 @@ def decode_main(args, fp8: bool) -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None if fp8 else measured_traffic(),
+            "traffic": measured_traffic(PMC_SUMMARY_FP8 if fp8 else PMC_SUMMARY),
             "bytes_per_launch": nbytes["gate_up"],
             "avg_launch_us": gate_up_ms * 1e3,
         },

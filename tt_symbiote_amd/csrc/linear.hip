@@ -300,20 +300,21 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
   }
 }
 
-// Rows in 32-row passes for M > 32 with K = 64 * 4 * kLinWaves: each wave's weights for its 4
-// K-steps are loaded once and stay in registers for every pass. The next pass's activations
+// Rows in passes of 16 * MT rows for M > 32 with K = 64 * 4 * kLinWaves, workgroup y of the grid
+// taking passes y, y + gridDim.y, ...: each wave's weights for its 4 K-steps are loaded once and
+// stay in registers for every pass of the workgroup. The next pass's activations
 // are requested into the same registers as soon as the current pass's MFMAs have read them, so
 // they arrive during the cross-wave reduction and the stores; the epilogue's bias and residual
 // are requested when the pass starts. (The general kernel above re-streams the weights and
 // waits for every load in every pass.)
-template <bool NORM, bool RES>
+template <bool NORM, bool RES, int MT = 2>
 __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ w,
     const uint16_t* __restrict__ bias, int M, int N, int K, const uint16_t* __restrict__ gamma,
     float eps, const uint16_t* __restrict__ residual, float* __restrict__ sumsq_parts,
     uint16_t* __restrict__ out_bf16, float* __restrict__ out_f32) {
-  constexpr int MT = 2, U = 4;
-  static_assert(256 * MT == kLinThreads, "one output element per thread and pass");
+  constexpr int U = 4;
+  static_assert(256 * MT <= kLinThreads, "at most one output element per thread and pass");
   __shared__ float s_red[kLinWaves][MT][4][64];
   __shared__ float s_ss[NORM ? kLinWaves : 1][16 * MT];
   __shared__ float s_r[16 * MT];
@@ -328,7 +329,10 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
   const int k0 = wave * U * 64 + kq * 16;  // this lane's first element of the wave's K range
   const uint16_t* wr = w + (size_t)(col0 + r16) * K + k0;
   // this thread's output element of each pass: element i of lane l's fragment of tile mt
-  const int e_mt = threadIdx.x >> 8, e_l = threadIdx.x & 63, e_i = (threadIdx.x >> 6) & 3;
+  // (with MT = 1 the upper 4 waves have no element: the store is wave-uniformly skipped)
+  const bool e_any = threadIdx.x < 256 * MT;
+  const int e_mt = min((int)(threadIdx.x >> 8), MT - 1), e_l = threadIdx.x & 63,
+            e_i = (threadIdx.x >> 6) & 3;
   const int e_row = e_mt * 16 + 4 * (e_l >> 4) + e_i;  // + mb
   const int e_col = col0 + (e_l & 15);
 
@@ -351,16 +355,18 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
       }
     }
   };
-  load_rows(0);
+  // workgroup y of the grid takes passes y, y + gridDim.y, ...
+  const int mb0 = blockIdx.y * 16 * MT, mstep = gridDim.y * 16 * MT;
+  load_rows(mb0);
   if constexpr (NORM) {
     const uint2 gl = *reinterpret_cast<const uint2*>(gamma + wave * U * 64 + 4 * lane);
     *reinterpret_cast<uint2*>(&s_g[wave * U * 64 + 4 * lane]) = gl;
   }
   const float bias_v = bias ? bf16_to_f32(bias[e_col]) : 0.f;
 
-  for (int mb = 0; mb < M; mb += 16 * MT) {
+  for (int mb = mb0; mb < M; mb += mstep) {
     const int row = mb + e_row;
-    const bool ok = row < M;
+    const bool ok = e_any && row < M;
     float res_v = 0.f;
     if constexpr (RES) res_v = ok ? bf16_to_f32(residual[(size_t)row * N + e_col]) : 0.f;
     floatx4 acc[MT];
@@ -387,23 +393,38 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
         s_r[threadIdx.x] = rsqrtf(t / (float)K + eps);
       }
       __syncthreads();
-#pragma unroll
-      for (int s = 0; s < U; ++s) {
-        gm[s][0] = *reinterpret_cast<const uint4*>(&s_g[k0 + s * 64]);
-        gm[s][1] = *reinterpret_cast<const uint4*>(&s_g[k0 + s * 64 + 8]);
-      }
       // normalised rows in place, one K-step at a time (a scheduling barrier after each keeps
-      // the compiler from converting all of them ahead of the MFMAs)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const float r = s_r[mt * 16 + r16];
+      // the compiler from converting all of them ahead of the MFMAs); with one row tile per
+      // pass gamma is read from LDS per step, which holds one step's fragments in registers
+      if constexpr (MT == 1) {
+        const float r = s_r[r16];
 #pragma unroll
         for (int s = 0; s < U; ++s) {
-          a[mt][s][0] = scale8(a[mt][s][0], gm[s][0], r);
-          a[mt][s][1] = scale8(a[mt][s][1], gm[s][1], r);
-          acc[mt] = mfma16x16x32(a[mt][s][0], b[s][0], acc[mt]);
-          acc[mt] = mfma16x16x32(a[mt][s][1], b[s][1], acc[mt]);
+          const uint4 g0 = *reinterpret_cast<const uint4*>(&s_g[k0 + s * 64]);
+          const uint4 g1 = *reinterpret_cast<const uint4*>(&s_g[k0 + s * 64 + 8]);
+          a[0][s][0] = scale8(a[0][s][0], g0, r);
+          a[0][s][1] = scale8(a[0][s][1], g1, r);
+          acc[0] = mfma16x16x32(a[0][s][0], b[s][0], acc[0]);
+          acc[0] = mfma16x16x32(a[0][s][1], b[s][1], acc[0]);
           __builtin_amdgcn_sched_barrier(0);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < U; ++s) {
+          gm[s][0] = *reinterpret_cast<const uint4*>(&s_g[k0 + s * 64]);
+          gm[s][1] = *reinterpret_cast<const uint4*>(&s_g[k0 + s * 64 + 8]);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const float r = s_r[mt * 16 + r16];
+#pragma unroll
+          for (int s = 0; s < U; ++s) {
+            a[mt][s][0] = scale8(a[mt][s][0], gm[s][0], r);
+            a[mt][s][1] = scale8(a[mt][s][1], gm[s][1], r);
+            acc[mt] = mfma16x16x32(a[mt][s][0], b[s][0], acc[mt]);
+            acc[mt] = mfma16x16x32(a[mt][s][1], b[s][1], acc[mt]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
         }
       }
     } else {
@@ -416,7 +437,7 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
         }
     }
     // the MFMAs have read the rows: the next pass's rows go into the same registers now
-    if (mb + 16 * MT < M) load_rows(mb + 16 * MT);
+    if (mb + mstep < M) load_rows(mb + mstep);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -425,6 +446,10 @@ __global__ __launch_bounds__(kLinThreads) void proj_rows_kernel(
     float v = bias_v;
 #pragma unroll
     for (int wv = 0; wv < kLinWaves; ++wv) v += s_red[wv][e_mt][e_i][e_l];
+    if (!e_any) {
+      __syncthreads();
+      continue;
+    }
     if constexpr (RES) {
       v += res_v;
       if (ok) out_f32[(size_t)row * N + e_col] = v;
@@ -461,14 +486,25 @@ template <bool NORM, bool RES>
 static void launch_proj(const void* x, const void* w, const void* bias, int M, int N, int K,
                         const void* gamma, float eps, const void* residual, float* sumsq_parts,
                         void* out_bf16, float* out_f32, hipStream_t s) {
-  // Above 32 rows with K = 2048: 32-row passes over weights held in registers. Other K above
-  // 32 rows: passes of 64 rows (32 with the norm fused, whose single-batch path a 64-row pass
-  // would leave: 24.4 against 18.7 us for 3072 x 2048 at 64 rows), each streaming the weights.
-  if (M > 32 && K == 64 * 4 * kLinWaves)
-    hipLaunchKernelGGL((proj_rows_kernel<NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
-                       (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,
-                       (const uint16_t*)gamma, eps, (const uint16_t*)residual, sumsq_parts,
-                       (uint16_t*)out_bf16, out_f32);
+  // Above 32 rows with K = 2048: row passes over weights held in registers, the passes spread
+  // over a second grid dimension (the weights of a column tile are re-read from L2 by its
+  // row-block workgroups, which share an XCD: N / 16 is a multiple of 8). Without the norm: one
+  // 32-row pass per workgroup (dense 2048 x 2048 at 128 rows: 19.7 -> 13.4 us). With the norm
+  // fused: two 16-row passes per workgroup, 128 VGPRs so that two workgroups share a CU (QKV
+  // 3072 x 2048 at 128 rows: 25.4 us with 32-row passes in one row block, 25.7 with one 16-row
+  // pass per workgroup, 21.7). Other K above 32 rows: passes of 64 rows (32 with the norm
+  // fused, whose single-batch path a 64-row pass would leave: 24.4 against 18.7 us for 3072 x
+  // 2048 at 64 rows), each streaming the weights.
+  if (M > 32 && K == 64 * 4 * kLinWaves && NORM)
+    hipLaunchKernelGGL((proj_rows_kernel<NORM, RES, 1>), dim3(N / 16, (M + 31) / 32),
+                       dim3(kLinThreads), 0, s, (const uint16_t*)x, (const uint16_t*)w,
+                       (const uint16_t*)bias, M, N, K, (const uint16_t*)gamma, eps,
+                       (const uint16_t*)residual, sumsq_parts, (uint16_t*)out_bf16, out_f32);
+  else if (M > 32 && K == 64 * 4 * kLinWaves)
+    hipLaunchKernelGGL((proj_rows_kernel<NORM, RES, 2>), dim3(N / 16, (M + 31) / 32),
+                       dim3(kLinThreads), 0, s, (const uint16_t*)x, (const uint16_t*)w,
+                       (const uint16_t*)bias, M, N, K, (const uint16_t*)gamma, eps,
+                       (const uint16_t*)residual, sumsq_parts, (uint16_t*)out_bf16, out_f32);
   else if (M > 32 && !NORM)
     hipLaunchKernelGGL((proj_kernel<4, 4, NORM, RES>), dim3(N / 16), dim3(kLinThreads), 0, s,
                        (const uint16_t*)x, (const uint16_t*)w, (const uint16_t*)bias, M, N, K,

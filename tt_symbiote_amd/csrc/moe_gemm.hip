@@ -496,7 +496,7 @@ __device__ __forceinline__ void gate_up_pass_fp8(const uint16_t* __restrict__ x,
 
 // gate/up + SwiGLU with fp8 weights: w_gu [E+1, 2I, H] e4m3fn bytes, s_gu [E+1, 2I/128, H/128].
 // Workgroup = (segment, 16 columns of h) as in moe_gate_up_kernel. It launches with two 128-wide
-// K-steps per load batch (U = 2, 112 VGPRs, 4 waves per SIMD): 99.2 against 101.5 us for U = 1
+// K-steps per load batch (U = 2, 108 VGPRs, 4 waves per SIMD): 99.2 against 101.5 us for U = 1
 // at batch 128 (U = 4 needs 190 registers, 2 waves per SIMD).
 template <int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_fp8_kernel(
