@@ -13,7 +13,13 @@
           --calib-fetch CF.csv --calib-write CW.csv --calib-kernel NAME --calib-bytes N [--json]
       HBM bytes per dispatch of kernel NAME from two ``rocprofv3 --pmc FETCH_SIZE`` /
       ``--pmc WRITE_SIZE`` runs (counter values in KiB per dispatch), each scaled by what the
-      same counter reads per dispatch for a plain copy kernel that reads and writes N bytes.
+      same counter reads per dispatch for a plain copy kernel that reads and writes N bytes;
+
+  python -m tt_symbiote_amd.rocprof_summary clock --trace T.csv --counters C.csv
+          [--kernel NAME ...] [--flops NAME=FLOPS ...]
+      from one ``rocprofv3 --kernel-trace --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES ...``
+      run: per kernel the shader clock over its dispatches and its MFMA use against the
+      MI355X bf16 peak (2.5 PFLOP/s at 2.4 GHz) and against the peak at that measured clock.
 """
 from __future__ import annotations
 
@@ -146,6 +152,74 @@ def pmc_traffic(args) -> dict:
     }
 
 
+XCDS = 8                 # GRBM_GUI_ACTIVE is counted per XCD and summed by rocprofv3
+PEAK_CLOCK_GHZ = 2.4     # the clock of the published 2.5 PFLOP/s dense bf16 peak
+BF16_FLOPS_PER_MFMA_CYCLE = 1024   # per SIMD: v_mfma_f32_16x16x32_bf16 is 16384 flops over 16
+                                   # busy cycles, v_mfma_f32_32x32x16_bf16 32768 over 32
+
+
+def _dispatch_table(trace_csv: str, counter_csv: str) -> list:
+    """[(kernel name, duration ns, {counter: value summed over the dispatch's rows})]"""
+    dur, names = {}, {}
+    with open(trace_csv, newline="") as f:
+        for row in csv.DictReader(f):
+            dur[row["Dispatch_Id"]] = int(row["End_Timestamp"]) - int(row["Start_Timestamp"])
+            names[row["Dispatch_Id"]] = row["Kernel_Name"]
+    counters = defaultdict(lambda: defaultdict(float))
+    with open(counter_csv, newline="") as f:
+        for row in csv.DictReader(f):
+            counters[row["Dispatch_Id"]][row["Counter_Name"]] += float(row["Counter_Value"])
+    return [(names[k], dur[k], dict(c)) for k, c in counters.items() if dur.get(k, 0) > 0]
+
+
+def profiler_window_cycles(table: list) -> tuple:
+    """Least-squares fit GRBM_GUI_ACTIVE = a + b * duration over the dispatches that issue no
+    MFMA: ``a`` is the part of the counter window outside the kernel (the profiler starts and
+    stops the counters around each dispatch), ``b`` the mean summed clock of those kernels."""
+    pts = [(d, c["GRBM_GUI_ACTIVE"]) for _, d, c in table
+           if "GRBM_GUI_ACTIVE" in c and c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0) == 0]
+    n = len(pts)
+    if n < 3:
+        return 0.0, 0.0
+    mx = sum(d for d, _ in pts) / n
+    my = sum(g for _, g in pts) / n
+    sxx = sum((d - mx) ** 2 for d, _ in pts)
+    b = sum((d - mx) * (g - my) for d, g in pts) / sxx
+    return my - b * mx, b
+
+
+def clock_report(trace_csv: str, counter_csv: str, kernels, flops: dict) -> None:
+    table = _dispatch_table(trace_csv, counter_csv)
+    a, b = profiler_window_cycles(table)
+    print(f"counter window outside the kernel: {a:.0f} GRBM cycles (fit over the dispatches "
+          f"without MFMA: {b / XCDS:.3f} GHz per XCD)")
+    per = defaultdict(list)
+    for name, d, c in table:
+        if kernels and not any(k in name for k in kernels):
+            continue
+        per[name].append((d, c))
+    print(f"{'calls':>5} {'us':>8} {'GHz':>6} {'(raw)':>6} {'MFMA TF/s':>10} {'/2.5PF':>7} "
+          f"{'/clk-pk':>7} {'algo TF/s':>10} {'/2.5PF':>7} {'/clk-pk':>7}  kernel")
+    for name, lst in sorted(per.items(), key=lambda kv: -statistics.median(x[0] for x in kv[1])):
+        t = statistics.median(d for d, _ in lst) * 1e-9
+        g = statistics.median(c.get("GRBM_GUI_ACTIVE", 0.0) for _, c in lst)
+        busy = statistics.median(c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) for _, c in lst)
+        clk = (g - a) / XCDS / t * 1e-9
+        raw = g / XCDS / t * 1e-9
+        peak = 2.5e15
+        clk_peak = peak * clk / PEAK_CLOCK_GHZ
+        ex = busy * BF16_FLOPS_PER_MFMA_CYCLE / t
+        line = (f"{len(lst):5d} {t * 1e6:8.1f} {clk:6.3f} {raw:6.3f} {ex / 1e12:10.1f} "
+                f"{ex / peak:7.3f} {ex / clk_peak:7.3f}")
+        algo = [v for k, v in flops.items() if k in name]
+        if algo:
+            al = algo[0] / t
+            line += f" {al / 1e12:10.1f} {al / peak:7.3f} {al / clk_peak:7.3f}"
+        else:
+            line += f" {'':>10} {'':>7} {'':>7}"
+        print(f"{line}  {name.split('(')[0][:60]}")
+
+
 def main(argv=None) -> None:
     ap = argparse.ArgumentParser()
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -167,7 +241,20 @@ def main(argv=None) -> None:
     p.add_argument("--calib-kernel", required=True)
     p.add_argument("--calib-bytes", type=float, required=True)
     p.add_argument("--json", action="store_true")
+    k = sub.add_parser("clock")
+    k.add_argument("--trace", required=True)
+    k.add_argument("--counters", required=True)
+    k.add_argument("--kernel", action="append", default=[])
+    k.add_argument("--flops", action="append", default=[],
+                   help="NAME=FLOPS: algorithmic flops per dispatch of the kernel matching NAME")
     args = ap.parse_args(argv)
+    if args.cmd == "clock":
+        flops = {}
+        for item in args.flops:
+            key, _, val = item.rpartition("=")
+            flops[key] = float(val)
+        clock_report(args.trace, args.counters, args.kernel, flops)
+        return
     if args.cmd == "trace":
         print_trace(args.db, args.top)
         return
