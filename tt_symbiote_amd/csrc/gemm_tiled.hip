@@ -229,59 +229,119 @@ __device__ __forceinline__ uint32_t a_row_offset(const TileArgs& p, const TileLo
 
 // Epilogue of one wave's 64 x (16 NJ) block. The MFMAs take the B fragment as their first
 // operand and A as their second, i.e. compute transposed 16 x 16 tiles: lane l holds row l%16,
-// columns 4*(l/16) .. +3 of each, stored as one 8-byte (bf16) or 16-byte (fp32) write.
+// columns 4*(l/16) .. +3 of each.
 // GATE_UP: tiles j < NJ/2 are gate columns col0 + 16 j .., tiles j + NJ/2 the matching up
 // columns; h = silu(gate) * up. Otherwise tile j is columns col0 + 16 j ..
+// The 4 output values of tile (i, j) held by this lane, for output row orow and first column
+// col (col < N): GATE_UP h, DENSE plus bias and fp32 residual, DOWN as computed.
+template <int MODE, int NJ>
+__device__ __forceinline__ void tile_values(const TileArgs& p, const floatx4 (&acc)[4][NJ], int i,
+                                            int j, size_t orow, int col, float (&v)[4]) {
+  if constexpr (MODE == kGateUp) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      // silu(g) = g / (1 + 2^(-g log2(e))) by v_exp_f32 and v_rcp_f32 (about 1 ulp each;
+      // h is rounded to bf16 next). g -> -inf: 1 / inf = 0; g -> +inf: 1 / 1.
+      const float g = acc[i][j][q], u = acc[i][j + NJ / 2][q];
+      const float e = __builtin_amdgcn_exp2f(g * -1.44269504f);
+      v[q] = g * __builtin_amdgcn_rcpf(1.0f + e) * u;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) v[q] = acc[i][j][q];
+    if constexpr (MODE == kDense) {
+      if (p.bias) {
+        const uint2 b = *reinterpret_cast<const uint2*>(p.bias + col);
+        v[0] += bf16_lo(b.x); v[1] += bf16_hi(b.x); v[2] += bf16_lo(b.y); v[3] += bf16_hi(b.y);
+      }
+      if (p.residual) {
+        const float4 rr = *reinterpret_cast<const float4*>(p.residual + orow * p.N + col);
+        v[0] += rr.x; v[1] += rr.y; v[2] += rr.z; v[3] += rr.w;
+      }
+    }
+  }
+}
+
+// Direct epilogue: each (i, j) tile as one 8-byte (bf16) or 16-byte (fp32) write per lane, i.e.
+// an instruction writes 32 or 64 bytes into each of 16 rows.
 template <int MODE, int NJ>
 __device__ __forceinline__ void store_block(const TileArgs& p, const floatx4 (&acc)[4][NJ],
                                             const TileLoc& loc, int rbase, int col0, int lane) {
   const int r16 = lane & 15, kq = lane >> 4;
+  constexpr int NT = MODE == kGateUp ? NJ / 2 : NJ;  // output tiles per 16-row sub-tile
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int r = rbase + i * 16 + r16;
     if (r >= loc.rows) continue;
     const size_t orow = (size_t)(loc.row0 + r);
-    if constexpr (MODE == kGateUp) {
 #pragma unroll
-      for (int j = 0; j < NJ / 2; ++j) {
-        const int col = col0 + j * 16 + kq * 4;
-        if (col >= p.N) continue;  // N % 16 == 0: the 4 columns are all valid or all not
-        float h[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          // silu(g) = g / (1 + 2^(-g log2(e))) by v_exp_f32 and v_rcp_f32 (about 1 ulp each;
-          // h is rounded to bf16 next). g -> -inf: 1 / inf = 0; g -> +inf: 1 / 1.
-          const float g = acc[i][j][q], u = acc[i][j + NJ / 2][q];
-          const float e = __builtin_amdgcn_exp2f(g * -1.44269504f);
-          h[q] = g * __builtin_amdgcn_rcpf(1.0f + e) * u;
-        }
+    for (int j = 0; j < NT; ++j) {
+      const int col = col0 + j * 16 + kq * 4;
+      if (col >= p.N) continue;  // N % 16 == 0: the 4 columns are all valid or all not
+      float v[4];
+      tile_values<MODE, NJ>(p, acc, i, j, orow, col, v);
+      if (MODE != kGateUp && p.out_f32)
+        *reinterpret_cast<float4*>(p.out_f32 + orow * p.N + col) =
+            make_float4(v[0], v[1], v[2], v[3]);
+      else
         *reinterpret_cast<uint2*>(p.out_bf16 + orow * p.N + col) =
-            make_uint2(pack_bf16x2(h[0], h[1]), pack_bf16x2(h[2], h[3]));
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < NJ; ++j) {
-        const int col = col0 + j * 16 + kq * 4;
-        if (col >= p.N) continue;
-        float v[4] = {acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]};
-        if constexpr (MODE == kDense) {
-          if (p.bias) {
-            const uint2 b = *reinterpret_cast<const uint2*>(p.bias + col);
-            v[0] += bf16_lo(b.x); v[1] += bf16_hi(b.x); v[2] += bf16_lo(b.y); v[3] += bf16_hi(b.y);
-          }
-          if (p.residual) {
-            const float4 rr = *reinterpret_cast<const float4*>(p.residual + orow * p.N + col);
-            v[0] += rr.x; v[1] += rr.y; v[2] += rr.z; v[3] += rr.w;
-          }
-        }
-        if (p.out_f32)
-          *reinterpret_cast<float4*>(p.out_f32 + orow * p.N + col) =
-              make_float4(v[0], v[1], v[2], v[3]);
-        else
-          *reinterpret_cast<uint2*>(p.out_bf16 + orow * p.N + col) =
-              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
-      }
+            make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
     }
+  }
+}
+
+// Epilogue through LDS (bf16 outputs): the wave's 64-row block (COLS = 128 columns, or 64 h
+// columns in GATE_UP) goes into the wave's own LDS region `buf` (64 x COLS bf16) in the MFMA
+// layout and comes back out as whole rows, so that a store instruction writes 1 KB of whole
+// 128-byte lines (4 rows x 256 B or 8 rows x 128 B) instead of 32 bytes into each of 16 rows:
+// the direct epilogue's partial lines made the tile's stores its most expensive phase after the
+// K loop. The region is row-major with its 16-byte chunks XOR-swizzled by row (chunk c of row r
+// at c ^ (r % 16) for 16 chunks per row, c ^ ((r / 2) % 8) for 8), so the 8-byte writes of 16
+// rows and the 16-byte reads of whole rows are both free of bank conflicts. LDS operations of a
+// wave complete in order, so no barrier is needed between the writes and the reads; the caller
+// guarantees that no other wave touches `buf` meanwhile.
+template <int MODE, int NJ>
+__device__ __forceinline__ void store_block_lds(const TileArgs& p, const floatx4 (&acc)[4][NJ],
+                                                const TileLoc& loc, int rbase, int col0,
+                                                int lane, uint16_t* buf) {
+  constexpr int NT = MODE == kGateUp ? NJ / 2 : NJ;
+  constexpr int COLS = NT * 16;   // columns of the wave's block
+  constexpr int CH = COLS / 8;    // 16-byte chunks per row (16 or 8)
+  constexpr int RPI = 64 / CH;    // rows per 1 KB store instruction (4 or 8)
+  // the lane index through an opaque copy: the per-lane addresses below are then computed here,
+  // not hoisted out of a persistent kernel's tile loop, where they would hold registers across
+  // the K loop
+  asm volatile("" : "+v"(lane));
+  const int r16 = lane & 15, kq = lane >> 4;
+  auto slot = [](int row, int ch) {
+    const int sw = CH == 16 ? (row & 15) : ((row >> 1) & 7);
+    return row * COLS + (ch ^ sw) * 8;
+  };
+  const int nrows = min(64, loc.rows - rbase);  // valid rows of the block (wave-uniform)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i * 16 >= nrows) break;
+    const int row = i * 16 + r16;
+    const size_t orow = (size_t)(loc.row0 + rbase + row);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const int col = col0 + j * 16 + kq * 4;
+      if (row >= nrows || col >= p.N) continue;
+      float v[4];
+      tile_values<MODE, NJ>(p, acc, i, j, orow, col, v);
+      *reinterpret_cast<uint2*>(buf + slot(row, 2 * j + (kq >> 1)) + (kq & 1) * 4) =
+          make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    }
+  }
+  const int rl = lane / CH, ch = lane % CH;
+  const int col = col0 + ch * 8;
+#pragma unroll
+  for (int it = 0; it < 64 / RPI; ++it) {
+    if (it * RPI >= nrows) break;
+    const int row = it * RPI + rl;
+    const uint4 v = *reinterpret_cast<const uint4*>(buf + slot(row, ch));
+    if (row < nrows && col < p.N)
+      *reinterpret_cast<uint4*>(p.out_bf16 + (size_t)(loc.row0 + rbase + row) * p.N + col) = v;
   }
 }
 
@@ -466,10 +526,17 @@ __device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_
     default: loop(std::integral_constant<int, 0>{}); break;
   }
   hook();
-  if (!m_on) return;
-
   const int col0 = MODE == kGateUp ? loc.ct * (kTN / 2) + wn * (kWC / 2) : loc.ct * kTN + wn * kWC;
-  store_block<MODE, kNJ>(p, acc, loc, wm * 64, col0, lane);
+  if (MODE == kGateUp || p.out_f32 == nullptr) {
+    // bf16 out, through the stages: every wave has read its last fragments (and thread 0 has
+    // written what the hook writes) before any wave overwrites them; no vmcnt wait, so a vector
+    // atomic of the hook still flies
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    constexpr int kBlockElems = 64 * (MODE == kGateUp ? kWC / 2 : kWC);
+    store_block_lds<MODE, kNJ>(p, acc, loc, wm * 64, col0, lane, smem + wave * kBlockElems);
+  } else if (m_on) {
+    store_block<MODE, kNJ>(p, acc, loc, wm * 64, col0, lane);
+  }
 }
 
 template <int MODE>
@@ -596,9 +663,8 @@ void gemm_tile_persistent(TileArgs p, int nx) {
     const int t = run0 + i;
     const int g = t / nx;
     const TileLoc loc = seg_tile<kTM>(tab, g, t - g * nx);
-    // every wave is done with the previous tile's stages (and s_next) before this tile's DMA
-    // refills them
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    // (every wave passed the barrier after the previous tile's epilogue, whose LDS reads of the
+    // stages had completed: this tile's DMA may refill them)
     big_tile<MODE>(p, loc, smem, [&]() {
       if (threadIdx.x == 0) {
         const int nxt = wpx + pend;
