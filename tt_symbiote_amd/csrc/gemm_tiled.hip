@@ -539,6 +539,154 @@ __device__ __forceinline__ void big_tile(TileArgs p, const TileLoc& loc, uint16_
   }
 }
 
+// ================================================================================================
+// Thin tiles: a 256-column tile of at most 64 valid rows (the persistent grouped kernels' tiles
+// of small experts under skewed routing). big_tile streams the whole weight tile for them but
+// computes one band of four, and each K-step waits a memory round trip with one step of
+// lookahead: per-tile timestamps put such tiles at 80% (gate/up) and 69% (down) of a whole
+// tile's time. Their A part is a quarter (64 rows), so three stages of 64 + 256 rows (40 KB)
+// fit in the 128 KB that big_tile's two stages use: two steps of lookahead. The 8 waves share
+// the DMA (1 A instruction and 4 B instructions each per step); waves 0 and 1 compute the 64 x
+// 128 blocks of the band, as in big_tile.
+// ================================================================================================
+namespace thin {
+constexpr int kTM = 64;
+constexpr int kAStage = kTM * big::kTK;             // bf16 elements (8 KB)
+constexpr int kStage = kAStage + big::kBStage;      // 40 KB
+constexpr int kStages = 3;
+static_assert(kStages * kStage <= 2 * big::kStage, "within big_tile's LDS");
+}  // namespace thin
+
+template <int MODE, typename Hook>
+__device__ __forceinline__ void thin_tile(TileArgs p, const TileLoc& loc, uint16_t* smem,
+                                          Hook hook) {
+  using namespace big;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // the lane index through an opaque copy: the per-lane values below are then computed here, not
+  // hoisted out of the persistent kernel's tile loop (where big_tile's would be held beside them)
+  int lane = tid & 63;
+  asm volatile("" : "+v"(lane));
+  const int wn = wave % kWavesN;
+  const int r16 = lane & 15, kq = lane >> 4;
+  const uint16_t* wbase = tile_weights<MODE>(p, loc);
+
+  // DMA: wave w fills A rows 8w .. 8w + 7 (while the tile has rows there) and B rows 32w ..
+  // 32w + 31 of each stage, lane l taking row + l / 8, chunk slot (l % 8) ^ swz(row)
+  const int lr = lane >> 3;
+  const uint32_t chunk_b = ((lane & 7) ^ swz(lr)) * 16;
+  const bool a_on = wave * kRowsPerDma < loc.rows;
+  uint32_t b_off[kBDma];
+#pragma unroll
+  for (int i = 0; i < kBDma; ++i)
+    b_off[i] = b_row_offset<MODE, kTN>(p, loc.ct, wave * kBRows + lr + kRowsPerDma * i) + chunk_b;
+  const int a_dst = wave * kRowsPerDma * kTK;
+  const int b_dst = thin::kAStage + wave * kBRows * kTK;
+  auto stage_of = [&](int kt) { return smem + (kt % thin::kStages) * thin::kStage; };
+  uint32_t a_off = 0;
+  auto issue_a = [&](int kt) {
+    if (a_on) dma16(p.a, a_off + (uint32_t)kt * (kTK * 2), stage_of(kt) + a_dst);
+  };
+  auto issue_b = [&](int kt) {
+    const uint32_t k = (uint32_t)kt * (kTK * 2);
+#pragma unroll
+    for (int i = 0; i < kBDma; ++i) dma16(wbase, b_off[i] + k, stage_of(kt) + b_dst + i * 512);
+  };
+  const int nk = p.K / kTK;
+  // wait for step kt, leaving what was issued after it in flight: at kt = 0 (issued B0, B1,
+  // A0, A1) step 1's A instruction, or for a wave without A rows step 1's 4 B instructions;
+  // later, step kt + 1's 5 (or 4) instructions, issued after all of step kt
+  auto sync_step = [&](int kt) {
+    if (kt + 1 >= nk) {
+      SYM_TILE_SYNC(0);
+    } else if (kt == 0) {
+      if (a_on) SYM_TILE_SYNC(1);
+      else SYM_TILE_SYNC(4);
+    } else if (a_on) {
+      SYM_TILE_SYNC(5);
+    } else {
+      SYM_TILE_SYNC(4);
+    }
+  };
+
+  // waves 0 and 1 compute: A rows 16 i + r16 of the band, B columns as big_tile's band 0
+  const bool m_on = wave < kWavesN;
+  const int ni = m_on ? min((loc.rows + 15) >> 4, 4) : 0;
+  const int a_frag0 = r16 * kTK;
+  const int b_frag0 = thin::kAStage + ((MODE == kGateUp ? wn * (kWC / 2) : wn * kWC) + r16) * kTK;
+  const int slot0 = (kq ^ swz(r16)) * 8, slot1 = ((4 + kq) ^ swz(r16)) * 8;
+  auto b_row = [](int j) {
+    return MODE == kGateUp ? (j < kNJ / 2 ? 0 : kTN / 2) + (j % (kNJ / 2)) * 16 : j * 16;
+  };
+  floatx4 acc[4][kNJ];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  constexpr int kNF = 4 + kNJ;
+  auto read_frags = [&](auto ni_tag, const uint16_t* stage, int slot, u32x4 (&f)[kNF]) {
+    constexpr int NI = decltype(ni_tag)::value;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+      f[i] = *reinterpret_cast<const u32x4*>(stage + a_frag0 + slot + i * 16 * kTK);
+#pragma unroll
+    for (int j = 0; j < kNJ; ++j)
+      f[4 + j] = *reinterpret_cast<const u32x4*>(stage + b_frag0 + slot + b_row(j) * kTK);
+  };
+  auto mfmas = [&](auto ni_tag, const u32x4 (&f)[kNF]) {
+    constexpr int NI = decltype(ni_tag)::value;
+#pragma unroll
+    for (int i = 0; i < NI; ++i)
+#pragma unroll
+      for (int j = 0; j < kNJ; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, f[4 + j]), __builtin_bit_cast(bf16x8, f[i]), acc[i][j],
+            0, 0, 0);
+  };
+  // Step kt uses stage kt % 3. Iteration kt waits for step kt (step kt + 1 may fly), and the
+  // barrier after that wait also means every wave has finished reading step kt - 1, whose
+  // stage then receives step kt + 2.
+  auto loop = [&](auto ni_tag) {
+    constexpr bool kMfma = decltype(ni_tag)::value > 0;
+    u32x4 fa[kNF], fb[kNF];
+    issue_b(0);
+    if (nk > 1) issue_b(1);
+    a_off = a_row_offset<MODE>(p, loc, min(wave * kRowsPerDma + lr, loc.rows - 1)) + chunk_b;
+    issue_a(0);
+    if (nk > 1) issue_a(1);
+    for (int kt = 0; kt < nk; ++kt) {
+      sync_step(kt);
+      if (kt + 2 < nk) {
+        issue_a(kt + 2);
+        issue_b(kt + 2);
+      }
+      if constexpr (kMfma) {
+        read_frags(ni_tag, stage_of(kt), slot0, fa);
+        read_frags(ni_tag, stage_of(kt), slot1, fb);
+        mfmas(ni_tag, fa);
+        mfmas(ni_tag, fb);
+      }
+    }
+  };
+  switch (ni) {
+    case 4: loop(std::integral_constant<int, 4>{}); break;
+    case 3: loop(std::integral_constant<int, 3>{}); break;
+    case 2: loop(std::integral_constant<int, 2>{}); break;
+    case 1: loop(std::integral_constant<int, 1>{}); break;
+    default: loop(std::integral_constant<int, 0>{}); break;
+  }
+  hook();
+  const int col0 = MODE == kGateUp ? loc.ct * (kTN / 2) + wn * (kWC / 2) : loc.ct * kTN + wn * kWC;
+  constexpr int kCols = MODE == kGateUp ? kWC / 2 : kWC;
+  if (MODE == kGateUp || p.out_f32 == nullptr) {
+    // (as in big_tile: every wave is done with the stages before the epilogue reuses them)
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    store_block_lds<MODE, kNJ>(p, acc, loc, m_on ? 0 : 64, col0, lane, smem + wave * 64 * kCols);
+  } else if (m_on) {
+    store_block<MODE, kNJ>(p, acc, loc, 0, col0, lane);
+  }
+}
+
 template <int MODE>
 __global__ __launch_bounds__(big::kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void gemm_tile_kernel(TileArgs p) {
@@ -550,18 +698,27 @@ void gemm_tile_kernel(TileArgs p) {
 }
 
 // Segment list of the grouped modes in LDS (at most kPersistSeg segments): the first row tile
-// of every segment (segments past the list: the total), its row count, first row and expert.
+// of every segment (segments past the list: the total), the estimated cost of the tiles before
+// it (kTileCost), its row count, first row and expert.
 constexpr int kPersistSeg = 512;
 struct SegTable {
-  int pre[kPersistSeg], cnt[kPersistSeg], off[kPersistSeg];
+  int pre[kPersistSeg], cpre[kPersistSeg], cnt[kPersistSeg], off[kPersistSeg];
   uint16_t exp[kPersistSeg];
-  int total;
+  int total, ctotal;
 };
+
+// Estimated cost of a tile: 16 for a 256-row tile of more than thin::kTM rows, 9 for a thin tile
+// (per-tile timestamps at the prefill workload: thin tiles took 0.56 of a whole tile's time in
+// gate/up, 0.54 in down, and tiles of 65-256 rows about the same as whole ones).
+constexpr int kTileCost = 16, kThinCost = 9;
+__device__ __forceinline__ int row_tile_cost(int cnt, int rt, int tm) {
+  return cnt - rt * tm <= thin::kTM ? kThinCost : kTileCost;
+}
 
 // Wave 0 reads the segment list (all loads in flight together with n_segments; lane l owns
 // segments 8l .. 8l+7) and scans the row-tile counts of tiles of TM rows into the table.
 template <int TM>
-__device__ __forceinline__ void load_seg_table(const TileArgs& p, SegTable& t) {
+__device__ __forceinline__ void load_seg_table(const TileArgs& p, SegTable& t, int nx) {
   const int lane = threadIdx.x & 63;
   if (threadIdx.x >= 64) return;
   int c[8], o[8], e[8];
@@ -574,27 +731,57 @@ __device__ __forceinline__ void load_seg_table(const TileArgs& p, SegTable& t) {
     e[i] = in ? p.seg_expert[sg] : 0;
   }
   const int nseg = p.n_segments[0];
-  int pre[8], run = 0;
+  int pre[8], cpre[8], run = 0, crun = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     pre[i] = run;
-    run += lane * 8 + i < nseg ? (c[i] + TM - 1) / TM : 0;
+    cpre[i] = crun;
+    const int nt = lane * 8 + i < nseg ? (c[i] + TM - 1) / TM : 0;
+    run += nt;
+    // (nt - 1) row tiles of TM rows, then the last one (thin or not)
+    crun += nt ? nx * ((nt - 1) * kTileCost + row_tile_cost(c[i], nt - 1, TM)) : 0;
   }
-  int x = run;  // inclusive scan of the lanes' tile counts
+  int x = run, cx = crun;  // inclusive scans of the lanes' row-tile counts and costs
 #pragma unroll
   for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(x, d);
-    if (lane >= d) x += y;
+    const int y = __shfl_up(x, d), cy = __shfl_up(cx, d);
+    if (lane >= d) {
+      x += y;
+      cx += cy;
+    }
   }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int sg = lane * 8 + i;
     t.pre[sg] = x - run + pre[i];
+    t.cpre[sg] = cx - crun + cpre[i];
     t.cnt[sg] = c[i];
     t.off[sg] = o[i];
     t.exp[sg] = (uint16_t)e[i];
   }
-  if (lane == 63) t.total = x;
+  if (lane == 63) {
+    t.total = x;
+    t.ctotal = cx;
+  }
+}
+
+// The first tile (index row tile * nx + column tile, in segment order) whose estimated cost
+// before it is at least c: the boundary of an XCD's run of tiles of equal cost. Wave-uniform.
+template <int TM>
+__device__ __forceinline__ int tile_at_cost(const SegTable& t, int c, int nx) {
+  if (c <= 0) return 0;
+  if (c >= t.ctotal) return t.total * nx;
+  int lo = 0, hi = kPersistSeg - 1;  // the last segment whose cost prefix is <= c
+  while (lo < hi) {
+    const int md = (lo + hi + 1) >> 1;
+    if (t.cpre[md] <= c) lo = md;
+    else hi = md - 1;
+  }
+  const int cnt = t.cnt[lo], r = c - t.cpre[lo];
+  const int rt = min(r / (nx * kTileCost), (cnt + TM - 1) / TM - 1);
+  const int per = row_tile_cost(cnt, rt, TM);
+  const int ct = (r - rt * nx * kTileCost + per - 1) / per;  // (nx: the next row tile's first)
+  return __builtin_amdgcn_readfirstlane((t.pre[lo] + rt) * nx + ct);
 }
 
 // Row tile g (of TM rows) of the table: the last segment whose first row tile is <= g (binary
@@ -628,8 +815,10 @@ constexpr size_t kTicketBytes = 8 * sizeof(int);
 // finds its segment there. gemm_tile_kernel's per-tile lookup is a memory round trip behind
 // the other workgroups' operand loads that no second workgroup on the CU hides; here only a
 // workgroup's first tile pays it. Workgroups are dispatched to the XCDs round-robin by id, so
-// XCD x = blockIdx.x % 8 owns the contiguous run of tiles that xcd_tile gives it (the column
-// tiles of a row tile and the row tiles of an expert meet in its L2). Its W = gridDim.x / 8
+// XCD x = blockIdx.x % 8 owns a contiguous run of tiles (the column tiles of a row tile and the
+// row tiles of an expert meet in its L2): the x-th of 8 runs of equal estimated cost
+// (kTileCost), since with thin tiles, runs of equal tile count left the XCDs' ends 56 us
+// (gate/up) and 34 us (down) apart under skewed routing. Its W = gridDim.x / 8
 // workgroups take the run's first W tiles in order and then draw the rest from the XCD's
 // ticket counter: tiles of a segment's last rows are shorter, and a static share would leave
 // the workgroups that drew several whole tiles last. Thread 0 draws one tile ahead (the ticket
@@ -644,12 +833,13 @@ void gemm_tile_persistent(TileArgs p, int nx) {
   __shared__ __align__(1024) uint16_t smem[2 * kStage];
   __shared__ SegTable tab;
   __shared__ int s_next;
-  load_seg_table<kTM>(p, tab);
+  load_seg_table<kTM>(p, tab, nx);
   __syncthreads();
-  const int total = tab.total * nx;  // (row tile, column tile) pairs
   const int x = blockIdx.x & 7, wpx = gridDim.x >> 3;
-  const int q = total >> 3, r = total & 7;
-  const int run0 = x * q + min(x, r), run = q + (x < r ? 1 : 0);  // this XCD's tiles
+  // this XCD's tiles: the x-th eighth of the estimated cost
+  const long long ctot = tab.ctotal;
+  const int run0 = tile_at_cost<kTM>(tab, (int)(ctot * x / 8), nx);
+  const int run = tile_at_cost<kTM>(tab, (int)(ctot * (x + 1) / 8), nx) - run0;
   // a per-lane (to the compiler: divergent) address, so the fetch-add is issued as it stands
   // and its result is waited for only where it is used
   int zero = 0;
@@ -665,7 +855,7 @@ void gemm_tile_persistent(TileArgs p, int nx) {
     const TileLoc loc = seg_tile<kTM>(tab, g, t - g * nx);
     // (every wave passed the barrier after the previous tile's epilogue, whose LDS reads of the
     // stages had completed: this tile's DMA may refill them)
-    big_tile<MODE>(p, loc, smem, [&]() {
+    auto hook = [&]() {
       if (threadIdx.x == 0) {
         const int nxt = wpx + pend;
         if (pend == run - 1)
@@ -674,7 +864,9 @@ void gemm_tile_persistent(TileArgs p, int nx) {
           pend = __hip_atomic_fetch_add(ticket, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_next = nxt;
       }
-    });
+    };
+    if (loc.rows <= thin::kTM) thin_tile<MODE>(p, loc, smem, hook);
+    else big_tile<MODE>(p, loc, smem, hook);
     __syncthreads();
     i = __builtin_amdgcn_readfirstlane(s_next);
   }
