@@ -307,6 +307,8 @@ def _gemm_case(T, E, H, I, top_k, seed, device, with_shared=True, skew=False):
     (200, 64, 256, 128, 6, True),       # segments of > 64 rows (several passes)
     (700, 64, 512, 256, 8, True),       # segments of several 128-row tiles
     (300, 64, 512, 192, 6, True),       # I not a multiple of the 128 h columns of a tile
+    (400, 64, 256, 64, 6, True),        # I = 64: the tiled down GEMM's K loop is one step, in
+                                        # thin tiles (at most 64 rows) and whole ones
     # 513 segment entries (E = 512 + shared): the tiled GEMMs leave the persistent kernel for
     # the per-tile lookup kernels (gemm_tile_kernel gate/up, gemm_tile128_kernel down)
     (700, 512, 512, 256, 8, True),      # skewed: segments spanning several 128- and 256-row tiles
