@@ -8,13 +8,16 @@
 // Design (gfx950). What bounds these kernels was measured, not assumed: a wave-wide load of
 // 16 rows x 64 bytes (a 32-column step of K-major rows) reaches ~30 B/clk per CU from L2, one of
 // 8 rows x 128 bytes ~50 B/clk, while LDS reads (~190 B/clk) and back-to-back MFMAs (94% of
-// peak) have room; and the chip clocks down to 1.5-2.1 GHz under these kernels. Two tile shapes:
+// peak) have room; and the chip clocks down to 2.0-2.25 GHz under these kernels. Two tile
+// shapes (and a thin variant of the first):
 //   gemm_tile_kernel / gemm_tile_persistent (dense projections; grouped gate/up and down on a
 //     persistent grid while the segment list has at most 512 entries): 256 x 256 tiles, one
 //     workgroup of 8 waves per CU, each wave a 64 x 128 block (4 x 8 v_mfma_f32_16x16x32_bf16
 //     tiles). The K loop moves 64 columns per step (128-byte rows: whole cache lines) through two
 //     64 KB LDS stages; each step is computed in two 32-column halves whose fragment reads
-//     overlap the other half's MFMAs, with one barrier per step.
+//     overlap the other half's MFMAs, with one barrier per step. In the persistent kernels a
+//     tile of at most 64 valid rows runs thin_tile instead: three 40 KB stages (64 A rows and
+//     256 B rows each), two steps of lookahead.
 //   gemm_tile128_kernel (router logits, N = E = 256: few tiles; grouped down projection over
 //     longer segment lists): 128 x 256 tiles, two workgroups of 8 waves per CU, each
 //     wave a 64 x 64 block; 32 columns per step through a 3-stage 72 KB ring. The second
@@ -26,7 +29,9 @@
 // chunk j of row r sits in slot j ^ swz(r) and the rows of an MFMA fragment read fall in
 // distinct banks. Workgroups are ordered so that each XCD's L2 sees a contiguous run of tiles.
 // The MFMAs compute transposed 16 x 16 tiles, so a lane ends with 4 consecutive columns of one
-// row and the epilogue writes 8 (bf16) or 16 (fp32) bytes per lane.
+// row; bf16 outputs of the 256 x 256 tiles go back out through LDS as whole 128-byte lines
+// (store_block_lds), fp32 outputs and the 128 x 256 tiles write 16 (fp32) or 8 (bf16) bytes per
+// lane directly.
 //   DENSE:   out[M, N] = A[M, K] . W[N, K]^T (+ bias) (+ residual fp32), bf16 or fp32 out.
 //   GATE_UP: rows of a segment gather x[sorted_tokens[row]]; the B tile holds 128 gate rows and
 //            the matching 128 up rows of the expert, so each wave's block pairs 64 gate with 64
