@@ -233,7 +233,8 @@ def _rmsnorm_bf16(x, gamma, eps):
 @pytest.mark.parametrize("M,N,K,bias", [(32, 3072, 2048, False), (64, 3072, 2048, False),
                                         (48, 512, 1024, True), (1, 256, 2048, True),
                                         (70, 128, 192, True), (128, 3072, 2048, False),
-                                        (97, 2048, 2048, True)])
+                                        (97, 2048, 2048, True), (20, 512, 2048, True),
+                                        (20, 3072, 2048, True)])
 def test_rmsnorm_linear(device, M, N, K, bias):
     g = torch.Generator().manual_seed(M * 3 + N + K)
     x = (torch.randn(M, K, generator=g) * 1.5).bfloat16()
@@ -250,6 +251,21 @@ def test_rmsnorm_linear(device, M, N, K, bias):
     out_bf = hip_ops.rmsnorm_linear(x.to(device), gamma.to(device), 1e-6, w.to(device),
                                     None if b is None else b.to(device))
     _close(out_bf, ref, atol=3e-3, rtol=8e-3)
+
+
+def test_rmsnorm_linear_row_blocks_agree(device):
+    # up to 32 rows the fused-norm projection runs 16-row blocks as a grid dimension, above 32
+    # rows 16-row passes over weights held in registers: the same roundings and summation order
+    # per row, so the rows of a batch do not depend on which of them run together
+    g = torch.Generator().manual_seed(11)
+    x = (torch.randn(64, 2048, generator=g) * 1.5).bfloat16().to(device)
+    gamma = (1 + 0.1 * torch.randn(2048, generator=g)).bfloat16().to(device)
+    w = (torch.randn(3072, 2048, generator=g) * 0.02).bfloat16().to(device)
+    full = hip_ops.rmsnorm_linear(x, gamma, 1e-6, w, None, out_dtype=torch.float32).cpu()
+    for m in (1, 15, 20, 32):
+        part = hip_ops.rmsnorm_linear(x[:m].contiguous(), gamma, 1e-6, w, None,
+                                      out_dtype=torch.float32).cpu()
+        assert torch.equal(part, full[:m]), m
 
 
 @pytest.mark.parametrize("M,N,K", [(32, 2048, 2048), (64, 2048, 2048), (5, 256, 512),
