@@ -378,6 +378,10 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
  *   bf16 out, or fp32 when out_fp32 != 0. Replaces the QKV / dense projections at sequence length
  *   > 1 (ttnn_attention.py:2001-2011, 2153-2230). N % 16 == 0, K % 64 == 0; a, w, out and
  *   residual 16-byte aligned, bias 8-byte aligned; a and w each under 4 GB.
+ * sym_gemm_bf16_res_bf16: out[M, N] (fp32) = a . w^T (+ bias) + residual[M, N] (bf16), the sum
+ *   taken in fp32 in the epilogue: the dense projection plus the decoder layer's first residual
+ *   add at sequence length > 1 (ttnn_attention.py:2211-2230 dense, modeling_bailing_moe_v2.py:
+ *   457-460 residual). Same shape rules as sym_gemm_bf16; residual 8-byte aligned.
  * sym_moe_gate_up_tiled / sym_moe_down_tiled: the grouped expert GEMMs of sym_moe_gate_up /
  *   sym_moe_down (same arguments and results; TTNNExperts.forward, ttnn_moe.py:1250-1289) for
  *   segments of many rows; rows = total rows of the segment list (T*top_k + T with the shared
@@ -394,6 +398,8 @@ int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_t* seg_expe
 size_t sym_moe_tiled_workspace_bytes(void);
 int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual, int M,
                   int N, int K, void* out, int out_fp32, void* stream);
+int sym_gemm_bf16_res_bf16(const void* a, const void* w, const void* bias, const void* residual,
+                           int M, int N, int K, float* out, void* stream);
 int sym_moe_gate_up_tiled(const void* x, int T, int H, int I, int rows,
                           const int32_t* sorted_tokens, const int32_t* seg_expert,
                           const int32_t* seg_offset, const int32_t* seg_count,

@@ -31,7 +31,8 @@ def _close(got, want, atol=1e-2, rtol=1e-2):
 
 
 # ------------------------------------------------------------------------------- rmsnorm
-@pytest.mark.parametrize("rows,cols", [(1, 2048), (32, 2048), (5, 136), (3, 16384)])
+@pytest.mark.parametrize("rows,cols", [(1, 2048), (32, 2048), (5, 136), (3, 16384),
+                                       (1001, 2048), (6, 3584)])
 def test_rmsnorm(device, rows, cols):
     g = torch.Generator().manual_seed(rows + cols)
     x = (torch.randn(rows, cols, generator=g) * 2).bfloat16()
@@ -46,6 +47,17 @@ def test_rmsnorm(device, rows, cols):
     ref2 = s_ref.float() * torch.rsqrt(s_ref.float().pow(2).mean(-1, keepdim=True) + 1e-6) \
         * w.float()
     _close(out2, ref2)
+
+
+@pytest.mark.parametrize("rows,cols", [(9942, 2048), (3, 1024), (5, 136)])
+def test_rmsnorm_f32_input(device, rows, cols):
+    # fp32 rows (a projection's output) in, bf16 out: one wave per row for widths of 512 * n
+    g = torch.Generator().manual_seed(rows * 7 + cols)
+    x = torch.randn(rows, cols, generator=g) * 3
+    w = (1 + 0.1 * torch.randn(cols, generator=g)).bfloat16()
+    out = hip_ops.rmsnorm(x.to(device), w.to(device), 1e-6)
+    ref = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()
+    _close(out, ref)
 
 
 # ------------------------------------------------------------------------------- router
@@ -438,6 +450,25 @@ def test_gemm_tiled(device, M, N, K, bias, res, out_dtype):
         torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=1e-4)
     else:
         _close(out, ref, atol=2e-3, rtol=8e-3)
+
+
+@pytest.mark.parametrize("M,N,K,bias", [(9942, 2048, 2048, False), (77, 400, 192, True),
+                                        (8500, 2048, 128, True)])
+def test_gemm_tiled_bf16_residual(device, M, N, K, bias):
+    # the prefill dense projection with the layer's bf16 residual added in the epilogue: the
+    # same fp32 sum as an fp32 output plus the widened residual, bit for bit
+    g = torch.Generator().manual_seed(M * 3 + N + K)
+    a = torch.randn(M, K, generator=g).bfloat16().to(device)
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16().to(device)
+    b = (torch.randn(N, generator=g) * 0.1).bfloat16().to(device) if bias else None
+    r = torch.randn(M, N, generator=g).bfloat16().to(device)
+    out = hip_ops.gemm(a, w, b, r, out_dtype=torch.float32)
+    plain = hip_ops.gemm(a, w, b, out_dtype=torch.float32)
+    assert torch.equal(out.cpu(), plain.cpu() + r.float().cpu())
+    ref = a.float().cpu() @ w.float().cpu().T + (b.float().cpu() if bias else 0.0) + r.float().cpu()
+    torch.testing.assert_close(out.cpu(), ref, rtol=1e-4, atol=1e-4)
+    with pytest.raises(TypeError):
+        hip_ops.gemm(a, w, b, r, out_dtype=torch.bfloat16)
 
 
 def test_combine(device):

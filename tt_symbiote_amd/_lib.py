@@ -128,6 +128,7 @@ _SIGNATURES = {
         [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _c_float, _vp, _vp],
     ),
     "sym_gemm_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp]),
+    "sym_gemm_bf16_res_bf16": (_c_int, [_vp, _vp, _vp, _vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "sym_moe_tiled_workspace_bytes": (_c_size, []),
     "sym_moe_gate_up_tiled": (
         _c_int,

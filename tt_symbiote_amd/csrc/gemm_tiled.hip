@@ -32,7 +32,8 @@
 // row; bf16 outputs of the 256 x 256 tiles go back out through LDS as whole 128-byte lines
 // (store_block_lds), fp32 outputs and the 128 x 256 tiles write 16 (fp32) or 8 (bf16) bytes per
 // lane directly.
-//   DENSE:   out[M, N] = A[M, K] . W[N, K]^T (+ bias) (+ residual fp32), bf16 or fp32 out.
+//   DENSE:   out[M, N] = A[M, K] . W[N, K]^T (+ bias) (+ residual fp32 or bf16), bf16 or
+//            fp32 out.
 //   GATE_UP: rows of a segment gather x[sorted_tokens[row]]; the B tile holds 128 gate rows and
 //            the matching 128 up rows of the expert, so each wave's block pairs 64 gate with 64
 //            up columns and the epilogue writes h = silu(gate) * up (bf16).
@@ -58,6 +59,7 @@ struct TileArgs {
   const uint16_t* w;        // DENSE: [N, K]; GATE_UP: [S, 2I, K]; DOWN: [S, N, K]
   const uint16_t* bias;     // DENSE, optional [N]
   const float* residual;    // DENSE, optional [M, N] fp32
+  const uint16_t* residual_bf16;  // DENSE, optional [M, N] bf16 (added after the fp32 one)
   const int32_t* sorted_tokens;
   const int32_t* seg_expert;
   const int32_t* seg_offset;
@@ -238,7 +240,7 @@ __device__ __forceinline__ uint32_t a_row_offset(const TileArgs& p, const TileLo
 // GATE_UP: tiles j < NJ/2 are gate columns col0 + 16 j .., tiles j + NJ/2 the matching up
 // columns; h = silu(gate) * up. Otherwise tile j is columns col0 + 16 j ..
 // The 4 output values of tile (i, j) held by this lane, for output row orow and first column
-// col (col < N): GATE_UP h, DENSE plus bias and fp32 residual, DOWN as computed.
+// col (col < N): GATE_UP h, DENSE plus bias and residual, DOWN as computed.
 template <int MODE, int NJ>
 __device__ __forceinline__ void tile_values(const TileArgs& p, const floatx4 (&acc)[4][NJ], int i,
                                             int j, size_t orow, int col, float (&v)[4]) {
@@ -262,6 +264,10 @@ __device__ __forceinline__ void tile_values(const TileArgs& p, const floatx4 (&a
       if (p.residual) {
         const float4 rr = *reinterpret_cast<const float4*>(p.residual + orow * p.N + col);
         v[0] += rr.x; v[1] += rr.y; v[2] += rr.z; v[3] += rr.w;
+      }
+      if (p.residual_bf16) {
+        const uint2 rb = *reinterpret_cast<const uint2*>(p.residual_bf16 + orow * p.N + col);
+        v[0] += bf16_lo(rb.x); v[1] += bf16_hi(rb.x); v[2] += bf16_lo(rb.y); v[3] += bf16_hi(rb.y);
       }
     }
   }
@@ -1044,29 +1050,31 @@ static void dense_tail_split(int M, int nx, int cus, int& full_rt, int& tail_row
   }
 }
 
-extern "C" int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual,
-                             int M, int N, int K, void* out, int out_fp32, void* stream) {
-  SYM_REQUIRE(M >= 0, SYM_ERR_INVALID, "gemm_bf16: M=%d < 0", M);
+static int gemm_dense(const char* what, const void* a, const void* w, const void* bias,
+                      const float* residual, const void* residual_bf16, int M, int N, int K,
+                      void* out, int out_fp32, void* stream) {
+  SYM_REQUIRE(M >= 0, SYM_ERR_INVALID, "%s: M=%d < 0", what, M);
   if (M == 0) return SYM_OK;
-  SYM_REQUIRE(a && w && out, SYM_ERR_INVALID, "gemm_bf16: null pointer argument");
+  SYM_REQUIRE(a && w && out, SYM_ERR_INVALID, "%s: null pointer argument", what);
   SYM_REQUIRE(N > 0 && N % 16 == 0, SYM_ERR_UNSUPPORTED,
-              "gemm_bf16: N=%d must be a positive multiple of 16", N);
+              "%s: N=%d must be a positive multiple of 16", what, N);
   SYM_REQUIRE(K > 0 && K % big::kTK == 0, SYM_ERR_UNSUPPORTED,
-              "gemm_bf16: K=%d must be a positive multiple of %d", K, big::kTK);
+              "%s: K=%d must be a positive multiple of %d", what, K, big::kTK);
   namespace C = big;
-  SYM_REQUIRE((M + C::kTM - 1) / C::kTM <= 65535, SYM_ERR_UNSUPPORTED, "gemm_bf16: M=%d too large",
-              M);
+  SYM_REQUIRE((M + C::kTM - 1) / C::kTM <= 65535, SYM_ERR_UNSUPPORTED, "%s: M=%d too large",
+              what, M);
   SYM_REQUIRE(fits_4g(M, K) && fits_4g(N, K), SYM_ERR_UNSUPPORTED,
-              "gemm_bf16: a [%d, %d] or w [%d, %d] is 4 GB or more", M, K, N, K);
+              "%s: a [%d, %d] or w [%d, %d] is 4 GB or more", what, M, K, N, K);
   SYM_REQUIRE(aligned(a, 16) && aligned(w, 16) && aligned(out, 16) && aligned(residual, 16) &&
-                  aligned(bias, 8),
-              SYM_ERR_INVALID, "gemm_bf16: a, w, out and residual must be 16-byte aligned, bias "
-              "8-byte aligned");
+                  aligned(residual_bf16, 8) && aligned(bias, 8),
+              SYM_ERR_INVALID, "%s: a, w, out and an fp32 residual must be 16-byte aligned, "
+              "bias and a bf16 residual 8-byte aligned", what);
   TileArgs p{};
   p.a = (const uint16_t*)a;
   p.w = (const uint16_t*)w;
   p.bias = (const uint16_t*)bias;
   p.residual = residual;
+  p.residual_bf16 = (const uint16_t*)residual_bf16;
   p.M = M;
   p.N = N;
   p.K = K;
@@ -1080,6 +1088,19 @@ extern "C" int sym_gemm_bf16(const void* a, const void* w, const void* bias, con
   hipLaunchKernelGGL((gemm_tile_kernel<kDense>), dim3(nx, rt), dim3(C::kThreads), 0,
                      (hipStream_t)stream, p);
   return sym_host::check_launch("gemm_tile_kernel");
+}
+
+extern "C" int sym_gemm_bf16(const void* a, const void* w, const void* bias, const float* residual,
+                             int M, int N, int K, void* out, int out_fp32, void* stream) {
+  return gemm_dense("gemm_bf16", a, w, bias, residual, nullptr, M, N, K, out, out_fp32, stream);
+}
+
+extern "C" int sym_gemm_bf16_res_bf16(const void* a, const void* w, const void* bias,
+                                      const void* residual, int M, int N, int K, float* out,
+                                      void* stream) {
+  SYM_REQUIRE(M <= 0 || residual, SYM_ERR_INVALID, "gemm_bf16_res_bf16: null residual");
+  return gemm_dense("gemm_bf16_res_bf16", a, w, bias, nullptr, residual, M, N, K, out, 1,
+                    stream);
 }
 
 // Router logits for prefill-size T on MFMA. The fp32 gate weight w [E, H] comes as three bf16

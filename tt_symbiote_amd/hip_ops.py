@@ -148,8 +148,8 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None
 def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
          residual: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.bfloat16,
          out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """a [M, K] . w [N, K]^T (+ bias) (+ residual fp32) with the tiled MFMA kernel (prefill-size
-    M)."""
+    """a [M, K] . w [N, K]^T (+ bias) (+ residual) with the tiled MFMA kernel (prefill-size M).
+    The residual is fp32, or bf16 with an fp32 output (added in fp32 in the epilogue)."""
     _check(a, "a", torch.bfloat16)
     if a.dim() != 2:
         raise ValueError(f"a must be [M, K], got {tuple(a.shape)}")
@@ -161,18 +161,26 @@ def gemm(a: torch.Tensor, w: torch.Tensor, bias: Optional[torch.Tensor] = None,
     if bias is not None:
         _check(bias, "bias", torch.bfloat16, a.device)
         _check_shape(bias, "bias", (N,))
+    res16 = residual is not None and residual.dtype == torch.bfloat16
     if residual is not None:
-        _check(residual, "residual", torch.float32, a.device)
+        _check(residual, "residual", torch.bfloat16 if res16 else torch.float32, a.device)
         _check_shape(residual, "residual", (M, N))
     if out_dtype not in (torch.bfloat16, torch.float32):
         raise TypeError(f"out_dtype {out_dtype} (bf16 or fp32)")
+    if res16 and out_dtype != torch.float32:
+        raise TypeError("a bf16 residual needs out_dtype=torch.float32")
     if out is None:
         out = torch.empty(M, N, dtype=out_dtype, device=a.device)
     _check(out, "out", out_dtype, a.device)
     _check_shape(out, "out", (M, N))
-    _timed("gemm", lambda: _lib.call(
-        "sym_gemm_bf16", _ptr(a), _ptr(w), _ptr(bias), _ptr(residual), M, N, K, _ptr(out),
-        1 if out_dtype == torch.float32 else 0, _stream()))
+    if res16:
+        _timed("gemm", lambda: _lib.call(
+            "sym_gemm_bf16_res_bf16", _ptr(a), _ptr(w), _ptr(bias), _ptr(residual), M, N, K,
+            _ptr(out), _stream()))
+    else:
+        _timed("gemm", lambda: _lib.call(
+            "sym_gemm_bf16", _ptr(a), _ptr(w), _ptr(bias), _ptr(residual), M, N, K, _ptr(out),
+            1 if out_dtype == torch.float32 else 0, _stream()))
     return out
 
 

@@ -215,12 +215,15 @@ class HIPBailingMoEAttention(StatefulHIPModule):
     def prefill_varlen(self, x: torch.Tensor, cu_seqlens: torch.Tensor, max_seqlen: int,
                        positions: torch.Tensor, seq_ids: torch.Tensor,
                        cache: HIPPagedAttentionKVCache,
-                       out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+                       out_dtype: torch.dtype = torch.bfloat16,
+                       residual: Optional[torch.Tensor] = None) -> torch.Tensor:
         """Prefill of packed sequences: x [T, H] (bf16, already normalised by the layer), token
         t of sequence seq_ids[t] at positions[t] (0 .. L-1; page-table row seq_ids[t]). Writes
         the sequences' K/V into the paged cache and returns the attention output after the
         dense projection, [T, H] in ``out_dtype`` (bf16, or fp32 for a caller that adds the
-        residual in fp32). The host counters are not advanced here (the forward methods do).
+        residual in fp32). With ``residual`` (bf16 [T, H]) the output is fp32 and already holds
+        it, added in fp32 in the projection's epilogue. The host counters are not advanced here
+        (the forward methods do).
         With an fp8 cache the K/V are appended per block after the prologue, at the page-table
         row and start position of each sequence's first token."""
         d = self._dev
@@ -240,6 +243,9 @@ class HIPBailingMoEAttention(StatefulHIPModule):
                 cache.value_scale(self.layer_idx), cache.page_table_device,
                 start_pos=positions[first].contiguous(), seq_rows=seq_ids[first].contiguous())
         o = hip_ops.prefill_attention(q, k, v, cu_seqlens, max_seqlen, self.scaling)
+        if residual is not None:
+            return hip_ops.gemm(o.view(-1, self.num_heads * self.head_dim), d["dense_w"],
+                                d["dense_b"], residual=residual, out_dtype=torch.float32)
         return hip_ops.gemm(o.view(-1, self.num_heads * self.head_dim), d["dense_w"],
                             d["dense_b"], out_dtype=out_dtype)
 

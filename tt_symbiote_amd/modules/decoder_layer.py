@@ -95,10 +95,11 @@ class HIPBailingMoEDecoderLayer(StatefulHIPModule):
         positions = positions.to(device=x.device, dtype=torch.int32).contiguous()
         seq_ids = seq_ids.to(device=x.device, dtype=torch.int32).contiguous()
         xn = hip_ops.rmsnorm(x, self._dev["ln1"], self.eps)
-        # the dense projection's fp32 output joins the residual in fp32 (one rounding less)
-        attn_out = self.attention.prefill_varlen(xn, cu_seqlens, max_seqlen, positions, seq_ids,
-                                                 cache, out_dtype=torch.float32)
-        xn2, h1 = hip_ops.rmsnorm(attn_out, self._dev["ln2"], self.eps, residual=x)
+        # the residual joins the dense projection's fp32 accumulator in its epilogue (one
+        # rounding less than a bf16 output, and no separate pass over the fp32 rows)
+        h1 = self.attention.prefill_varlen(xn, cu_seqlens, max_seqlen, positions, seq_ids,
+                                           cache, residual=x)
+        xn2 = hip_ops.rmsnorm(h1, self._dev["ln2"], self.eps)
         return self.mlp(xn2, residual=h1)
 
     def reset_trace_state(self):
