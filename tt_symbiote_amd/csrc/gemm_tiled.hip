@@ -59,7 +59,7 @@ struct TileArgs {
   const uint16_t* w;        // DENSE: [N, K]; GATE_UP: [S, 2I, K]; DOWN: [S, N, K]
   const uint16_t* bias;     // DENSE, optional [N]
   const float* residual;    // DENSE, optional [M, N] fp32
-  const uint16_t* residual_bf16;  // DENSE, optional [M, N] bf16 (added after the fp32 one)
+  const uint16_t* residual_bf16;  // DENSE with out_f32, optional [M, N] bf16 (store_block)
   const int32_t* sorted_tokens;
   const int32_t* seg_expert;
   const int32_t* seg_offset;
@@ -265,10 +265,6 @@ __device__ __forceinline__ void tile_values(const TileArgs& p, const floatx4 (&a
         const float4 rr = *reinterpret_cast<const float4*>(p.residual + orow * p.N + col);
         v[0] += rr.x; v[1] += rr.y; v[2] += rr.z; v[3] += rr.w;
       }
-      if (p.residual_bf16) {
-        const uint2 rb = *reinterpret_cast<const uint2*>(p.residual_bf16 + orow * p.N + col);
-        v[0] += bf16_lo(rb.x); v[1] += bf16_hi(rb.x); v[2] += bf16_lo(rb.y); v[3] += bf16_hi(rb.y);
-      }
     }
   }
 }
@@ -285,12 +281,30 @@ __device__ __forceinline__ void store_block(const TileArgs& p, const floatx4 (&a
     const int r = rbase + i * 16 + r16;
     if (r >= loc.rows) continue;
     const size_t orow = (size_t)(loc.row0 + r);
+    // a bf16 residual: the sub-tile's loads all go out before its stores (a load after a store
+    // to memory that may alias it would wait for its own round trip)
+    uint2 rb[MODE == kDense ? NT : 1];
+    if constexpr (MODE == kDense) {
+      if (p.residual_bf16) {
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          const int col = min(col0 + j * 16 + kq * 4, p.N - 4);
+          rb[j] = *reinterpret_cast<const uint2*>(p.residual_bf16 + orow * p.N + col);
+        }
+      }
+    }
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       const int col = col0 + j * 16 + kq * 4;
       if (col >= p.N) continue;  // N % 16 == 0: the 4 columns are all valid or all not
       float v[4];
       tile_values<MODE, NJ>(p, acc, i, j, orow, col, v);
+      if constexpr (MODE == kDense) {
+        if (p.residual_bf16) {
+          v[0] += bf16_lo(rb[j].x); v[1] += bf16_hi(rb[j].x);
+          v[2] += bf16_lo(rb[j].y); v[3] += bf16_hi(rb[j].y);
+        }
+      }
       if (MODE != kGateUp && p.out_f32)
         *reinterpret_cast<float4*>(p.out_f32 + orow * p.N + col) =
             make_float4(v[0], v[1], v[2], v[3]);
