@@ -143,6 +143,18 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
   const int s_end = ((wave + 1) * nsteps) / kLinWaves;
   const uint16_t* wr = w + (size_t)(col0 + r16) * K + kq * 16;
   const uint16_t* gr = NORM ? gamma + kq * 16 : nullptr;
+  // RES: this thread's residual element of the first pass is requested before the weights (it
+  // does not depend on them), so the epilogue does not wait a round trip for it after the
+  // reduction barrier; later passes (M above 16 * MT * gridDim.y) load theirs there
+  float res_first = 0.f;
+  if constexpr (RES) {
+    if (threadIdx.x < 256 * MT) {
+      const int l = threadIdx.x & 63;
+      const int row = blockIdx.y * 16 * MT + (threadIdx.x >> 8) * 16 + 4 * (l >> 4) +
+                      ((threadIdx.x >> 6) & 3);
+      if (row < M) res_first = bf16_to_f32(residual[(size_t)row * N + col0 + (l & 15)]);
+    }
+  }
 
   for (int mb = blockIdx.y * 16 * MT; mb < M; mb += gridDim.y * 16 * MT) {
     const int nmt = min(MT, (M - mb + 15) >> 4);
@@ -281,7 +293,9 @@ __global__ __launch_bounds__(kLinThreads) void proj_kernel(
       const bool ok = row < M;
       if constexpr (RES) {
         if (ok) {
-          v += bf16_to_f32(residual[(size_t)row * N + col]);
+          v += (mb == blockIdx.y * 16 * MT && e == (int)threadIdx.x)
+                   ? res_first
+                   : bf16_to_f32(residual[(size_t)row * N + col]);
           out_f32[(size_t)row * N + col] = v;
         }
         // sum of squares over the 16 columns of this row (16 consecutive lanes)
