@@ -102,6 +102,21 @@ def test_gemm_and_norm_reject_bad_shapes():
     assert rc == 1  # positions beyond the page table
 
 
+def test_gemm_with_bf16_residual_rejects_bad_arguments():
+    # a, w, bias, residual, M, N, K, out, stream
+    rc, msg = _call("sym_gemm_bf16_res_bf16", FAKE, FAKE, None, None, 64, 2048, 2048, FAKE, None)
+    assert rc == 1 and "residual" in msg
+    rc, _ = _call("sym_gemm_bf16_res_bf16", FAKE, FAKE, None, FAKE, 64, 2040, 2048, FAKE, None)
+    assert rc == 2  # N not a multiple of 16
+    rc, _ = _call("sym_gemm_bf16_res_bf16", FAKE, FAKE, None, FAKE, 64, 2048, 2000, FAKE, None)
+    assert rc == 2  # K not a multiple of 64
+    rc, msg = _call("sym_gemm_bf16_res_bf16", FAKE, FAKE, None, ctypes.c_void_p(18), 64, 2048,
+                    2048, FAKE, None)
+    assert rc == 1 and "aligned" in msg
+    rc, _ = _call("sym_gemm_bf16_res_bf16", FAKE, FAKE, None, None, 0, 2048, 2048, FAKE, None)
+    assert rc == 0  # nothing to do
+
+
 def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "absent.so"))
