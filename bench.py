@@ -449,8 +449,8 @@ def main():
         copy_calibration()
         return
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported on this build "
-              "(one GPU only).", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (one GPU only).",
+              file=sys.stderr)
         sys.exit(2)
     if args.workload == "prefill":
         prefill_main(args)

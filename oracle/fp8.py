@@ -11,7 +11,7 @@ Formats restated here:
     TTNNExperts.from_torch (ttnn_moe.py:1055-1078) would take in place of bf16.
   * A paged KV cache in e4m3fn with one fp32 scale per (block, kv head) (pools laid out as
     TTNNPagedAttentionKVCache, ttnn_attention.py:116-137). The reference keeps its cache in
-    bf16, so the scale rule is this build's (power-of-two scales that grow as a block fills);
+    bf16, so the scale rule is this library's (power-of-two scales that grow as a block fills);
     it is stated by `kv_block_append`.
 
 Every function works on numpy arrays with float32 arithmetic in a fixed order, so a kernel that

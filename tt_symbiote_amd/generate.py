@@ -1,6 +1,6 @@
 """Greedy generation on the device.
 
-The reference generates with HF ``GenerationMixin.generate`` (SURVEY of the reference: the HF
+The reference generates with HF ``GenerationMixin.generate`` (the HF
 token loop calls the TTNN model once per token, reads the logits back and takes the argmax on
 the host; the model's layer loop is Python, one op dispatch at a time;
 modeling_bailing_moe_v2.py:97-334, run_config.py:595-647). Here a batch of prompts is generated

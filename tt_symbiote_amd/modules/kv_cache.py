@@ -15,7 +15,7 @@ power-of-two fp32 scale per (block, kv head) per layer (``key_scale`` / ``value_
 grows. Its V pool is dim-major inside each (block, head), ``[max_num_blocks, num_kv_heads,
 head_dim, block_size]`` (the operand layout of the attention's P.V; ``hip_ops.fp8_v_rows``
 views it as token rows), and block_size is a multiple of 8. The reference's cache is bf16 only;
-the format and its rule are this build's.
+the format and its rule are this library's.
 
 Differences: pools are torch tensors in HBM (one allocation per pool); the page table is
 validated on the host when installed (every entry must name a block of the pool) and copied in

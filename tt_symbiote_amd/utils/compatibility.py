@@ -3,7 +3,7 @@
 Mirrors the observable shape of the reference's ``compatibility.report`` (utils/compatibility.py
 :187-270): ``set_device`` records the swapped modules; every successful HIP forward bumps a
 per-module success counter; a HIP forward that raised is recorded as a failure (the reference
-records a torch fallback there; this build has none). ``regressions`` lists the failing HF
+records a torch fallback there; this library has none). ``regressions`` lists the failing HF
 classes the recipe does not declare as expected CPU classes.
 """
 from __future__ import annotations
