@@ -194,13 +194,14 @@ __device__ __forceinline__ void gate_up_epilogue(float (*s_red)[MT][2][4][64],
 // (count, expert, offset, row count) is loaded in one round trip before the exit test; rows are
 // processed in passes of 16 (a routed expert at decode has a few rows; the shared expert's
 // second pass finds its weight rows in L2).
+constexpr size_t kGateUpLds = sizeof(float) * 4 * 2 * 4 * 64;  // moe_gate_up_kernel's static LDS
 template <int U>
 __global__ __launch_bounds__(kGemmThreads) void moe_gate_up_kernel(
     const uint16_t* __restrict__ x, int H, int I, const int32_t* __restrict__ sorted_tokens,
     const int32_t* __restrict__ seg_expert, const int32_t* __restrict__ seg_offset,
     const int32_t* __restrict__ seg_count, const int32_t* __restrict__ n_segments,
     const uint16_t* __restrict__ w_gu, uint16_t* __restrict__ h, int tiles_per_seg) {
-  __shared__ float s_red[4][1][2][4][64];
+  __shared__ float s_red[4][1][2][4][64];  // kGateUpLds bytes
   // the grid strides over the live tiles (segments * tiles_per_seg), from the last one down
   SYM_FIRST_SEGMENTS(ntiles, m0, m1);
   int it = 0;
@@ -351,6 +352,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
 // flight.
 constexpr int kDownLdsSlot = 1024 + 16;  // bytes per staged row: 16 rows of an A read fall in
                                          // distinct banks (row stride 260 dwords)
+constexpr size_t kDownLds = 16 * kDownLdsSlot;  // moe_down_lds_kernel's static LDS
 template <int NS>
 __global__ __launch_bounds__(kGemmThreads) void moe_down_lds_kernel(
     const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
@@ -790,6 +792,14 @@ using namespace sym;
 // for 5120 / 6144; down 59 against 62 us.
 constexpr int kPersistWGsPerCU = 16;
 
+// The bf16 decode expert GEMMs are launched with dynamic LDS that brings a workgroup's total to
+// 64 KB, so that at most two of them are resident per CU (160 KB of LDS) instead of 3 (gate/up,
+// by registers) or 5 (down): fewer weight streams in flight at once stream faster (batch 32:
+// 225.6 against 227.4-227.9 us per step; down alone at 4 or 3 per CU made no difference, at 1
+// per CU it was 8 us slower). The kernels do not read the dynamic part.
+constexpr size_t kDecodeGemmLds = 64 * 1024;
+static_assert(kGateUpLds < kDecodeGemmLds && kDownLds < kDecodeGemmLds, "the static LDS fits");
+
 static int persistent_grid(int max_tiles) {
   const int n = kPersistWGsPerCU * sym_host::cu_count();
   return max_tiles < n ? max_tiles : n;
@@ -821,7 +831,8 @@ extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t
   const int wave_steps = H / 256;  // K-steps of 64 per wave (4 waves split H)
   const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_GATE_UP(UU)                                                                  \
-  hipLaunchKernelGGL((moe_gate_up_kernel<UU>), grid, block, 0, (hipStream_t)stream,              \
+  hipLaunchKernelGGL((moe_gate_up_kernel<UU>), grid, block, kDecodeGemmLds - kGateUpLds,         \
+                     (hipStream_t)stream,                                                        \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
                      n_segments, (const uint16_t*)w_gate_up, (uint16_t*)h, tiles)
   if (wave_steps % 4 == 0) SYM_LAUNCH_GATE_UP(4);
@@ -847,7 +858,8 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
   if (steps <= 8) {
 #define SYM_LAUNCH_DOWN_LDS(NS)                                                                 \
   case NS:                                                                                      \
-    hipLaunchKernelGGL((moe_down_lds_kernel<NS>), grid, block, 0, (hipStream_t)stream,           \
+    hipLaunchKernelGGL((moe_down_lds_kernel<NS>), grid, block, kDecodeGemmLds - kDownLds,        \
+                       (hipStream_t)stream,                                                      \
                        (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,  \
                        (const uint16_t*)w_down, y, tiles);                                       \
     break;
