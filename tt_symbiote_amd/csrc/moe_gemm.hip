@@ -785,18 +785,20 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
 
 using namespace sym;
 
-// Grid of the decode expert GEMMs: kPersistWGsPerCU workgroups per CU (4 rounds of the 4
-// resident per CU), striding over the live tiles, or fewer when there are fewer tiles at most.
-// Measured at batch 32 (4832 live tiles): 3072 or 4096 workgroups 107 us for gate/up against
-// 113 us for one workgroup per possible tile (8224, most past the live ones exiting at once) or
-// for 5120 / 6144; down 59 against 62 us.
-constexpr int kPersistWGsPerCU = 16;
+// Grid of the decode expert GEMMs: kPersistWGsPerCU workgroups per CU, striding over the live
+// tiles, or fewer when there are fewer tiles at most. Measured with the bf16 kernels at two
+// resident per CU (below), batch 32 (4832 live tiles of 8224 possible): 20 to 32 per CU
+// 223.3-223.8 us per step, 24 223.3-223.6, 16 224.5-225.2, 12 226.3-226.6, 8 228.2-228.5; the
+// fp8 step at batch 128: 24 per CU 334.6-334.9 against 338.1-338.9 us at 16.
+constexpr int kPersistWGsPerCU = 24;
 
 // The bf16 decode expert GEMMs are launched with dynamic LDS that brings a workgroup's total to
 // 64 KB, so that at most two of them are resident per CU (160 KB of LDS) instead of 3 (gate/up,
 // by registers) or 5 (down): fewer weight streams in flight at once stream faster (batch 32:
 // 225.6 against 227.4-227.9 us per step; down alone at 4 or 3 per CU made no difference, at 1
-// per CU it was 8 us slower). The kernels do not read the dynamic part.
+// per CU it was 8 us slower). The kernels do not read the dynamic part. The fp8 kernels keep
+// their own bound (4 and 5 per CU): capped at 3 per CU the fp8 step was no faster, at 2 it was
+// 18 us slower.
 constexpr size_t kDecodeGemmLds = 64 * 1024;
 static_assert(kGateUpLds < kDecodeGemmLds && kDownLds < kDecodeGemmLds, "the static LDS fits");
 
