@@ -246,7 +246,8 @@ def _rmsnorm_bf16(x, gamma, eps):
                                         (48, 512, 1024, True), (1, 256, 2048, True),
                                         (70, 128, 192, True), (128, 3072, 2048, False),
                                         (97, 2048, 2048, True), (20, 512, 2048, True),
-                                        (20, 3072, 2048, True)])
+                                        (20, 3072, 2048, True), (33, 3072, 2048, True),
+                                        (50, 512, 2048, False)])
 def test_rmsnorm_linear(device, M, N, K, bias):
     g = torch.Generator().manual_seed(M * 3 + N + K)
     x = (torch.randn(M, K, generator=g) * 1.5).bfloat16()

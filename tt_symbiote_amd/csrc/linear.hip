@@ -506,11 +506,13 @@ static void launch_proj(const void* x, const void* w, const void* bias, int M, i
   // 32-row pass per workgroup (dense 2048 x 2048 at 128 rows: 19.7 -> 13.4 us). With the norm
   // fused: two 16-row passes per workgroup, 128 VGPRs so that two workgroups share a CU (QKV
   // 3072 x 2048 at 128 rows: 25.4 us with 32-row passes in one row block, 25.7 with one 16-row
-  // pass per workgroup, 21.7). Other K above 32 rows: passes of 64 rows (32 with the norm
-  // fused, whose single-batch path a 64-row pass would leave: 24.4 against 18.7 us for 3072 x
-  // 2048 at 64 rows), each streaming the weights.
+  // pass per workgroup, 21.7); up to 64 rows one 16-row pass per workgroup is faster (QKV at 64
+  // rows: 15.3 against 16.1 us for two passes). Other K above 32 rows: passes of 64 rows (32
+  // with the norm fused, whose single-batch path a 64-row pass would leave: 24.4 against 18.7 us
+  // for 3072 x 2048 at 64 rows), each streaming the weights.
   if (M > 32 && K == 64 * 4 * kLinWaves && NORM)
-    hipLaunchKernelGGL((proj_rows_kernel<NORM, RES, 1>), dim3(N / 16, (M + 31) / 32),
+    hipLaunchKernelGGL((proj_rows_kernel<NORM, RES, 1>),
+                       dim3(N / 16, M <= 64 ? (M + 15) / 16 : (M + 31) / 32),
                        dim3(kLinThreads), 0, s, (const uint16_t*)x, (const uint16_t*)w,
                        (const uint16_t*)bias, M, N, K, (const uint16_t*)gamma, eps,
                        (const uint16_t*)residual, sumsq_parts, (uint16_t*)out_bf16, out_f32);
