@@ -732,17 +732,22 @@ struct SegTable {
   int total, ctotal;
 };
 
-// Estimated cost of a tile: 16 for a 256-row tile of more than thin::kTM rows, 9 for a thin tile
-// (per-tile timestamps at the prefill workload: thin tiles took 0.56 of a whole tile's time in
-// gate/up, 0.54 in down, and tiles of 65-256 rows about the same as whole ones).
-constexpr int kTileCost = 16, kThinCost = 9;
+// Estimated cost of a tile: 16 for a 256-row tile of more than thin::kTM rows, less for a thin
+// tile (per-tile timestamps at the prefill workload: thin tiles took 0.56 of a whole tile's time
+// in gate/up, 0.54 in down, and tiles of 65-256 rows about the same as whole ones). The thin
+// costs were then tuned on the kernel time at that workload: gate/up with 11 took 411-412
+// against 416-418 us with 9 (8: 422-423, 10: 416); down is fastest with 9 (282 against 283-287
+// us with 8, 10 or 11).
+constexpr int kTileCost = 16, kThinCostGateUp = 11, kThinCostDown = 9;
+template <int MODE>
 __device__ __forceinline__ int row_tile_cost(int cnt, int rt, int tm) {
-  return cnt - rt * tm <= thin::kTM ? kThinCost : kTileCost;
+  return cnt - rt * tm <= thin::kTM ? (MODE == kGateUp ? kThinCostGateUp : kThinCostDown)
+                                    : kTileCost;
 }
 
 // Wave 0 reads the segment list (all loads in flight together with n_segments; lane l owns
 // segments 8l .. 8l+7) and scans the row-tile counts of tiles of TM rows into the table.
-template <int TM>
+template <int TM, int MODE>
 __device__ __forceinline__ void load_seg_table(const TileArgs& p, SegTable& t, int nx) {
   const int lane = threadIdx.x & 63;
   if (threadIdx.x >= 64) return;
@@ -764,7 +769,7 @@ __device__ __forceinline__ void load_seg_table(const TileArgs& p, SegTable& t, i
     const int nt = lane * 8 + i < nseg ? (c[i] + TM - 1) / TM : 0;
     run += nt;
     // (nt - 1) row tiles of TM rows, then the last one (thin or not)
-    crun += nt ? nx * ((nt - 1) * kTileCost + row_tile_cost(c[i], nt - 1, TM)) : 0;
+    crun += nt ? nx * ((nt - 1) * kTileCost + row_tile_cost<MODE>(c[i], nt - 1, TM)) : 0;
   }
   int x = run, cx = crun;  // inclusive scans of the lanes' row-tile counts and costs
 #pragma unroll
@@ -792,7 +797,7 @@ __device__ __forceinline__ void load_seg_table(const TileArgs& p, SegTable& t, i
 
 // The first tile (index row tile * nx + column tile, in segment order) whose estimated cost
 // before it is at least c: the boundary of an XCD's run of tiles of equal cost. Wave-uniform.
-template <int TM>
+template <int TM, int MODE>
 __device__ __forceinline__ int tile_at_cost(const SegTable& t, int c, int nx) {
   if (c <= 0) return 0;
   if (c >= t.ctotal) return t.total * nx;
@@ -804,7 +809,7 @@ __device__ __forceinline__ int tile_at_cost(const SegTable& t, int c, int nx) {
   }
   const int cnt = t.cnt[lo], r = c - t.cpre[lo];
   const int rt = min(r / (nx * kTileCost), (cnt + TM - 1) / TM - 1);
-  const int per = row_tile_cost(cnt, rt, TM);
+  const int per = row_tile_cost<MODE>(cnt, rt, TM);
   const int ct = (r - rt * nx * kTileCost + per - 1) / per;  // (nx: the next row tile's first)
   return __builtin_amdgcn_readfirstlane((t.pre[lo] + rt) * nx + ct);
 }
@@ -858,13 +863,13 @@ void gemm_tile_persistent(TileArgs p, int nx) {
   __shared__ __align__(1024) uint16_t smem[2 * kStage];
   __shared__ SegTable tab;
   __shared__ int s_next;
-  load_seg_table<kTM>(p, tab, nx);
+  load_seg_table<kTM, MODE>(p, tab, nx);
   __syncthreads();
   const int x = blockIdx.x & 7, wpx = gridDim.x >> 3;
   // this XCD's tiles: the x-th eighth of the estimated cost
   const long long ctot = tab.ctotal;
-  const int run0 = tile_at_cost<kTM>(tab, (int)(ctot * x / 8), nx);
-  const int run = tile_at_cost<kTM>(tab, (int)(ctot * (x + 1) / 8), nx) - run0;
+  const int run0 = tile_at_cost<kTM, MODE>(tab, (int)(ctot * x / 8), nx);
+  const int run = tile_at_cost<kTM, MODE>(tab, (int)(ctot * (x + 1) / 8), nx) - run0;
   // a per-lane (to the compiler: divergent) address, so the fetch-add is issued as it stands
   // and its result is waited for only where it is used
   int zero = 0;
