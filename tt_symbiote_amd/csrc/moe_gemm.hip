@@ -344,17 +344,21 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_kernel(
 //  * a wave requests its 16 columns' weights over the whole of I at the start of the tile (NS x
 //    32 bytes per lane, one round trip per tile instead of one per batch of 4 K-steps), and
 //    keeps them in registers for every 16-row pass of the segment;
-//  * the segment's h rows (the A operand, shared by the workgroup's 4 waves) are copied once
-//    per pass into LDS by LDS-DMA, wave w moving rows 4w .. 4w+3 (clamped to the last row, so
+//  * the segment's h rows (the A operand, shared by the workgroup's waves) are copied once
+//    per pass into LDS by LDS-DMA, wave w moving rows 8w .. 8w+7 (clamped to the last row, so
 //    rows past the segment hold copies of it), and read back per K-step right before the
-//    MFMAs: no registers for A, and a quarter of the L2 reads of h.
+//    MFMAs: no registers for A, and half the L2 reads of h.
 // The h DMA is issued before the weights, so waiting for it (vmcnt) leaves the weights in
-// flight.
+// flight. A workgroup is kDownWaves = 2 waves (32 columns): small workgroups that drift apart
+// keep a CU streaming through each other's barriers and stores (batch 32, 3 resident per CU:
+// down 53.9-54.0 us against 56.8-57.1 for 4-wave workgroups at 2 per CU; 8-wave workgroups
+// 58.2-58.6 at 2 per CU and 64.2-64.4 at 1 per CU; 1-wave workgroups at 6 per CU 54.4-54.6).
 constexpr int kDownLdsSlot = 1024 + 16;  // bytes per staged row: 16 rows of an A read fall in
                                          // distinct banks (row stride 260 dwords)
 constexpr size_t kDownLds = 16 * kDownLdsSlot;  // moe_down_lds_kernel's static LDS
+constexpr int kDownWaves = 2;                     // waves (16 columns each) per workgroup
 template <int NS>
-__global__ __launch_bounds__(kGemmThreads) void moe_down_lds_kernel(
+__global__ __launch_bounds__(64 * kDownWaves) void moe_down_lds_kernel(
     const uint16_t* __restrict__ hbuf, int H, int I, const int32_t* __restrict__ seg_expert,
     const int32_t* __restrict__ seg_offset, const int32_t* __restrict__ seg_count,
     const int32_t* __restrict__ n_segments, const uint16_t* __restrict__ w_d,
@@ -377,7 +381,7 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_lds_kernel(
     const SegInfo m = SYM_TILE_SEGMENT(it, wt, m0, m1);
     const int e = m.e, row0 = m.row0, cnt = m.cnt;
     const int tile = wt - seg * tiles_per_seg;
-    const int col0 = (tile * 4 + wave) * 16;
+    const int col0 = (tile * kDownWaves + wave) * 16;
     const uint16_t* wd = w_d + ((size_t)e * H + col0 + r16) * (size_t)I + kq * kKLane;
     uint4 b[NS][2];
     for (int mb = 0; mb < cnt; mb += 16) {
@@ -385,10 +389,11 @@ __global__ __launch_bounds__(kGemmThreads) void moe_down_lds_kernel(
       // every wave is done with the previous pass's rows before they are replaced
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       const uint16_t* hb = hbuf + (size_t)(row0 + mb) * I;
+      constexpr int kRowsPerWave = 16 / kDownWaves;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int r = __builtin_amdgcn_readfirstlane(min(wave * 4 + j, rows - 1));
-        dma16(hb + (size_t)r * I, dma_off, s_h + (wave * 4 + j) * (kDownLdsSlot / 2));
+      for (int j = 0; j < kRowsPerWave; ++j) {
+        const int r = __builtin_amdgcn_readfirstlane(min(wave * kRowsPerWave + j, rows - 1));
+        dma16(hb + (size_t)r * I, dma_off, s_h + (wave * kRowsPerWave + j) * (kDownLdsSlot / 2));
       }
       if (mb == 0) {
 #pragma unroll
@@ -785,25 +790,31 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
 
 using namespace sym;
 
-// Grid of the decode expert GEMMs: kPersistWGsPerCU workgroups per CU, striding over the live
-// tiles, or fewer when there are fewer tiles at most. Measured with the bf16 kernels at two
-// resident per CU (below), batch 32 (4832 live tiles of 8224 possible): 20 to 32 per CU
+// Grid of the decode expert GEMMs: kPersistWGsPerCU workgroups per CU (kDownWGsPerCU for the
+// bf16 down kernel), striding over the live tiles, or fewer when there are fewer tiles at most.
+// Measured with the bf16 kernels at two resident per CU (below), batch 32 (4832 live tiles of
+// 8224 possible): 20 to 32 per CU
 // 223.3-223.8 us per step, 24 223.3-223.6, 16 224.5-225.2, 12 226.3-226.6, 8 228.2-228.5; the
 // fp8 step at batch 128: 24 per CU 334.6-334.9 against 338.1-338.9 us at 16.
 constexpr int kPersistWGsPerCU = 24;
 
-// The bf16 decode expert GEMMs are launched with dynamic LDS that brings a workgroup's total to
-// 64 KB, so that at most two of them are resident per CU (160 KB of LDS) instead of 3 (gate/up,
-// by registers) or 5 (down): fewer weight streams in flight at once stream faster (batch 32:
-// 225.6 against 227.4-227.9 us per step; down alone at 4 or 3 per CU made no difference, at 1
-// per CU it was 8 us slower). The kernels do not read the dynamic part. The fp8 kernels keep
-// their own bound (4 and 5 per CU): capped at 3 per CU the fp8 step was no faster, at 2 it was
-// 18 us slower.
+// The bf16 decode expert GEMMs are launched with dynamic LDS (not read by the kernels) that
+// bounds how many of them share a CU's 160 KB: gate/up at 64 KB, so at most 2 per CU (8 waves)
+// instead of 3 by registers; fewer weight streams in flight at once stream faster (batch 32,
+// with down's 4-wave workgroups also held to 2: 225.6 against 227.4-227.9 us per step). Down
+// runs 2-wave workgroups held to 3 per CU (below). The fp8 kernels keep their own bound (4 and
+// 5 per CU): capped at 3 per CU the fp8 step was no faster, at 2 it was 18 us slower.
 constexpr size_t kDecodeGemmLds = 64 * 1024;
-static_assert(kGateUpLds < kDecodeGemmLds && kDownLds < kDecodeGemmLds, "the static LDS fits");
+// moe_down_lds_kernel's 2-wave workgroups are held to 3 per CU (48 KB each; 6 waves per CU): at
+// 2 per CU the step took 233.6-233.9 us, at 4 or 5 per CU 223.0-223.5, at 3 per CU 220.3-221.1,
+// and 32 workgroups per CU in the grid (9664 live tiles at batch 32) 220.0-220.5 against
+// 220.7-221.1 at 48, 220.8-221.0 at 28 and 222.0-223.3 at 16-24.
+constexpr size_t kDownGemmLds = 48 * 1024;
+constexpr int kDownWGsPerCU = 32;
+static_assert(kGateUpLds < kDecodeGemmLds && kDownLds < kDownGemmLds, "the static LDS fits");
 
-static int persistent_grid(int max_tiles) {
-  const int n = kPersistWGsPerCU * sym_host::cu_count();
+static int persistent_grid(int max_tiles, int per_cu = kPersistWGsPerCU) {
+  const int n = per_cu * sym_host::cu_count();
   return max_tiles < n ? max_tiles : n;
 }
 
@@ -854,13 +865,14 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
   SYM_REQUIRE(h && seg_expert && seg_offset && seg_count && n_segments && w_down && y,
               SYM_ERR_INVALID, "moe_down: null pointer argument");
   (void)hipGetLastError();
-  const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
   const int steps = I / 64;  // K-steps of 64 per wave (one wave covers all of I)
-  const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
   if (steps <= 8) {
+    const int tiles = H / (16 * kDownWaves);
+    const dim3 grid(persistent_grid(max_segments * tiles, kDownWGsPerCU)),
+        block(64 * kDownWaves);
 #define SYM_LAUNCH_DOWN_LDS(NS)                                                                 \
   case NS:                                                                                      \
-    hipLaunchKernelGGL((moe_down_lds_kernel<NS>), grid, block, kDecodeGemmLds - kDownLds,        \
+    hipLaunchKernelGGL((moe_down_lds_kernel<NS>), grid, block, kDownGemmLds - kDownLds,        \
                        (hipStream_t)stream,                                                      \
                        (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,  \
                        (const uint16_t*)w_down, y, tiles);                                       \
@@ -873,6 +885,8 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
 #undef SYM_LAUNCH_DOWN_LDS
     return sym_host::check_launch("moe_down_lds_kernel");
   }
+  const int tiles = (H + kColsPerWG - 1) / kColsPerWG;
+  const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
 #define SYM_LAUNCH_DOWN(UU)                                                                     \
   hipLaunchKernelGGL((moe_down_kernel<UU>), grid, block, 0, (hipStream_t)stream,                 \
                      (const uint16_t*)h, H, I, seg_expert, seg_offset, seg_count, n_segments,    \
