@@ -811,6 +811,9 @@ constexpr size_t kDecodeGemmLds = 64 * 1024;
 // 220.7-221.1 at 48, 220.8-221.0 at 28 and 222.0-223.3 at 16-24.
 constexpr size_t kDownGemmLds = 48 * 1024;
 constexpr int kDownWGsPerCU = 32;
+// The fp8 gate/up and LDS down kernels (batch 128: 7904 live tiles each): 40 workgroups per CU,
+// one per tile, 331.5-332.1 us per fp8 step against 333.2-334.0 at 24 (48 and 64 the same as 40).
+constexpr int kFp8WGsPerCU = 40;
 static_assert(kGateUpLds < kDecodeGemmLds && kDownLds < kDownGemmLds, "the static LDS fits");
 
 static int persistent_grid(int max_tiles, int per_cu = kPersistWGsPerCU) {
@@ -967,7 +970,7 @@ extern "C" int sym_moe_gate_up_fp8(const void* x, int T, int H, int I,
               SYM_ERR_INVALID, "moe_gate_up_fp8: null pointer argument");
   (void)hipGetLastError();
   const int tiles = I / 16;
-  const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
+  const dim3 grid(persistent_grid(max_segments * tiles, kFp8WGsPerCU)), block(kGemmThreads);
 #define SYM_LAUNCH_GATE_UP_FP8(UU)                                                              \
   hipLaunchKernelGGL((moe_gate_up_fp8_kernel<UU>), grid, block, 0, (hipStream_t)stream,          \
                      (const uint16_t*)x, H, I, sorted_tokens, seg_expert, seg_offset, seg_count, \
@@ -991,7 +994,7 @@ extern "C" int sym_moe_down_fp8(const void* h, int T, int H, int I, const int32_
   (void)hipGetLastError();
   if (I <= 512) {
     const int tiles = H / kColsPerWG8Lds;
-    const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
+    const dim3 grid(persistent_grid(max_segments * tiles, kFp8WGsPerCU)), block(kGemmThreads);
 #define SYM_LAUNCH_DOWN_FP8_LDS(NS)                                                             \
   case NS:                                                                                      \
     hipLaunchKernelGGL((moe_down_fp8_lds_kernel<NS>), grid, block, 0, (hipStream_t)stream,       \
