@@ -811,6 +811,11 @@ constexpr size_t kDecodeGemmLds = 64 * 1024;
 // 220.7-221.1 at 48, 220.8-221.0 at 28 and 222.0-223.3 at 16-24.
 constexpr size_t kDownGemmLds = 48 * 1024;
 constexpr int kDownWGsPerCU = 32;
+// Above 32 rows more experts are live and their tiles outnumber those grids: gate/up at 32 and
+// down at 56 per CU took the whole-model decode at batch 64 from 6.76 to 6.67-6.68 ms per step
+// (gate/up at 32 alone 6.71; both at 40 / 64 6.68), while at batch 32 they cost 1.5 us.
+constexpr int kPersistWGsPerCULarge = 32;
+constexpr int kDownWGsPerCULarge = 56;
 // The fp8 gate/up and LDS down kernels (batch 128: 7904 live tiles each): 40 workgroups per CU,
 // one per tile, 331.5-332.1 us per fp8 step against 333.2-334.0 at 24 (48 and 64 the same as 40).
 constexpr int kFp8WGsPerCU = 40;
@@ -845,7 +850,9 @@ extern "C" int sym_moe_gate_up(const void* x, int T, int H, int I, const int32_t
   (void)hipGetLastError();
   const int tiles = I / 16;
   const int wave_steps = H / 256;  // K-steps of 64 per wave (4 waves split H)
-  const dim3 grid(persistent_grid(max_segments * tiles)), block(kGemmThreads);
+  const dim3 grid(persistent_grid(max_segments * tiles, T > 32 ? kPersistWGsPerCULarge
+                                                               : kPersistWGsPerCU)),
+      block(kGemmThreads);
 #define SYM_LAUNCH_GATE_UP(UU)                                                                  \
   hipLaunchKernelGGL((moe_gate_up_kernel<UU>), grid, block, kDecodeGemmLds - kGateUpLds,         \
                      (hipStream_t)stream,                                                        \
@@ -871,7 +878,8 @@ extern "C" int sym_moe_down(const void* h, int T, int H, int I, const int32_t* s
   const int steps = I / 64;  // K-steps of 64 per wave (one wave covers all of I)
   if (steps <= 8) {
     const int tiles = H / (16 * kDownWaves);
-    const dim3 grid(persistent_grid(max_segments * tiles, kDownWGsPerCU)),
+    const dim3 grid(persistent_grid(max_segments * tiles,
+                                    T > 32 ? kDownWGsPerCULarge : kDownWGsPerCU)),
         block(64 * kDownWaves);
 #define SYM_LAUNCH_DOWN_LDS(NS)                                                                 \
   case NS:                                                                                      \
