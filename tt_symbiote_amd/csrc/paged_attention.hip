@@ -1404,12 +1404,12 @@ static int launch_decode(const char* what, const void* q, const FusedQKV* fq, vo
   // mapping from row to row; the extra split starts at or past max_context and exits at once.
   // (fp8 batch 128, 1024-8192 tokens: 32 -> 33 splits, 153 -> 123 us.)
   const dim3 grid(max_splits | 1, Hkv, B), block(kAttnThreads);
-  // live workgroups first in dispatch order (decode_item), up to 256 sequences, for the bf16
-  // cache: batch 32 with 128-4096 cached tokens (about one round of workgroups), split kernel
-  // 26.6-26.7 against 27.6-27.7 us. The fp8 cache's batch 128 with 1024-8192 tokens (several
-  // rounds) runs slower that way (120.6-120.9 against 115.3-116.5 us) and keeps the odd-width
-  // grid order.
-  const int compact = !fp8 && B <= 256 ? 1 : 0;
+  // live workgroups first in dispatch order (decode_item), for the bf16 cache up to 32
+  // sequences: batch 32 with 128-4096 cached tokens (about one round of workgroups), split kernel
+  // 26.6-26.7 against 27.6-27.7 us. With several rounds the odd-width grid order is faster: the
+  // whole model at batch 64 with 2048-2176 tokens, 6.63-6.64 against 6.67 ms per step; the fp8
+  // cache's batch 128 with 1024-8192 tokens, 115.3-116.5 against 120.6-120.9 us.
+  const int compact = !fp8 && B <= 32 ? 1 : 0;
   const uint16_t* qq = (const uint16_t*)q;
   uint16_t* kp = (uint16_t*)k_pool;
   uint16_t* vp = (uint16_t*)v_pool;
