@@ -14,9 +14,9 @@
 // sorted_tokens) form the A operand; rows past the segment repeat its last row and their outputs are dropped. Both operands use the
 // same lane -> K mapping, so the K order inside a step is free to follow memory order. Up to
 // MT row tiles (16 rows each) are accumulated per pass over the weights.
-// Segments live on the device: a fixed grid (24 workgroups per CU) strides over the live tiles
-// (*n_segments of them times the tiles per segment), so no host synchronization is needed and no
-// workgroup is launched only to find its segment absent.
+// Segments live on the device: a grid of a fixed size per kernel and batch (24 to 56 workgroups
+// per CU, the constants below) strides over the live tiles (*n_segments of them times the tiles
+// per segment), so no host synchronization is needed.
 #include "common.h"
 
 namespace sym {
