@@ -507,6 +507,7 @@ def _dev_ctx(ctx, device):
     (3, 16, 2, 64, 250, 260),
     (5, 16, 16, 32, 1, 300),
     (2, 32, 4, 32, 1000, 3000),
+    (48, 16, 4, 32, 100, 1500),    # above 32 sequences: the odd-width grid order
 ])
 def test_paged_decode(device, B, Hq, Hkv, bs, lo, hi):
     ctx = paged_context(B, lo, hi, block_size=bs, num_kv_heads=Hkv, seed=B + Hq + bs)
@@ -659,6 +660,7 @@ def test_decode_prologue(device, rotary_dim, use_norm):
     (5, 16, 2, 128, False, 0, 300, 16, None),      # 8 q heads per kv head
     (6, 8, 8, 64, True, 250, 600, 64, None),       # 1 q head per kv head
     (6, 16, 4, 64, True, 100, 700, 32, 512),       # some positions beyond the attention cap
+    (40, 16, 4, 64, True, 5, 2000, 32, None),      # above 32 sequences: odd-width grid order
 ])
 def test_decode_step_matches_prologue_then_decode(device, B, Hq, Hkv, rd, use_norm, lo, hi, bs,
                                                    cap):
